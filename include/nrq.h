@@ -1,0 +1,130 @@
+/*
+ * libnrq — MI355X (gfx950) quantized matrix kernels, C ABI.
+ *
+ * Drop-in for the quantized kernels of the reference's nr-tensor crate
+ * (crates/nr-tensor). Plain pointers and sizes only; every function returns
+ * an int status (NRQ_OK = 0) and never unwinds. On failure nrq_last_error()
+ * returns a message; shape failures carry the text of the reference
+ * assertion they replace, so a binding can re-panic with it.
+ *
+ * Lengths are element counts of the reference's Rust slices: `w_len`,
+ * `x_len` count blocks (BlockQ8_0 = 34 B, BlockQ4K = 144 B, BlockQ6K =
+ * 210 B, BlockQ8K = 292 B), `y_len` and `src_len` count f32 values.
+ *
+ * f32 results are bit-identical to one of the reference's CPU kernels,
+ * selected with nrq_set_order():
+ *   NRQ_ORDER_SCALAR : dot_q8_scalar / dot_q4k_scalar / dot_q6k_scalar
+ *                      (also what the reference's NEON path returns)
+ *   NRQ_ORDER_AVX2   : dot_q8_avx2 / dot_q4k_avx2 / dot_q6k_avx2 (x86 fast path)
+ */
+#ifndef NRQ_H
+#define NRQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define NRQ_OK 0
+#define NRQ_ERR_ARG (-1)         /* null pointer, unknown dtype/order, misaligned device pointer */
+#define NRQ_ERR_SHAPE (-2)       /* a reference assert!/assert_eq! would have panicked */
+#define NRQ_ERR_DEVICE (-3)      /* HIP error, or no gfx950 device */
+#define NRQ_ERR_UNSUPPORTED (-4) /* row wider than the kernels' LDS tile */
+#define NRQ_ERR_NOT_INIT (-5)    /* nrq_init was not called */
+
+/* weight dtypes: TensorDtype ids (crates/nr-model/src/format.rs:97-102) */
+#define NRQ_Q8_0 1
+#define NRQ_Q4_K 2
+#define NRQ_Q6_K 3
+
+/* f32 accumulation order to reproduce */
+#define NRQ_ORDER_SCALAR 0
+#define NRQ_ORDER_AVX2 1
+
+/* ---- lifecycle ------------------------------------------------------------ */
+
+/* Selects HIP device `device`, checks it is gfx950, creates the library's
+ * stream. Replaces the CPU-feature probe cpu::fast_path
+ * (crates/nr-tensor/src/cpu.rs:46-49) and the worker-pool bring-up
+ * POOL.activate (crates/nr-tensor/src/parallel.rs:47-50). Idempotent. */
+int nrq_init(int device);
+/* Frees every device buffer and the stream. */
+int nrq_shutdown(void);
+/* Message of the last failure on this thread ("" if none). */
+const char *nrq_last_error(void);
+/* "gfx950 <name>, <n> CUs, <bytes> HBM" into buf. */
+int nrq_device_info(char *buf, size_t len);
+
+/* Order used by the host-slice entry points below (default NRQ_ORDER_SCALAR).
+ * The reference picks AVX2 vs scalar per call with cpu::fast_path()
+ * (kernels.rs:58, kquant.rs:544); this is that switch. */
+int nrq_set_order(int order);
+int nrq_get_order(void);
+
+/* ---- weight residency ------------------------------------------------------- */
+
+/* Copies `bytes` of quantized weights at `host` into HBM once, in their
+ * original block layout (no dequantized copy). Later calls whose `w` slice
+ * lies inside [host, host+bytes) read the HBM copy. This is the device side
+ * of InferCtx::new taking zero-copy weight views
+ * (crates/nr-model/src/infer.rs:352-419, format.rs:201-214). Host slices that
+ * are not registered are uploaded on every call. */
+int nrq_register_weights(const void *host, size_t bytes);
+int nrq_unregister_weights(const void *host);
+
+/* ---- nr-tensor API over host slices (synchronous) ----------------------------- */
+
+/* kernels::matvec_q8 (crates/nr-tensor/src/kernels.rs:36-47):
+ * y[r] = dot(w[r,:], x); asserts y_len == rows, x_len == cols/32,
+ * w_len >= rows*cols/32. */
+int nrq_matvec_q8(float *y, size_t y_len, const void *w, size_t w_len, const void *x, size_t x_len, size_t rows,
+                  size_t cols);
+/* kernels::matmul_q8 (kernels.rs:91-143): y is [batch][rows], xs is
+ * [batch][cols/32]; bit-identical to matvec_q8 per batch row. */
+int nrq_matmul_q8(float *y, size_t y_len, const void *w, size_t w_len, const void *xs, size_t xs_len, size_t rows,
+                  size_t cols, size_t batch);
+/* kquant::matvec_q4k / matvec_q6k (crates/nr-tensor/src/kquant.rs:536-564) */
+int nrq_matvec_q4k(float *y, size_t y_len, const void *w, size_t w_len, const void *x, size_t x_len, size_t rows,
+                   size_t cols);
+int nrq_matvec_q6k(float *y, size_t y_len, const void *w, size_t w_len, const void *x, size_t x_len, size_t rows,
+                   size_t cols);
+/* kquant::matmul_q4k / matmul_q6k (kquant.rs:566-639) */
+int nrq_matmul_q4k(float *y, size_t y_len, const void *w, size_t w_len, const void *xs, size_t xs_len, size_t rows,
+                   size_t cols, size_t batch);
+int nrq_matmul_q6k(float *y, size_t y_len, const void *w, size_t w_len, const void *xs, size_t xs_len, size_t rows,
+                   size_t cols, size_t batch);
+/* q8::quantize (crates/nr-tensor/src/q8.rs:27-44); asserts src_len == out_len*32 */
+int nrq_quantize(const float *src, size_t src_len, void *out, size_t out_len);
+/* kquant::quantize_q8k (kquant.rs:157-187); asserts src_len == out_len*256 */
+int nrq_quantize_q8k(const float *src, size_t src_len, void *out, size_t out_len);
+
+/* ---- device-resident entry points (asynchronous on `stream`) --------------------
+ * All pointers are device pointers; `stream` is a hipStream_t (NULL = the
+ * library's stream). Weight pointers must be 16-byte aligned (any HIP
+ * allocation is); a weight buffer must stay readable up to the next
+ * 16-byte boundary past its end (true of every HIP allocation). */
+
+/* matvec / matmul with an explicit dtype and order; same contracts as above */
+int nrq_dev_matvec(int dtype, int order, float *y, const void *w, const void *x, size_t rows, size_t cols,
+                   void *stream);
+int nrq_dev_matmul(int dtype, int order, float *y, const void *w, const void *xs, size_t rows, size_t cols,
+                   size_t batch, void *stream);
+/* q8::quantize / kquant::quantize_q8k over n f32 values already in HBM */
+int nrq_dev_quantize_q8_0(const float *src, size_t n, void *out, void *stream);
+int nrq_dev_quantize_q8k(const float *src, size_t n, void *out, void *stream);
+/* Exact per-(row, block) integer sums the scalar kernels form before any f32
+ * step (kernels.rs:75-78, kquant.rs:200-214, kquant.rs:232-242):
+ *   Q8_0: 1 int per block; Q4_K: 8 sub-block sums + sum_m; Q6_K: 16 group sums.
+ * out is [rows][cols/QK][1|9|16] int32. Diagnostic path for parity tests. */
+int nrq_dev_block_sums(int dtype, const void *w, const void *x, int32_t *out, size_t rows, size_t cols,
+                       void *stream);
+/* Waits for all work on `stream` (NULL = library stream). */
+int nrq_sync(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NRQ_H */

@@ -1,0 +1,87 @@
+// Device-side building blocks shared by the gfx950 kernels of libnrq.
+//
+// Block layouts are the reference's GGUF-compatible ones, read in place:
+//   Q8_0 : d:f16@0  qs:i8[32]@2                                   34 B  (q8.rs:9-17)
+//   Q4_K : d:f16@0  dmin:f16@2  scales:u8[12]@4  qs:u8[128]@16     144 B (kquant.rs:26-31)
+//   Q6_K : ql:u8[128]@0  qh:u8[64]@128  scales:i8[16]@192  d:f16@208 210 B (kquant.rs:37-42)
+//   Q8_K : d:f32@0  qs:i8[256]@4  bsums:i16[16]@260               292 B (kquant.rs:48-52)
+//
+// All f32 arithmetic in these kernels is written out operation by operation;
+// the library is compiled with -ffp-contract=off so a*b+c stays two rounded
+// operations wherever the reference has two, and fmaf() is used exactly where
+// the reference's AVX2 kernels use _mm256_fmadd_ps.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nrq {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kQ8_0 = 1;  // TensorDtype ids (crates/nr-model/src/format.rs:97-102)
+constexpr int kQ4K = 2;
+constexpr int kQ6K = 3;
+
+constexpr int kOrderScalar = 0;  // dot_*_scalar (and the NEON kernels, bit for bit)
+constexpr int kOrderAvx2 = 1;    // dot_*_avx2 / dot_*_avx2_x4
+
+constexpr int kQ8_0Bytes = 34;
+constexpr int kQ4KBytes = 144;
+constexpr int kQ6KBytes = 210;
+constexpr int kQ8KBytes = 292;
+
+// IEEE binary16 -> f32. The hardware conversion is exact for every finite
+// and infinite f16 (f16 denormals are enabled in the kernel float mode), so it
+// equals the reference's softfloat f16_to_f32 (f16.rs:3-23) bit for bit on
+// all non-NaN inputs; NaNs stay NaN.
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
+  _Float16 h;
+  uint16_t b = (uint16_t)bits16;
+  __builtin_memcpy(&h, &b, 2);
+  return (float)h;
+}
+
+// Exact 4-way int8 dot product with accumulate (v_dot4_i32_i8).
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Dword starting at an even LDS byte offset `off` (2- or 4-aligned):
+// two aligned reads and a byte funnel shift.
+__device__ __forceinline__ uint32_t lds_u32_even(const uint32_t* lds32, uint32_t off) {
+  uint32_t w = off >> 2;
+  return __builtin_amdgcn_alignbyte(lds32[w + 1], lds32[w], off & 3u);
+}
+
+__device__ __forceinline__ uint32_t lds_u16(const uint8_t* lds, uint32_t off) {
+  return *(const uint16_t*)(lds + off);
+}
+
+// Q4_K 6-bit (scale, min) unpack for all j = 0..7 (kquant.rs:83-92).
+// s0,s1,s2 hold scales[0..4], scales[4..8], scales[8..12] little-endian.
+__device__ __forceinline__ void q4k_unpack_scales(uint32_t s0, uint32_t s1, uint32_t s2, int sc[8], int mn[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    uint32_t a = (s0 >> (8 * j)) & 0xffu;  // scales[j]
+    uint32_t b = (s1 >> (8 * j)) & 0xffu;  // scales[j+4]
+    uint32_t c = (s2 >> (8 * j)) & 0xffu;  // scales[j+8]
+    sc[j] = (int)(a & 63u);
+    mn[j] = (int)(b & 63u);
+    sc[j + 4] = (int)((c & 0x0fu) | ((a >> 6) << 4));
+    mn[j + 4] = (int)((c >> 4) | ((b >> 6) << 4));
+  }
+}
+
+// The four 6-bit planes of a Q6_K half for one l-dword (4 consecutive l),
+// following the scalar unpack of kquant.rs:233-237: plane n holds quants
+// n*32 + l of the half.
+__device__ __forceinline__ void q6k_planes(uint32_t qlA, uint32_t qlB, uint32_t qh, uint32_t q6[4]) {
+  const uint32_t m4 = 0x0f0f0f0fu, m2h = 0x30303030u;
+  q6[0] = (qlA & m4) | ((qh << 4) & m2h);
+  q6[1] = (qlB & m4) | ((qh << 2) & m2h);
+  q6[2] = ((qlA >> 4) & m4) | (qh & m2h);
+  q6[3] = ((qlB >> 4) & m4) | ((qh >> 2) & m2h);
+}
+
+}  // namespace nrq

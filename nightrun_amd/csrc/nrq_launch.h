@@ -1,0 +1,53 @@
+// Internal launch interface between the C ABI (nrq_api.hip) and the kernel
+// files. Not installed; the public interface is include/nrq.h.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace nrq {
+
+enum {
+  NRQ_LAUNCH_OK = 0,
+  NRQ_LAUNCH_BAD_ARG = -1,
+  NRQ_LAUNCH_TOO_WIDE = -2,  // row does not fit the kernel's LDS tile
+  NRQ_LAUNCH_FAILED = -3,
+};
+
+struct MatvecLaunch {
+  const void* w;  // device, 16-byte aligned, rows * bpr blocks
+  const void* x;  // device activation blocks (Q8_0 or Q8_K), bpr blocks
+  float* y;       // device, rows floats
+  int rows;
+  int bpr;
+  int tile_rows;  // 0 = library choice
+  void* stream;   // hipStream_t
+};
+
+struct MatmulLaunch {
+  const void* w;  // device, 16-byte aligned
+  const void* xs; // device, batch * bpr activation blocks
+  float* y;       // device, [batch][rows]
+  int rows;
+  int bpr;
+  int batch;
+  void* stream;
+};
+
+struct QuantLaunch {
+  const float* src;  // device f32[n]
+  void* dst;         // device blocks
+  long long n;       // elements (multiple of the block size)
+  void* stream;
+};
+
+int launch_matvec(int dtype, int order, const MatvecLaunch& L);
+int launch_matmul(int dtype, int order, const MatmulLaunch& L);
+int launch_quantize_q8_0(const QuantLaunch& L);
+// y[0..n) = +0.0 (a kernel, not hipMemsetAsync, so it is safe under graph capture)
+int launch_fill_zero(float* y, long long n, void* stream);
+int launch_quantize_q8k(const QuantLaunch& L);
+// Q4_K/Q6_K/Q8_0 per-(row, block) exact integer sums (test/diagnostic path).
+int launch_block_sums(int dtype, const void* w, const void* x, int32_t* out, int rows, int bpr, void* stream);
+
+}  // namespace nrq

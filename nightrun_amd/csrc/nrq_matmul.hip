@@ -1,0 +1,28 @@
+// Batched matmul (prefill, batch <= 64): y[b][r] = dot(W[r,:], xs[b]).
+// The reference guarantees matmul == per-token matvec bit for bit
+// (kernels.rs:84-90, kquant.rs:566-569). This first version runs the decode
+// kernel once per token, which is bitwise equal by construction.
+#include "nrq_device.h"
+#include "nrq_launch.h"
+
+namespace nrq {
+
+int launch_matmul(int dtype, int order, const MatmulLaunch& L) {
+  if (L.rows <= 0 || L.bpr <= 0 || L.batch <= 0) return 0;
+  const size_t xb = dtype == kQ8_0 ? (size_t)kQ8_0Bytes : (size_t)kQ8KBytes;
+  for (int b = 0; b < L.batch; b++) {
+    MatvecLaunch M;
+    M.w = L.w;
+    M.x = (const uint8_t*)L.xs + (size_t)b * L.bpr * xb;
+    M.y = L.y + (size_t)b * L.rows;
+    M.rows = L.rows;
+    M.bpr = L.bpr;
+    M.tile_rows = 0;
+    M.stream = L.stream;
+    int rc = launch_matvec(dtype, order, M);
+    if (rc) return rc;
+  }
+  return 0;
+}
+
+}  // namespace nrq

@@ -1,0 +1,174 @@
+// Activation quantizers on gfx950, bit-exact restatements of
+//   q8::quantize        (crates/nr-tensor/src/q8.rs:27-44)      f32 -> Q8_0
+//   kquant::quantize_q8k (crates/nr-tensor/src/kquant.rs:157-187) f32 -> Q8_K
+// including the reference's softfloat f32 -> f16 (f16.rs:25-56), whose
+// subnormal rounding is half-up rather than the hardware's nearest-even.
+#include "nrq_device.h"
+#include "nrq_launch.h"
+
+namespace nrq {
+
+// f16.rs:25-56
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float v) {
+  uint32_t bits = __float_as_uint(v);
+  uint32_t sign = (bits >> 31) << 15;
+  int exp = (int)((bits >> 23) & 0xffu);
+  uint32_t frac = bits & 0x7fffffu;
+  if (exp == 0xff) return sign | 0x7c00u | (frac != 0 ? 0x200u : 0u);
+  int e = exp - 127 + 15;
+  if (e >= 0x1f) return sign | 0x7c00u;
+  if (e <= 0) {
+    if (e < -10) return sign;
+    uint32_t f = frac | 0x800000u;
+    uint32_t shift = (uint32_t)(14 - e);
+    uint32_t half = 1u << (shift - 1);
+    return (sign | ((f + half) >> shift)) & 0xffffu;
+  }
+  uint32_t out = sign | ((uint32_t)e << 10) | (frac >> 13);
+  uint32_t round = frac & 0x1fffu;
+  if (round > 0x1000u || (round == 0x1000u && (out & 1u) != 0)) out += 1;
+  return out & 0xffffu;
+}
+
+// Rust `f as i32`: truncate, saturate, NaN -> 0.
+__device__ __forceinline__ int rust_f32_to_i32(float f) {
+  if (f != f) return 0;
+  if (f >= 2147483648.0f) return 2147483647;
+  if (f <= -2147483648.0f) return (-2147483647 - 1);
+  return (int)f;
+}
+
+// One wave per 64 consecutive Q8_0 blocks' worth of work: lane i of a
+// 32-lane half handles element i of its block.
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restrict__ src, uint8_t* __restrict__ dst,
+                                                            long long nblocks) {
+  long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  long long b = gid >> 5;
+  int i = (int)(gid & 31);
+  if (b >= nblocks) return;
+  float v = src[b * 32 + i];
+  // amax over the block; max is order-independent, and fmaxf ignores NaN as
+  // f32::max does.
+  float amax = fabsf(v);
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+  amax = fmaxf(0.0f, amax);
+  uint32_t d_bits = f32_to_f16_bits(amax / 127.0f);
+  float d = f16_bits_to_f32(d_bits);
+  float inv = d > 0.0f ? 1.0f / d : 0.0f;
+  float x = v * inv;
+  float r = x >= 0.0f ? x + 0.5f : x - 0.5f;
+  int q = rust_f32_to_i32(r);
+  q = q < -127 ? -127 : (q > 127 ? 127 : q);
+  uint8_t* blk = dst + b * kQ8_0Bytes;
+  blk[2 + i] = (uint8_t)(int8_t)q;
+  if (i == 0) {
+    blk[0] = (uint8_t)(d_bits & 0xff);
+    blk[1] = (uint8_t)(d_bits >> 8);
+  }
+}
+
+// kquant.rs:145-153
+__device__ __forceinline__ int nearest_int(float v) {
+  return v >= 0.0f ? rust_f32_to_i32(v + 0.5f) : rust_f32_to_i32(v - 0.5f);
+}
+
+// One 256-thread workgroup per Q8_K block.
+__global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ src, uint8_t* __restrict__ dst) {
+  __shared__ float s_abs[4];
+  __shared__ int s_idx[4];
+  __shared__ int s_q[256];
+  const long long b = blockIdx.x;
+  const int i = threadIdx.x;
+  const float v = src[b * 256 + i];
+  // The first index holding the largest |v| (strict `>` scan, NaN never wins).
+  float a = fabsf(v);
+  if (a != a) a = -1.0f;
+  int idx = i;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    float oa = __shfl_xor(a, m);
+    int oi = __shfl_xor(idx, m);
+    if (oa > a || (oa == a && oi < idx)) {
+      a = oa;
+      idx = oi;
+    }
+  }
+  const int wave = i >> 6;
+  if ((i & 63) == 0) {
+    s_abs[wave] = a;
+    s_idx[wave] = idx;
+  }
+  __syncthreads();
+  float ba = s_abs[0];
+  int bi = s_idx[0];
+  for (int w = 1; w < 4; w++) {
+    if (s_abs[w] > ba || (s_abs[w] == ba && s_idx[w] < bi)) {
+      ba = s_abs[w];
+      bi = s_idx[w];
+    }
+  }
+  uint8_t* blk = dst + b * kQ8KBytes;
+  if (!(ba > 0.0f)) {  // amax == 0: all-zero block (kquant.rs:168-172)
+    blk[4 + i] = 0;
+    if (i < 4) blk[i] = 0;
+    if (i < 32) blk[260 + i] = 0;
+    return;
+  }
+  const float max = src[b * 256 + bi];
+  const float iscale = -128.0f / max;
+  int q = nearest_int(iscale * v);
+  q = q > 127 ? 127 : q;
+  const int8_t q8 = (int8_t)q;
+  blk[4 + i] = (uint8_t)q8;
+  s_q[i] = q8;
+  __syncthreads();
+  if (i < 16) {
+    int s = 0;
+    for (int k = 0; k < 16; k++) s += s_q[i * 16 + k];
+    int16_t s16 = (int16_t)s;
+    blk[260 + 2 * i] = (uint8_t)(s16 & 0xff);
+    blk[261 + 2 * i] = (uint8_t)((uint16_t)s16 >> 8);
+  }
+  if (i == 0) {
+    float d = 1.0f / iscale;
+    uint32_t db = __float_as_uint(d);
+    blk[0] = (uint8_t)(db & 0xff);
+    blk[1] = (uint8_t)((db >> 8) & 0xff);
+    blk[2] = (uint8_t)((db >> 16) & 0xff);
+    blk[3] = (uint8_t)(db >> 24);
+  }
+}
+
+__global__ void fill_zero_kernel(float* __restrict__ y, long long n) {
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = 0.0f;
+}
+
+int launch_fill_zero(float* y, long long n, void* stream) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, y, n);
+  return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
+}
+
+int launch_quantize_q8_0(const QuantLaunch& L) {
+  if (L.n <= 0) return 0;
+  if (L.n % 32) return NRQ_LAUNCH_BAD_ARG;
+  long long nb = L.n / 32;
+  long long threads = nb * 32;
+  int grid = (int)((threads + 255) / 256);
+  hipLaunchKernelGGL(quantize_q8_0_kernel, dim3(grid), dim3(256), 0, (hipStream_t)L.stream, L.src, (uint8_t*)L.dst,
+                     nb);
+  return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
+}
+
+int launch_quantize_q8k(const QuantLaunch& L) {
+  if (L.n <= 0) return 0;
+  if (L.n % 256) return NRQ_LAUNCH_BAD_ARG;
+  long long nb = L.n / 256;
+  hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)L.stream, L.src,
+                     (uint8_t*)L.dst);
+  return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
+}
+
+}  // namespace nrq

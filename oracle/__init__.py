@@ -1,0 +1,256 @@
+"""CPU oracle for the quantized matrix path -- TEST INFRASTRUCTURE ONLY.
+
+ctypes view of ``liboracle.so`` (built from ``nrq_oracle.c`` by the Makefile
+beside this file). Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg import this module, and only as the
+checker; the product library (``nightrun_amd``) never imports it.
+
+Each wrapped function restates a function of the reference's Rust crate
+``crates/nr-tensor`` (citations in ``nrq_oracle.h``). Blocks travel as numpy
+``uint8`` arrays of shape ``(nblocks, block_bytes)``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+Q8_0, Q4K, Q6K = 1, 2, 3
+ORDER_SCALAR, ORDER_AVX2 = 0, 1
+QK = {Q8_0: 32, Q4K: 256, Q6K: 256}
+WBYTES = {Q8_0: 34, Q4K: 144, Q6K: 210}
+XBYTES = {Q8_0: 34, Q4K: 292, Q6K: 292}
+Q8K_BYTES = 292
+
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the Makefile beside this file."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-C", HERE, "-B" if force else "all"], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        vp, sz, f32p = C.c_void_p, C.c_size_t, C.POINTER(C.c_float)
+        L.nro_f16_to_f32.argtypes, L.nro_f16_to_f32.restype = [C.c_uint16], C.c_float
+        L.nro_f32_to_f16.argtypes, L.nro_f32_to_f16.restype = [C.c_float], C.c_uint16
+        for name in ("nro_quantize_q8_0", "nro_quantize_q8k"):
+            getattr(L, name).argtypes = [vp, sz, vp]
+        L.nro_dequantize_q8_0.argtypes = [vp, sz, vp]
+        L.nro_q4k_scale_min.argtypes = [vp, C.c_int, C.POINTER(C.c_uint8), C.POINTER(C.c_uint8)]
+        for name in ("nro_dequant_q4k", "nro_dequant_q6k", "nro_quantize_q4k_ref", "nro_quantize_q6k_ref"):
+            getattr(L, name).argtypes = [vp, vp]
+        for q in ("q8", "q4k", "q6k"):
+            for kind in ("scalar", "avx2"):
+                fn = getattr(L, f"nro_dot_{q}_{kind}")
+                fn.argtypes, fn.restype = [vp, vp, sz], C.c_float
+            getattr(L, f"nro_dot_{q}_avx2_x4").argtypes = [vp, C.POINTER(vp), sz, f32p]
+        L.nro_matvec.argtypes = [C.c_int, C.c_int, vp, vp, vp, sz, sz, C.c_int]
+        L.nro_matmul.argtypes = [C.c_int, C.c_int, vp, vp, vp, sz, sz, sz, C.c_int]
+        L.nro_block_sums.argtypes, L.nro_block_sums.restype = [C.c_int, vp, vp, sz, vp], sz
+        L.nro_rng_vec.argtypes = [C.POINTER(C.c_uint64), vp, sz]
+        L.nro_rng_adversarial.argtypes = [C.POINTER(C.c_uint64), vp, sz]
+        L.nro_rng_normal.argtypes = [C.POINTER(C.c_uint64), vp, sz, C.c_float]
+        L.nro_rng_bytes.argtypes = [C.POINTER(C.c_uint64), vp, sz]
+        L.nro_gen_weights.argtypes = [C.c_int, C.c_uint64, vp, sz]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ---- f16.rs -----------------------------------------------------------------
+
+def f16_to_f32(bits: int) -> float:
+    return lib().nro_f16_to_f32(bits)
+
+
+def f32_to_f16(v: float) -> int:
+    return lib().nro_f32_to_f16(v)
+
+
+def f16_to_f32_array(bits: np.ndarray) -> np.ndarray:
+    L = lib()
+    return np.array([L.nro_f16_to_f32(int(b)) for b in bits.ravel()], dtype=np.float32).reshape(bits.shape)
+
+
+# ---- quantizers ---------------------------------------------------------------
+
+def quantize_q8_0(src: np.ndarray) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.float32).ravel()
+    out = np.zeros((src.size // 32, 34), dtype=np.uint8)
+    lib().nro_quantize_q8_0(_p(src), src.size, _p(out))
+    return out
+
+
+def dequantize_q8_0(blocks: np.ndarray) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.zeros(blocks.shape[0] * 32, dtype=np.float32)
+    lib().nro_dequantize_q8_0(_p(blocks), blocks.shape[0], _p(out))
+    return out
+
+
+def quantize_q8k(src: np.ndarray) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.float32).ravel()
+    out = np.zeros((src.size // 256, Q8K_BYTES), dtype=np.uint8)
+    lib().nro_quantize_q8k(_p(src), src.size, _p(out))
+    return out
+
+
+def quantize_act(dtype: int, src: np.ndarray) -> np.ndarray:
+    """The activation format each weight dtype consumes (Q8_0 or Q8_K)."""
+    return quantize_q8_0(src) if dtype == Q8_0 else quantize_q8k(src)
+
+
+def q8k_fields(blocks: np.ndarray):
+    """(d f32[n], qs i8[n,256], bsums i16[n,16]) views of Q8_K blocks."""
+    b = np.ascontiguousarray(blocks, dtype=np.uint8)
+    d = b[:, 0:4].copy().view(np.float32).ravel()
+    qs = b[:, 4:260].view(np.int8)
+    bsums = b[:, 260:292].copy().view(np.int16)
+    return d, qs, bsums
+
+
+def q4k_scale_min(scales12: np.ndarray, j: int):
+    s = np.ascontiguousarray(scales12, dtype=np.uint8)
+    sc, m = C.c_uint8(), C.c_uint8()
+    lib().nro_q4k_scale_min(_p(s), j, C.byref(sc), C.byref(m))
+    return sc.value, m.value
+
+
+def dequant_q4k(block: np.ndarray) -> np.ndarray:
+    block = np.ascontiguousarray(block, dtype=np.uint8)
+    out = np.zeros(256, dtype=np.float32)
+    lib().nro_dequant_q4k(_p(block), _p(out))
+    return out
+
+
+def dequant_q6k(block: np.ndarray) -> np.ndarray:
+    block = np.ascontiguousarray(block, dtype=np.uint8)
+    out = np.zeros(256, dtype=np.float32)
+    lib().nro_dequant_q6k(_p(block), _p(out))
+    return out
+
+
+def quantize_q4k_ref(src: np.ndarray) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.float32).ravel()
+    n = src.size // 256
+    out = np.zeros((n, 144), dtype=np.uint8)
+    for i in range(n):
+        lib().nro_quantize_q4k_ref(_p(src[i * 256:(i + 1) * 256]), _p(out[i]))
+    return out
+
+
+def quantize_q6k_ref(src: np.ndarray) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.float32).ravel()
+    n = src.size // 256
+    out = np.zeros((n, 210), dtype=np.uint8)
+    for i in range(n):
+        lib().nro_quantize_q6k_ref(_p(src[i * 256:(i + 1) * 256]), _p(out[i]))
+    return out
+
+
+def quantize_weights_ref(dtype: int, src: np.ndarray) -> np.ndarray:
+    if dtype == Q8_0:
+        return quantize_q8_0(src)
+    return quantize_q4k_ref(src) if dtype == Q4K else quantize_q6k_ref(src)
+
+
+# ---- dots ---------------------------------------------------------------------
+
+_DOT = {Q8_0: "q8", Q4K: "q4k", Q6K: "q6k"}
+
+
+def dot(dtype: int, order: int, w: np.ndarray, x: np.ndarray) -> float:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.uint8)
+    kind = "avx2" if order == ORDER_AVX2 else "scalar"
+    fn = getattr(lib(), f"nro_dot_{_DOT[dtype]}_{kind}")
+    return fn(_p(w), _p(x), min(w.shape[0], x.shape[0]))
+
+
+def dot_x4(dtype: int, w: np.ndarray, xs) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    xs = [np.ascontiguousarray(x, dtype=np.uint8) for x in xs]
+    arr = (C.c_void_p * 4)(*[x.ctypes.data for x in xs])
+    out = np.zeros(4, dtype=np.float32)
+    getattr(lib(), f"nro_dot_{_DOT[dtype]}_avx2_x4")(_p(w), arr, w.shape[0], out.ctypes.data_as(C.POINTER(C.c_float)))
+    return out
+
+
+def matvec(dtype: int, order: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int, threads: int = 1) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.uint8)
+    y = np.zeros(rows, dtype=np.float32)
+    lib().nro_matvec(dtype, order, _p(y), _p(w), _p(x), rows, cols, threads)
+    return y
+
+
+def matmul(dtype: int, order: int, w: np.ndarray, xs: np.ndarray, rows: int, cols: int, batch: int,
+           threads: int = 1) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    xs = np.ascontiguousarray(xs, dtype=np.uint8)
+    y = np.zeros(batch * rows, dtype=np.float32)
+    lib().nro_matmul(dtype, order, _p(y), _p(w), _p(xs), rows, cols, batch, threads)
+    return y
+
+
+def block_sums(dtype: int, w_row: np.ndarray, x: np.ndarray) -> np.ndarray:
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.uint8)
+    nb = min(w_row.shape[0], x.shape[0])
+    per = {Q8_0: 1, Q4K: 9, Q6K: 16}[dtype]
+    out = np.zeros(nb * per, dtype=np.int32)
+    lib().nro_block_sums(dtype, _p(w_row), _p(x), nb, _p(out))
+    return out
+
+
+# ---- generators ----------------------------------------------------------------
+
+class Rng:
+    """xorshift64 13/7/17 (tests/kernels.rs:9-29, tests/kquant.rs:7-39)."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(seed)
+
+    def vec(self, n: int) -> np.ndarray:
+        out = np.zeros(n, dtype=np.float32)
+        lib().nro_rng_vec(C.byref(self.state), _p(out), n)
+        return out
+
+    def adversarial(self, n: int) -> np.ndarray:
+        out = np.zeros(n, dtype=np.float32)
+        lib().nro_rng_adversarial(C.byref(self.state), _p(out), n)
+        return out
+
+    def normal(self, n: int, sigma: float = 1.0) -> np.ndarray:
+        out = np.zeros(n, dtype=np.float32)
+        lib().nro_rng_normal(C.byref(self.state), _p(out), n, sigma)
+        return out
+
+    def bytes(self, n: int) -> np.ndarray:
+        out = np.zeros(n, dtype=np.uint8)
+        lib().nro_rng_bytes(C.byref(self.state), _p(out), n)
+        return out
+
+
+def gen_weights(dtype: int, seed: int, rows: int, cols: int) -> np.ndarray:
+    nb = rows * (cols // QK[dtype])
+    out = np.zeros((nb, WBYTES[dtype]), dtype=np.uint8)
+    lib().nro_gen_weights(dtype, seed, _p(out), nb)
+    return out

@@ -1,0 +1,354 @@
+"""GPU parity: libnrq's gfx950 kernels against the CPU oracle, bit for bit.
+
+Every comparison here is exact (f32 outputs compared as bit patterns, integer
+sums and quantized blocks byte for byte) in the f32 order under test; the
+reference's own tolerance (1e-5 relative) is never needed because both
+orders are reproduced exactly. Calls go through the C ABI (host-slice mirror
+of nr-tensor, or the device entry points over torch tensors).
+"""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [1, 2, 3]
+NAMES = {1: "q8_0", 2: "q4k", 3: "q6k"}
+ORDERS = [0, 1]
+ONAMES = {0: "scalar", 1: "avx2"}
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def assert_bitwise(got, want, what=""):
+    got, want = bits(got), bits(want)
+    if not np.array_equal(got, want):
+        bad = np.nonzero(got != want)[0]
+        i = bad[0]
+        raise AssertionError(f"{what}: {bad.size} of {got.size} differ; first at {i}: "
+                             f"{got[i:i + 1].view(np.float32)} vs {want[i:i + 1].view(np.float32)}")
+
+
+def dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def gpu_matvec(dtype, order, w, x, rows, cols):
+    import torch
+
+    from nightrun_amd import device
+
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    device.matvec(dtype, order, y, dev(w), dev(x), rows, cols)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def gpu_matmul(dtype, order, w, xs, rows, cols, batch):
+    import torch
+
+    from nightrun_amd import device
+
+    y = torch.empty(rows * batch, dtype=torch.float32, device="cuda")
+    device.matmul(dtype, order, y, dev(w), dev(xs), rows, cols, batch)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def golden():
+    path = os.path.join(os.path.dirname(__file__), "golden", "golden.npz")
+    return dict(np.load(path, allow_pickle=False))
+
+
+# ---- committed fixtures --------------------------------------------------------
+
+
+@pytest.mark.parametrize("order", ORDERS)
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_golden_matvec_host_api(gpu, golden, dtype, order):
+    """nr-tensor mirror (host slices, synchronous) reproduces the fixtures."""
+    from nightrun_amd.nr_tensor import kernels, kquant
+
+    n = NAMES[dtype]
+    w, x = golden[f"{n}_w"], golden[f"{n}_x"]
+    rows, cols = 37, (160 if dtype == 1 else 768)
+    gpu.set_order(order)
+    try:
+        y = np.zeros(rows, dtype=np.float32)
+        fn = {1: kernels.matvec_q8, 2: kquant.matvec_q4k, 3: kquant.matvec_q6k}[dtype]
+        fn(y, w, x, rows, cols)
+        assert_bitwise(y, golden[f"{n}_y_{ONAMES[order]}"], f"{n} {ONAMES[order]}")
+        ym = np.zeros(rows * 5, dtype=np.float32)
+        fm = {1: kernels.matmul_q8, 2: kquant.matmul_q4k, 3: kquant.matmul_q6k}[dtype]
+        fm(ym, w, golden[f"{n}_xs"], rows, cols, 5)
+        assert_bitwise(ym, golden[f"{n}_ym_{ONAMES[order]}"], f"{n} matmul {ONAMES[order]}")
+    finally:
+        gpu.set_order(0)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_golden_block_sums(gpu, golden, dtype):
+    """Per-block integer dot products are bit-exact (kernels.rs:75-78,
+    kquant.rs:200-214, 232-242)."""
+    import torch
+
+    from nightrun_amd import device
+
+    n = NAMES[dtype]
+    rows, cols = 37, (160 if dtype == 1 else 768)
+    want = golden[f"{n}_sums"]
+    out = torch.zeros(want.size, dtype=torch.int32, device="cuda")
+    device.block_sums(dtype, out, dev(golden[f"{n}_w"]), dev(golden[f"{n}_x"]), rows, cols)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_golden_quantize(gpu, golden, dtype):
+    from nightrun_amd.nr_tensor import kquant, q8
+
+    n = NAMES[dtype]
+    for src_key, q_key in ((f"{n}_xf", f"{n}_x"), (f"{n}_xsf", f"{n}_xs")):
+        src, want = golden[src_key], golden[q_key]
+        out = np.zeros_like(want)
+        (q8.quantize if dtype == 1 else kquant.quantize_q8k)(src, out)
+        assert np.array_equal(out, want), src_key
+
+
+# ---- quantizers -------------------------------------------------------------------
+
+
+def quant_inputs(oracle, n):
+    rng = oracle.Rng(77)
+    f = np.finfo(np.float32)
+    cases = [rng.vec(n), rng.adversarial(n), rng.normal(n), np.zeros(n, np.float32), rng.vec(n) * np.float32(1e-30),
+             rng.vec(n) * np.float32(3e38)]
+    ties = ((np.arange(n) % 1023) + 0.5).astype(np.float32) * np.float32(2.0 ** -24) * np.float32(127.0)
+    cases.append(ties)
+    special = rng.normal(n)
+    special[::37] = np.nan
+    special[5::41] = np.inf
+    special[9::43] = -np.inf
+    special[11::47] = f.tiny / 4
+    cases.append(special)
+    return cases
+
+
+def test_quantize_q8_0_bitexact(gpu, oracle):
+    """q8::quantize (q8.rs:27-44) incl. the softfloat f16 scale and Rust's
+    saturating float->int cast, over random, adversarial, zero, tiny, huge,
+    subnormal-tie and NaN/inf inputs."""
+    from nightrun_amd.nr_tensor import q8
+
+    for i, src in enumerate(quant_inputs(oracle, 32 * 96)):
+        out = np.zeros((96, 34), dtype=np.uint8)
+        q8.quantize(src, out)
+        assert np.array_equal(out, oracle.quantize_q8_0(src)), f"case {i}"
+
+
+def test_quantize_q8k_bitexact(gpu, oracle):
+    """kquant::quantize_q8k (kquant.rs:157-187)."""
+    from nightrun_amd.nr_tensor import kquant
+
+    for i, src in enumerate(quant_inputs(oracle, 256 * 12)):
+        out = np.zeros((12, 292), dtype=np.uint8)
+        kquant.quantize_q8k(src, out)
+        assert np.array_equal(out, oracle.quantize_q8k(src)), f"case {i}"
+
+
+def test_quantize_device_entry_points(gpu, oracle):
+    import torch
+
+    from nightrun_amd import device
+
+    src = oracle.Rng(5).normal(256 * 40)
+    o8 = torch.zeros(40 * 8 * 34, dtype=torch.uint8, device="cuda")
+    device.quantize_q8_0(dev(src), o8)
+    ok = torch.zeros(40 * 292, dtype=torch.uint8, device="cuda")
+    device.quantize_q8k(dev(src), ok)
+    torch.cuda.synchronize()
+    assert np.array_equal(o8.cpu().numpy().reshape(-1, 34), oracle.quantize_q8_0(src))
+    assert np.array_equal(ok.cpu().numpy().reshape(-1, 292), oracle.quantize_q8k(src))
+
+
+# ---- f16 scale decode --------------------------------------------------------------
+
+
+@pytest.mark.parametrize("order", ORDERS)
+def test_f16_scale_decode_all_patterns(gpu, oracle, order):
+    """Every f16 weight-scale bit pattern decodes like f16_to_f32 (f16.rs:3-23):
+    row r of a Q8_0 matrix has d = r and one unit quant, against x = e0 with
+    dx = 1, so y[r] = (1 * f16(r)) * 1."""
+    rows = 65536
+    w = np.zeros((rows, 34), dtype=np.uint8)
+    w[:, 0:2] = np.arange(rows, dtype=np.uint32).astype(np.uint16).view(np.uint8).reshape(rows, 2)
+    w[:, 2] = 1
+    x = np.zeros((1, 34), dtype=np.uint8)
+    x[0, 0:2] = np.array([0x3C00], dtype=np.uint16).view(np.uint8)
+    x[0, 2] = 1
+    y = gpu_matvec(1, order, w, x, rows, 32)
+    want = oracle.matvec(1, order, w, x, rows, 32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(y), nan)
+    assert_bitwise(y[~nan], want[~nan], "f16 decode")
+
+
+# ---- shapes ------------------------------------------------------------------------
+
+SHAPES = {
+    1: [(1, 32), (7, 64), (64, 2048), (1000, 256), (513, 8192), (4099, 2048)],
+    2: [(1, 256), (5, 512), (64, 3072), (777, 2560), (300, 4096), (2049, 3072)],
+    3: [(1, 256), (5, 768), (64, 3072), (777, 2560), (301, 9728), (2049, 3072)],
+}
+
+
+@pytest.mark.parametrize("order", ORDERS)
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_matvec_shapes_bitexact(gpu, oracle, dtype, order):
+    """Ragged row counts, 1..256 blocks per row, rows that are not 16-byte
+    multiples (Q6_K 210-byte and Q8_0 34-byte blocks), both orders."""
+    for i, (rows, cols) in enumerate(SHAPES[dtype]):
+        w = oracle.gen_weights(dtype, 1000 + i, rows, cols)
+        x = oracle.quantize_act(dtype, oracle.Rng(2000 + i).normal(cols))
+        want = oracle.matvec(dtype, order, w, x, rows, cols, threads=THREADS)
+        assert_bitwise(gpu_matvec(dtype, order, w, x, rows, cols), want, f"{NAMES[dtype]} {rows}x{cols}")
+
+
+@pytest.mark.parametrize("order", ORDERS)
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_matvec_adversarial_weights(gpu, oracle, dtype, order):
+    """Weights from the reference's test quantizers over adversarial data,
+    and the saturated blocks of tests/kquant.rs:210-245."""
+    qk = oracle.QK[dtype]
+    rows, cols = 40, 4 * qk
+    rng = oracle.Rng(300 + dtype)
+    w = oracle.quantize_weights_ref(dtype, rng.adversarial(rows * cols))
+    x = oracle.quantize_act(dtype, rng.adversarial(cols))
+    assert_bitwise(gpu_matvec(dtype, order, w, x, rows, cols), oracle.matvec(dtype, order, w, x, rows, cols))
+    if dtype != 1:
+        from tests.test_oracle import saturated_blocks
+
+        q4, q6 = saturated_blocks(oracle)
+        blk = q4 if dtype == 2 else q6
+        ws = np.repeat(blk, rows * 4, axis=0)
+        assert_bitwise(gpu_matvec(dtype, order, ws, x, rows, cols), oracle.matvec(dtype, order, ws, x, rows, cols))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_w_longer_than_rows_times_bpr(gpu, oracle, dtype):
+    """`w.len() >= rows * bpr` (kernels.rs:40): trailing blocks are ignored."""
+    from nightrun_amd.nr_tensor import kernels, kquant
+
+    qk = oracle.QK[dtype]
+    rows, cols = 9, 3 * qk
+    w = oracle.gen_weights(dtype, 7, rows + 2, cols)
+    x = oracle.quantize_act(dtype, oracle.Rng(8).normal(cols))
+    y = np.zeros(rows, dtype=np.float32)
+    fn = {1: kernels.matvec_q8, 2: kquant.matvec_q4k, 3: kquant.matvec_q6k}[dtype]
+    fn(y, w, x, rows, cols)
+    assert_bitwise(y, oracle.matvec(dtype, 0, w, x, rows, cols))
+
+
+# ---- matmul == matvec ----------------------------------------------------------------
+
+
+@pytest.mark.parametrize("order", ORDERS)
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_matmul_bit_equals_matvec(gpu, oracle, dtype, order):
+    """Batched output equals per-token matvecs bit for bit (tests/kernels.rs:277-292,
+    tests/kquant.rs:297-329), at batch 1, 4, 5, 17, 63 and 64 (MAX_BATCH,
+    crates/nr-model/src/infer.rs:101)."""
+    qk = oracle.QK[dtype]
+    rows, cols = 96, 8 * qk
+    bpr = cols // qk
+    w = oracle.gen_weights(dtype, 55, rows, cols)
+    for batch in (1, 4, 5, 17, 63, 64):
+        xs = oracle.quantize_act(dtype, oracle.Rng(60 + batch).normal(batch * cols))
+        ym = gpu_matmul(dtype, order, w, xs, rows, cols, batch)
+        assert_bitwise(ym, oracle.matmul(dtype, order, w, xs, rows, cols, batch, threads=THREADS), f"batch {batch}")
+        for b in (0, batch - 1):
+            yv = gpu_matvec(dtype, order, w, xs[b * bpr:(b + 1) * bpr], rows, cols)
+            assert_bitwise(ym[b * rows:(b + 1) * rows], yv, f"batch {batch} row {b}")
+
+
+# ---- boundary behaviour -----------------------------------------------------------------
+
+
+def test_shape_assertions_panic(gpu):
+    """Shape mismatches raise with the reference assertion's text
+    (kernels.rs:38-40, kquant.rs:541-543, q8.rs:28)."""
+    from nightrun_amd import NrPanic
+    from nightrun_amd.nr_tensor import kernels, kquant, q8
+
+    w = np.zeros((8, 34), dtype=np.uint8)
+    x = np.zeros((2, 34), dtype=np.uint8)
+    with pytest.raises(NrPanic, match=r"y.len\(\) == rows"):
+        kernels.matvec_q8(np.zeros(3, np.float32), w, x, 4, 64)
+    with pytest.raises(NrPanic, match=r"x.len\(\) == bpr"):
+        kernels.matvec_q8(np.zeros(4, np.float32), w, x[:1], 4, 64)
+    with pytest.raises(NrPanic, match=r"w.len\(\) >= rows \* bpr"):
+        kernels.matvec_q8(np.zeros(5, np.float32), w, x, 5, 64)
+    with pytest.raises(NrPanic, match=r"xs.len\(\) == batch \* bpr"):
+        kernels.matmul_q8(np.zeros(8, np.float32), w, x, 4, 64, 2)
+    with pytest.raises(NrPanic):
+        kquant.matvec_q4k(np.zeros(2, np.float32), np.zeros((2, 144), np.uint8), np.zeros((2, 292), np.uint8), 2, 256)
+    with pytest.raises(NrPanic):
+        q8.quantize(np.zeros(33, np.float32), np.zeros((1, 34), np.uint8))
+
+
+def test_empty_and_zero_width(gpu):
+    """rows = 0 is a no-op; cols < QK gives empty dots (+0.0)."""
+    from nightrun_amd.nr_tensor import kernels
+
+    kernels.matvec_q8(np.zeros(0, np.float32), np.zeros((0, 34), np.uint8), np.zeros((0, 34), np.uint8), 0, 0)
+    y = np.full(3, 7.0, dtype=np.float32)
+    kernels.matvec_q8(y, np.zeros((0, 34), np.uint8), np.zeros((0, 34), np.uint8), 3, 31)
+    assert_bitwise(y, np.zeros(3, np.float32))
+
+
+def test_registered_weights_match_unregistered(gpu, oracle):
+    from nightrun_amd import nr_tensor
+    from nightrun_amd.nr_tensor import kquant
+
+    rows, cols = 300, 3072
+    w = oracle.gen_weights(3, 99, rows, cols)
+    x = oracle.quantize_q8k(oracle.Rng(3).normal(cols))
+    y0 = np.zeros(rows, np.float32)
+    kquant.matvec_q6k(y0, w, x, rows, cols)
+    nr_tensor.register_weights(w)
+    try:
+        y1 = np.zeros(rows, np.float32)
+        kquant.matvec_q6k(y1, w, x, rows, cols)
+        # a slice of the registered region: rows 10.. (2520-byte rows, 8-byte aligned only)
+        y2 = np.zeros(rows - 16, np.float32)
+        kquant.matvec_q6k(y2, w[16 * 12:], x, rows - 16, cols)
+    finally:
+        nr_tensor.unregister_weights(w)
+    assert_bitwise(y1, y0)
+    assert_bitwise(y2, y0[16:])
+
+
+# ---- full benchmark shapes ------------------------------------------------------------------
+
+CONFIGS = {
+    "cfg1_q8_0_8192x2048": (1, 8192, 2048, 0x5EED0001),
+    "cfg2_q4k_8192x3072": (2, 8192, 3072, 0x5EED0002),
+    "cfg3_q6k_128256x3072": (3, 128256, 3072, 0x5EED0003),
+}
+
+
+@pytest.mark.parametrize("order", ORDERS)
+@pytest.mark.parametrize("cfg", list(CONFIGS))
+def test_benchmark_configs_bitexact(gpu, oracle, cfg, order):
+    dtype, rows, cols, seed = CONFIGS[cfg]
+    w = oracle.gen_weights(dtype, seed, rows, cols)
+    x = oracle.quantize_act(dtype, oracle.Rng(seed ^ 0xABCDEF).normal(cols))
+    want = oracle.matvec(dtype, order, w, x, rows, cols, threads=THREADS)
+    assert_bitwise(gpu_matvec(dtype, order, w, x, rows, cols), want, cfg)
