@@ -344,6 +344,8 @@ int nrq_dev_matvec(int dtype, int order, float* y, const void* w, const void* x,
   if (rows == 0) return NRQ_OK;
   if (!y || (bpr && (!w || !x))) return fail(NRQ_ERR_ARG, "nrq_dev_matvec: null pointer");
   if (((uintptr_t)w & 15) != 0) return fail(NRQ_ERR_ARG, "nrq_dev_matvec: weights not 16-byte aligned");
+  if (((uintptr_t)x & (dtype == NRQ_Q8_0 ? 1 : 3)) != 0)
+    return fail(NRQ_ERR_ARG, "nrq_dev_matvec: activation blocks not aligned like their Rust type");
   if (rows > 0x7fffffff || bpr > 0x7fffffff) return fail(NRQ_ERR_UNSUPPORTED, "nrq_dev_matvec: dimension exceeds 2^31");
   hipStream_t st = stream_or_default(stream);
   if (bpr == 0) {
@@ -361,6 +363,8 @@ int nrq_dev_matmul(int dtype, int order, float* y, const void* w, const void* xs
   if (rows == 0 || batch == 0) return NRQ_OK;
   if (!y || (bpr && (!w || !xs))) return fail(NRQ_ERR_ARG, "nrq_dev_matmul: null pointer");
   if (((uintptr_t)w & 15) != 0) return fail(NRQ_ERR_ARG, "nrq_dev_matmul: weights not 16-byte aligned");
+  if (((uintptr_t)xs & (dtype == NRQ_Q8_0 ? 1 : 3)) != 0)
+    return fail(NRQ_ERR_ARG, "nrq_dev_matmul: activation blocks not aligned like their Rust type");
   if (rows > 0x7fffffff || bpr > 0x7fffffff || batch > 0x7fffffff)
     return fail(NRQ_ERR_UNSUPPORTED, "nrq_dev_matmul: dimension exceeds 2^31");
   hipStream_t st = stream_or_default(stream);
@@ -398,6 +402,8 @@ int nrq_dev_block_sums(int dtype, const void* w, const void* x, int32_t* out, si
   if (rows == 0 || bpr == 0) return NRQ_OK;
   if (!w || !x || !out) return fail(NRQ_ERR_ARG, "nrq_dev_block_sums: null pointer");
   if (((uintptr_t)w & 15) != 0) return fail(NRQ_ERR_ARG, "nrq_dev_block_sums: weights not 16-byte aligned");
+  if (((uintptr_t)x & (dtype == NRQ_Q8_0 ? 1 : 3)) != 0)
+    return fail(NRQ_ERR_ARG, "nrq_dev_block_sums: activation blocks not aligned like their Rust type");
   return launch_rc(nrq::launch_block_sums(dtype, w, x, out, (int)rows, (int)bpr, stream_or_default(stream)),
                    "nrq_dev_block_sums");
 }

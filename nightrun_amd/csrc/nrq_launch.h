@@ -20,8 +20,9 @@ struct MatvecLaunch {
   float* y;       // device, rows floats
   int rows;
   int bpr;
-  int tile_rows;  // 0 = library choice
+  int tile_rows;  // 0 = library choice, else rows per tile
   void* stream;   // hipStream_t
+  int variant = 0;  // scalar order: 0 streaming (default), 1 one-shot LDS tiles, 2 direct-to-register
 };
 
 struct MatmulLaunch {
@@ -42,6 +43,10 @@ struct QuantLaunch {
 };
 
 int launch_matvec(int dtype, int order, const MatvecLaunch& L);
+// Scalar-order decode kernels: weights HBM -> registers (nrq_decode.hip) and
+// persistent double-buffered LDS streaming (nrq_stream.hip).
+int launch_decode_scalar(int dtype, const MatvecLaunch& L);
+int launch_stream_scalar(int dtype, const MatvecLaunch& L);
 int launch_matmul(int dtype, int order, const MatmulLaunch& L);
 int launch_quantize_q8_0(const QuantLaunch& L);
 // y[0..n) = +0.0 (a kernel, not hipMemsetAsync, so it is safe under graph capture)
