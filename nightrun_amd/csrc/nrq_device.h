@@ -18,6 +18,7 @@
 namespace nrq {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kQ8_0 = 1;  // TensorDtype ids (crates/nr-model/src/format.rs:97-102)
 constexpr int kQ4K = 2;
@@ -45,6 +46,16 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
 // Exact 4-way int8 dot product with accumulate (v_dot4_i32_i8).
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Exact dot of two i16 pairs packed in dwords, with accumulate (v_dot2_i32_i16).
+// The operands are taken by value as plain dwords: a bit cast applied
+// directly to an ext-vector element can read the wrong element.
+__device__ __forceinline__ int sdot2(uint32_t a, uint32_t b, int c) {
+  short2_t sa, sb;
+  __builtin_memcpy(&sa, &a, 4);
+  __builtin_memcpy(&sb, &b, 4);
+  return __builtin_amdgcn_sdot2(sa, sb, c, false);
 }
 
 // Dword starting at an even LDS byte offset `off` (2- or 4-aligned):

@@ -22,7 +22,8 @@ struct MatvecLaunch {
   int bpr;
   int tile_rows;  // 0 = library choice, else rows per tile
   void* stream;   // hipStream_t
-  int variant = 0;  // scalar order: 0 streaming (default), 1 one-shot LDS tiles, 2 direct-to-register
+  int variant = 0;  // scalar order: 0 default, 1 one-shot LDS tiles, 2 direct-to-register,
+                    // 3 workgroup-pipelined LDS streaming, 4 per-wave LDS streaming
 };
 
 struct MatmulLaunch {
@@ -47,6 +48,8 @@ int launch_matvec(int dtype, int order, const MatvecLaunch& L);
 // persistent double-buffered LDS streaming (nrq_stream.hip).
 int launch_decode_scalar(int dtype, const MatvecLaunch& L);
 int launch_stream_scalar(int dtype, const MatvecLaunch& L);
+// Scalar-order decode, one lane per block, per-wave LDS streaming (nrq_wstream.hip).
+int launch_wstream_scalar(int dtype, const MatvecLaunch& L);
 int launch_matmul(int dtype, int order, const MatmulLaunch& L);
 int launch_quantize_q8_0(const QuantLaunch& L);
 // y[0..n) = +0.0 (a kernel, not hipMemsetAsync, so it is safe under graph capture)

@@ -546,7 +546,8 @@ int launch_block_sums(int dtype, const void* w, const void* x, int32_t* out, int
 
 int launch_matvec(int dtype, int order, const MatvecLaunch& L) {
   if (L.rows <= 0 || L.bpr <= 0) return 0;
-  if (order == kOrderScalar && L.variant == 0) return launch_stream_scalar(dtype, L);
+  if (order == kOrderScalar && (L.variant == 0 || L.variant == 4)) return launch_wstream_scalar(dtype, L);
+  if (order == kOrderScalar && L.variant == 3) return launch_stream_scalar(dtype, L);
   if (order == kOrderScalar && L.variant == 2) return launch_decode_scalar(dtype, L);
   if (order == kOrderScalar) {
     if (dtype == kQ8_0) return launch_matvec_t<kQ8_0, kOrderScalar>(L);

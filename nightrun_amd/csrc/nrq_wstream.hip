@@ -1,0 +1,449 @@
+// Decode matvec, scalar f32 order, one lane per block, per-wave streaming.
+// Bit-identical to the reference's scalar kernels
+//   dot_q8_scalar  (crates/nr-tensor/src/kernels.rs:72-82)
+//   dot_q4k_scalar (crates/nr-tensor/src/kquant.rs:192-218)
+//   dot_q6k_scalar (crates/nr-tensor/src/kquant.rs:220-250)
+// inside the row loops of matvec_q8 (kernels.rs:36-70) and kquant_matvec!
+// (kquant.rs:536-564).
+//
+// Work split. Each wave owns `rpw` consecutive rows. Their blocks are one
+// contiguous byte range of W, cut into tiles of 64 lanes x BPL blocks. A tile
+// moves HBM -> LDS with global_load_lds_dwordx4 (1 KiB per wave instruction)
+// into one of NS per-wave stages, so up to NS tiles are in flight. A wave
+// waits only on its own loads (s_waitcnt vmcnt); after the activation is
+// staged, waves never wait for each other.
+//
+// Compute. Lane l of a tile forms the contribution of block l (+64k) exactly
+// as the scalar kernel does: exact integer sub-dots with v_dot4_i32_i8 (and
+// v_dot2_i32_i16 for the Q4_K min term), then the reference's f32 steps in
+// its order. Contributions go to the wave's LDS slot u[b * rpw + r]; after
+// the last tile, lane r adds row r's contributions in block order, the
+// reference's `sumf +=` chain.
+#include "nrq_device.h"
+#include "nrq_launch.h"
+
+namespace nrq {
+
+namespace {
+
+__device__ __forceinline__ void ws_dma16(const void* g, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(g) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void ws_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ void ws_wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0x7f | (0 << 8) | (3 << 14)); }
+
+// Workgroup barrier over LDS only; global loads in flight keep running.
+__device__ __forceinline__ void ws_lds_barrier() {
+  asm volatile("" ::: "memory");
+  ws_wait_lgkm0();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t ws_lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+
+// Per-format constants.
+//   BS   weight block bytes       XB  activation block bytes
+//   BPL  blocks per lane per tile NI  1 KiB DMA instructions per tile
+//   XS   activation dwords per block in LDS
+// Activation LDS layouts (dwords):
+//   Q8_0 : [qs 8][d][pad 3]                                    stride 12
+//   Q4_K : [qs 64][bsum pair sums as i16x2: 4][d][pad 15]      stride 84
+//   Q6_K : [qs 64][-32 * group sums: 16][d][pad 3]             stride 84
+// Strides 12 and 84 put the blocks read by one instruction on distinct
+// 4-bank groups (84 = 20 mod 64).
+template <int FMT>
+struct WS;
+template <>
+struct WS<kQ8_0> {
+  static constexpr int BS = kQ8_0Bytes, XB = kQ8_0Bytes, BPL = 4, NI = 9, XS = 12;
+};
+template <>
+struct WS<kQ4K> {
+  static constexpr int BS = kQ4KBytes, XB = kQ8KBytes, BPL = 1, NI = 9, XS = 84;
+};
+template <>
+struct WS<kQ6K> {
+  static constexpr int BS = kQ6KBytes, XB = kQ8KBytes, BPL = 1, NI = 14, XS = 84;
+};
+
+// Raw activation (already in LDS, `xskew` bytes into `raw`) -> padded layout.
+template <int FMT>
+__device__ void ws_repack(const uint32_t* raw, uint32_t xskew, int bpr, uint32_t* xl, int tid, int nt) {
+  constexpr int XS = WS<FMT>::XS;
+  if constexpr (FMT == kQ8_0) {
+    for (int i = tid; i < bpr * 9; i += nt) {
+      const int b = i / 9, t = i - b * 9;
+      const uint32_t o = xskew + (uint32_t)b * kQ8_0Bytes;
+      if (t < 8) xl[b * XS + t] = lds_u32_even(raw, o + 2 + 4 * t);
+      else xl[b * XS + 8] = __float_as_uint(f16_bits_to_f32(lds_u16((const uint8_t*)raw, o)));
+    }
+  } else {
+    // Q8_K block = 73 dwords: d @0, qs @1..64, bsums @65..72 (xskew is 4-aligned).
+    const uint32_t* rw = raw + (xskew >> 2);
+    for (int i = tid; i < bpr * 64; i += nt) {
+      const int b = i >> 6, t = i & 63;
+      xl[b * XS + t] = rw[b * 73 + 1 + t];
+    }
+    for (int i = tid; i < bpr * 16; i += nt) {
+      const int b = i >> 4, g = i & 15;
+      if constexpr (FMT == kQ4K) {
+        if (g < 4) {
+          // sub-blocks 2g, 2g+1: bsums[4g] + bsums[4g+1] | (bsums[4g+2] + bsums[4g+3]) << 16.
+          // Each pair sum is a sum of 32 int8 values, so it fits an i16.
+          const uint32_t v0 = rw[b * 73 + 65 + 2 * g], v1 = rw[b * 73 + 66 + 2 * g];
+          const int s0 = (int)(int16_t)(v0 & 0xffffu) + (int)(int16_t)(v0 >> 16);
+          const int s1 = (int)(int16_t)(v1 & 0xffffu) + (int)(int16_t)(v1 >> 16);
+          xl[b * XS + 64 + g] = ((uint32_t)s0 & 0xffffu) | ((uint32_t)s1 << 16);
+        } else if (g == 4) {
+          xl[b * XS + 68] = rw[b * 73];
+        }
+      } else {
+        int s = 0;  // -32 * (sum of the group's 16 quants): the (q - 32) term of the scalar dot
+#pragma unroll
+        for (int k = 0; k < 4; k++) s = sdot4(rw[b * 73 + 1 + 4 * g + k], 0xe0e0e0e0u, s);
+        xl[b * XS + 64 + g] = (uint32_t)s;
+        if (g == 0) xl[b * XS + 80] = rw[b * 73];
+      }
+    }
+  }
+}
+
+// ---- per-block contributions (one lane, LDS in) --------------------------------------
+
+// Q8_0 at even LDS byte offset o: (f32(acc) * dw) * dx (kernels.rs:75-79).
+__device__ __forceinline__ float ws_q80(const uint32_t* w32, uint32_t o, const uint32_t* xb) {
+  const uint32_t q0 = o + 2, base = q0 >> 2, sh = q0 & 3u;
+  uint32_t D[9];
+#pragma unroll
+  for (int t = 0; t < 9; t++) D[t] = w32[base + t];
+  const u32x4 xa = *(const u32x4*)xb, xc = *(const u32x4*)(xb + 4);
+  const uint32_t X[8] = {xa.x, xa.y, xa.z, xa.w, xc.x, xc.y, xc.z, xc.w};
+  int acc = 0;
+#pragma unroll
+  for (int t = 0; t < 8; t++) acc = sdot4(__builtin_amdgcn_alignbyte(D[t + 1], D[t], sh), X[t], acc);
+  const uint32_t dbits = (o & 2) ? (w32[o >> 2] >> 16) : (w32[o >> 2] & 0xffffu);
+  const float t1 = (float)acc * f16_bits_to_f32(dbits);
+  return t1 * __uint_as_float(xb[8]);
+}
+
+// Q4_K at 16-byte-aligned LDS byte offset o (kquant.rs:195-215):
+//   sub_j = sum of 32 q4*q8 (i32); sum_q += f32(sc_j) * f32(sub_j) in j order;
+//   sum_m = sum_j m_j * (bsums[2j] + bsums[2j+1]);
+//   contribution = d_all * sum_q - dmin_all * f32(sum_m).
+// f32(sc) * f32(sub) == f32(sc * sub): |sc * sub| <= 63 * 61440 < 2^24, and the
+// chain starts from +0.0, so a -0.0 product cannot change the sum.
+__device__ __forceinline__ float ws_q4k(const uint8_t* lds_w, uint32_t o, const uint32_t* xb) {
+  const u32x4 h = *(const u32x4*)(lds_w + o);
+  // 6-bit scales and mins (kquant.rs:83-92), four per word:
+  //   sc[0..4) = s[0..4] & 63             m[0..4) = s[4..8] & 63
+  //   sc[4..8) = (s[8..12] & 15) | (s[0..4] >> 6) << 4
+  //   m[4..8)  = (s[8..12] >> 4) | (s[4..8] >> 6) << 4
+  const uint32_t s0 = h.y, s1 = h.z, s2 = h.w;
+  const uint32_t scA = s0 & 0x3f3f3f3fu;
+  const uint32_t mnA = s1 & 0x3f3f3f3fu;
+  const uint32_t scB = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+  const uint32_t mnB = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+  int sub[8];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const u32x4 qa = *(const u32x4*)(lds_w + o + 16 + 32 * c);
+    const u32x4 qb = *(const u32x4*)(lds_w + o + 32 + 32 * c);
+    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    const u32x4 x0 = *(const u32x4*)(xb + 16 * c), x1 = *(const u32x4*)(xb + 16 * c + 4);
+    const u32x4 x2 = *(const u32x4*)(xb + 16 * c + 8), x3 = *(const u32x4*)(xb + 16 * c + 12);
+    const uint32_t xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    const uint32_t xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+    int lo = 0, hi = 0;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      lo = sdot4(q[t] & 0x0f0f0f0fu, xl[t], lo);
+      hi = sdot4((q[t] >> 4) & 0x0f0f0f0fu, xh[t], hi);
+    }
+    sub[2 * c] = lo;
+    sub[2 * c + 1] = hi;
+  }
+  float sum_q = (float)((int)(scA & 0xffu) * sub[0]);
+  sum_q = sum_q + (float)((int)((scA >> 8) & 0xffu) * sub[1]);
+  sum_q = sum_q + (float)((int)((scA >> 16) & 0xffu) * sub[2]);
+  sum_q = sum_q + (float)((int)(scA >> 24) * sub[3]);
+  sum_q = sum_q + (float)((int)(scB & 0xffu) * sub[4]);
+  sum_q = sum_q + (float)((int)((scB >> 8) & 0xffu) * sub[5]);
+  sum_q = sum_q + (float)((int)((scB >> 16) & 0xffu) * sub[6]);
+  sum_q = sum_q + (float)((int)(scB >> 24) * sub[7]);
+  // sum_m: m_j zero-extended into i16 pairs, dotted with the i16 pair sums.
+  const u32x4 bs = *(const u32x4*)(xb + 64);
+  int sum_m = sdot2(__builtin_amdgcn_perm(0u, mnA, 0x0c010c00u), bs.x, 0);
+  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnA, 0x0c030c02u), bs.y, sum_m);
+  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnB, 0x0c010c00u), bs.z, sum_m);
+  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnB, 0x0c030c02u), bs.w, sum_m);
+  const float xd = __uint_as_float(xb[68]);
+  const float d_all = f16_bits_to_f32(h.x & 0xffffu) * xd;
+  const float dmin_all = f16_bits_to_f32(h.x >> 16) * xd;
+  const float a = d_all * sum_q;
+  const float m = dmin_all * (float)sum_m;
+  return a - m;
+}
+
+// Q6_K at even LDS byte offset o (kquant.rs:223-247): per half, the four
+// planes of quants (q - 32), 16 group sums of (q - 32) * q8 (i32), then
+// sum += f32(sc[g]) * f32(gs[g]) in g order and d_all * sum.
+// f32(sc) * f32(gs) == f32(sc * gs): |sc * gs| <= 128 * 65536 < 2^24.
+__device__ __forceinline__ float ws_q6k(const uint32_t* w32, uint32_t o, const uint32_t* xb) {
+  const uint32_t sh = o & 3u, base = o >> 2;
+  int gs[16];
+  {
+    const u32x4 c0 = *(const u32x4*)(xb + 64), c1 = *(const u32x4*)(xb + 68);
+    const u32x4 c2 = *(const u32x4*)(xb + 72), c3 = *(const u32x4*)(xb + 76);
+    const uint32_t C[16] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w,
+                            c2.x, c2.y, c2.z, c2.w, c3.x, c3.y, c3.z, c3.w};
+#pragma unroll
+    for (int g = 0; g < 16; g++) gs[g] = (int)C[g];
+  }
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++) {
+    uint32_t L[17], H[9];
+#pragma unroll
+    for (int t = 0; t < 17; t++) L[t] = w32[base + 16 * hh + t];       // ql[64hh ..]
+#pragma unroll
+    for (int t = 0; t < 9; t++) H[t] = w32[base + 32 + 8 * hh + t];    // qh[32hh ..]
+    uint32_t X[32];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const u32x4 v = *(const u32x4*)(xb + 32 * hh + 4 * k);
+      X[4 * k] = v.x;
+      X[4 * k + 1] = v.y;
+      X[4 * k + 2] = v.z;
+      X[4 * k + 3] = v.w;
+    }
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const uint32_t qlA = __builtin_amdgcn_alignbyte(L[t + 1], L[t], sh);
+      const uint32_t qlB = __builtin_amdgcn_alignbyte(L[t + 9], L[t + 8], sh);
+      const uint32_t qh = __builtin_amdgcn_alignbyte(H[t + 1], H[t], sh);
+      uint32_t q6[4];
+      q6k_planes(qlA, qlB, qh, q6);
+#pragma unroll
+      for (int n = 0; n < 4; n++) {
+        const int g = 8 * hh + 2 * n + (t >> 2);
+        gs[g] = sdot4(q6[n], X[8 * n + t], gs[g]);
+      }
+    }
+  }
+  const uint32_t S0 = __builtin_amdgcn_alignbyte(w32[base + 49], w32[base + 48], sh);  // scales[0..4)
+  const uint32_t S1 = __builtin_amdgcn_alignbyte(w32[base + 50], w32[base + 49], sh);
+  const uint32_t S2 = __builtin_amdgcn_alignbyte(w32[base + 51], w32[base + 50], sh);
+  const uint32_t S3 = __builtin_amdgcn_alignbyte(w32[base + 52], w32[base + 51], sh);
+  const uint32_t S[4] = {S0, S1, S2, S3};
+  float sum = 0.0f;
+#pragma unroll
+  for (int g = 0; g < 16; g++) {
+    const int s = (int)(int8_t)((S[g >> 2] >> (8 * (g & 3))) & 0xffu);
+    sum = sum + (float)(s * gs[g]);
+  }
+  const uint32_t dw = w32[(o + 208) >> 2];
+  const uint32_t dbits = ((o + 208) & 2) ? (dw >> 16) : (dw & 0xffffu);
+  const float d_all = f16_bits_to_f32(dbits) * __uint_as_float(xb[80]);
+  return d_all * sum;
+}
+
+}  // namespace
+
+// LDS layout of one workgroup:
+//   [activation, padded: bpr*XS dwords][raw activation window][per wave: NS stages | u]
+template <int FMT>
+struct WSGeom {
+  size_t xl, xraw, stage, u, per_wave, total;
+  __host__ __device__ WSGeom(int bpr, int rpw, int ns, int nw) {
+    xl = ((size_t)bpr * WS<FMT>::XS * 4 + 15) & ~(size_t)15;
+    // the DMA writes whole KiB per wave instruction
+    xraw = ((size_t)bpr * WS<FMT>::XB + 15 + 15 + 1023) & ~(size_t)1023;
+    stage = (size_t)WS<FMT>::NI * 1024;
+    u = ((size_t)rpw * bpr * 4 + 15) & ~(size_t)15;
+    per_wave = (size_t)ns * stage + u;
+    total = xl + xraw + (size_t)nw * per_wave;
+  }
+};
+
+template <int FMT, int NW, int NS>
+__global__ __launch_bounds__(64 * NW) void wstream_matvec(const uint8_t* __restrict__ W, const uint8_t* __restrict__ X,
+                                                          float* __restrict__ Y, int rows, int bpr, int rpw,
+                                                          int nstages) {
+  using F = WS<FMT>;
+  constexpr int NI = F::NI, BS = F::BS, TBK = 64 * F::BPL, STAGE = NI * 1024;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const WSGeom<FMT> G(bpr, rpw, nstages, NW);
+  uint32_t* xl = (uint32_t*)smem;
+  uint8_t* xraw = smem + G.xl;
+  uint8_t* stages = xraw + G.xraw + (size_t)wave * G.per_wave;
+  float* u = (float*)(stages + (size_t)nstages * STAGE);
+  const uint32_t stage0 = ws_lds_addr(stages);
+
+  const int row0 = (blockIdx.x * NW + wave) * rpw;
+  const int nr = max(0, min(rpw, rows - row0));
+  const int nb = nr * bpr;
+  const size_t fbeg = (size_t)max(row0, 0) * bpr;  // first flat block of this wave
+  const int ntiles = (nb + TBK - 1) / TBK;
+
+  // Tile t: flat blocks [fbeg + t*TBK, ...) -> 16-byte window [a0, a0 + 16*n16), stage t % nstages.
+  auto issue = [&](int t) {
+    const size_t fb0 = fbeg + (size_t)t * TBK;
+    const size_t fb1 = fbeg + (size_t)min(nb, (t + 1) * TBK);
+    const size_t a0 = (fb0 * BS) & ~(size_t)15;
+    const int n16 = (int)(((((fb1 * BS) + 15) & ~(size_t)15) - a0) >> 4);
+    const uint32_t sbase = stage0 + (uint32_t)((t % nstages) * STAGE);
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+      const int ci = min(k * 64 + lane, n16 - 1);  // past the window: reload its last chunk
+      ws_dma16(W + a0 + 16 * (size_t)ci, sbase + (uint32_t)k * 1024u);
+    }
+  };
+
+  // Activation window first, so an in-order vmcnt wait below covers it.
+  {
+    const uintptr_t xa = (uintptr_t)X;
+    const uintptr_t xa0 = xa & ~(uintptr_t)15;
+    const int n16x = (int)(((((xa + (size_t)bpr * F::XB) + 15) & ~(uintptr_t)15) - xa0) >> 4);
+    const uint32_t rbase = ws_lds_addr(xraw);
+    for (int grp = wave; grp * 64 < n16x; grp += NW) {
+      const int ci = min(grp * 64 + lane, n16x - 1);
+      ws_dma16((const uint8_t*)xa0 + 16 * (size_t)ci, rbase + (uint32_t)grp * 1024u);
+    }
+  }
+  const int pro = min(nstages, ntiles);
+  for (int t = 0; t < pro; t++) issue(t);
+  // the activation landed once at most `pro` tiles' loads are outstanding
+  switch (pro) {
+    case 0: ws_wait_vm<0>(); break;
+    case 1: ws_wait_vm<NI>(); break;
+    case 2: ws_wait_vm<2 * NI>(); break;
+    default: ws_wait_vm<3 * NI>(); break;
+  }
+  ws_lds_barrier();
+  ws_repack<FMT>((const uint32_t*)xraw, (uint32_t)((uintptr_t)X & 15), bpr, xl, tid, 64 * NW);
+  ws_lds_barrier();
+
+  // Lane l's k-th block of tile t is flat block fbeg + t*TBK + l + 64k; track its (row, block).
+  int rr[F::BPL], bb[F::BPL];
+#pragma unroll
+  for (int k = 0; k < F::BPL; k++) {
+    const int f = lane + 64 * k;
+    rr[k] = f / bpr;
+    bb[k] = f - rr[k] * bpr;
+  }
+  const int step_r = TBK / bpr, step_b = TBK - step_r * bpr;
+
+  for (int t = 0; t < ntiles; t++) {
+    const int after = min(nstages - 1, ntiles - 1 - t);  // tiles issued after t
+    if (after >= 2) ws_wait_vm<2 * NI>();
+    else if (after == 1) ws_wait_vm<NI>();
+    else ws_wait_vm<0>();
+    asm volatile("" ::: "memory");
+    const uint8_t* cur = stages + (t % nstages) * STAGE;
+    const int tb0 = t * TBK;
+    const uint32_t skew = (uint32_t)(((fbeg + tb0) * BS) & 15);
+#pragma unroll
+    for (int k = 0; k < F::BPL; k++) {
+      const int i = lane + 64 * k;
+      if (tb0 + i < nb) {
+        const uint32_t o = skew + (uint32_t)i * BS;
+        const uint32_t* xb = xl + bb[k] * F::XS;
+        float c;
+        if constexpr (FMT == kQ8_0) c = ws_q80((const uint32_t*)cur, o, xb);
+        else if constexpr (FMT == kQ4K) c = ws_q4k(cur, o, xb);
+        else c = ws_q6k((const uint32_t*)cur, o, xb);
+        u[bb[k] * rpw + rr[k]] = c;
+      }
+      rr[k] += step_r;
+      bb[k] += step_b;
+      if (bb[k] >= bpr) {
+        bb[k] -= bpr;
+        rr[k] += 1;
+      }
+    }
+    if (t + nstages < ntiles) {
+      ws_wait_lgkm0();  // this stage's reads are done before the DMA refills it
+      asm volatile("" ::: "memory");
+      issue(t + nstages);
+    }
+  }
+  ws_wait_lgkm0();
+  asm volatile("" ::: "memory");
+  // the reference's `sumf += contribution` chain, block order
+  if (lane < nr) {
+    float s = 0.0f;
+    for (int b = 0; b < bpr; b++) s = s + u[b * rpw + lane];
+    Y[row0 + lane] = s;
+  }
+}
+
+// ---- launch ----------------------------------------------------------------------------------
+
+template <int FMT, int NW, int NS>
+static int launch_ws_t(const MatvecLaunch& L, int rpw) {
+  constexpr int TBK = 64 * WS<FMT>::BPL;
+  const int bpr = L.bpr;
+  const long waves = (L.rows + rpw - 1) / rpw;
+  const long tiles_per_wave = ((long)rpw * bpr + TBK - 1) / TBK;
+  const int nstages = (int)(tiles_per_wave < NS ? tiles_per_wave : NS);
+  const WSGeom<FMT> G(bpr, rpw, nstages, NW);
+  if (G.total > 160 * 1024) return NRQ_LAUNCH_TOO_WIDE;
+  const int grid = (int)((waves + NW - 1) / NW);
+  hipLaunchKernelGGL((wstream_matvec<FMT, NW, NS>), dim3(grid), dim3(64 * NW), G.total, (hipStream_t)L.stream,
+                     (const uint8_t*)L.w, (const uint8_t*)L.x, L.y, L.rows, bpr, rpw, nstages);
+  return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
+}
+
+// Rows per wave: the smallest count whose blocks fill at least 85% of the
+// lanes of the wave's tiles (a partly empty tile costs as much as a full one).
+// Small counts also give the most waves, which short matrices need to cover
+// every CU.
+template <int FMT>
+static int ws_rows_per_wave(int bpr, int cap) {
+  constexpr int TBK = 64 * WS<FMT>::BPL;
+  if (cap > 0) return cap < 64 ? cap : 64;
+  int best = 1;
+  double best_util = 0.0;
+  for (int r = 1; r <= 64; r++) {
+    const long blocks = (long)r * bpr;
+    const long slots = (blocks + TBK - 1) / TBK * TBK;
+    const double util = (double)blocks / (double)slots;
+    if (util >= 0.85) return r;
+    if (util > best_util) {
+      best_util = util;
+      best = r;
+    }
+  }
+  return best;
+}
+
+template <int FMT>
+static int launch_ws(const MatvecLaunch& L) {
+  const int rpw = ws_rows_per_wave<FMT>(L.bpr, L.tile_rows);
+  // NW = 4 waves share one activation copy; NS = 2 (double buffering) keeps a
+  // tile in flight per wave while the other is computed, within the LDS of a CU.
+  int rc = launch_ws_t<FMT, 4, 2>(L, rpw);
+  if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2>(L, rpw);
+  if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2>(L, 1);
+  return rc;
+}
+
+int launch_wstream_scalar(int dtype, const MatvecLaunch& L) {
+  if (L.rows <= 0 || L.bpr <= 0) return 0;
+  if (dtype == kQ8_0) return launch_ws<kQ8_0>(L);
+  if (dtype == kQ4K) return launch_ws<kQ4K>(L);
+  if (dtype == kQ6K) return launch_ws<kQ6K>(L);
+  return NRQ_LAUNCH_BAD_ARG;
+}
+
+}  // namespace nrq
