@@ -34,6 +34,7 @@ struct MatmulLaunch {
   int bpr;
   int batch;
   void* stream;
+  int variant = 0;  // scalar order: 0 int8-MFMA tile kernel, 1 one decode launch per token
 };
 
 struct QuantLaunch {
@@ -51,6 +52,8 @@ int launch_stream_scalar(int dtype, const MatvecLaunch& L);
 // Scalar-order decode, one lane per block, per-wave LDS streaming (nrq_wstream.hip).
 int launch_wstream_scalar(int dtype, const MatvecLaunch& L);
 int launch_matmul(int dtype, int order, const MatmulLaunch& L);
+// Scalar-order batched matmul on int8 MFMA (nrq_mmq.hip).
+int launch_mmq(int dtype, const MatmulLaunch& L);
 int launch_quantize_q8_0(const QuantLaunch& L);
 // y[0..n) = +0.0 (a kernel, not hipMemsetAsync, so it is safe under graph capture)
 int launch_fill_zero(float* y, long long n, void* stream);

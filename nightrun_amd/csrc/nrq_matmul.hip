@@ -1,7 +1,9 @@
-// Batched matmul (prefill, batch <= 64): y[b][r] = dot(W[r,:], xs[b]).
+// Batched matmul (prefill): y[b][r] = dot(W[r,:], xs[b]).
 // The reference guarantees matmul == per-token matvec bit for bit
-// (kernels.rs:84-90, kquant.rs:566-569). This first version runs the decode
-// kernel once per token, which is bitwise equal by construction.
+// (kernels.rs:84-90, kquant.rs:566-569). Scalar order runs the int8-MFMA tile
+// kernel (nrq_mmq.hip). AVX2 order runs the decode kernel once per token,
+// which is bitwise equal by construction: the reference's 4-wide AVX2 tiles
+// return the 1-wide result per lane (kernels.rs:222-223).
 #include "nrq_device.h"
 #include "nrq_launch.h"
 
@@ -9,6 +11,7 @@ namespace nrq {
 
 int launch_matmul(int dtype, int order, const MatmulLaunch& L) {
   if (L.rows <= 0 || L.bpr <= 0 || L.batch <= 0) return 0;
+  if (order == kOrderScalar && L.variant == 0) return launch_mmq(dtype, L);
   const size_t xb = dtype == kQ8_0 ? (size_t)kQ8_0Bytes : (size_t)kQ8KBytes;
   for (int b = 0; b < L.batch; b++) {
     MatvecLaunch M;

@@ -352,3 +352,57 @@ def test_benchmark_configs_bitexact(gpu, oracle, cfg, order):
     x = oracle.quantize_act(dtype, oracle.Rng(seed ^ 0xABCDEF).normal(cols))
     want = oracle.matvec(dtype, order, w, x, rows, cols, threads=THREADS)
     assert_bitwise(gpu_matvec(dtype, order, w, x, rows, cols), want, cfg)
+
+
+# ---- prefill matmul (int8 MFMA tile in scalar order) -------------------------------------
+
+# Qwen3-4B layer at M = 64 tokens: hidden 2560, attention width 4096, ffn 9728,
+# 8 KV heads x 128 (kv width 1024); Q/K/V/O/gate/up Q4_K, down Q6_K.
+QWEN3_4B_LAYER = {
+    "wq": (2, 4096, 2560), "wk": (2, 1024, 2560), "wv": (2, 1024, 2560), "wo": (2, 2560, 4096),
+    "w_gate": (2, 9728, 2560), "w_up": (2, 9728, 2560), "w_down": (3, 2560, 9728),
+}
+
+
+@pytest.mark.parametrize("name", list(QWEN3_4B_LAYER))
+def test_prefill_qwen3_4b_layer_bitexact(gpu, oracle, name):
+    """Batched M = 64 matmul on the layer's real shapes equals the oracle's
+    matmul (== 64 matvecs, tests/kquant.rs:297-329) bit for bit."""
+    dtype, rows, cols = QWEN3_4B_LAYER[name]
+    seed = 0x5EED0004 + list(QWEN3_4B_LAYER).index(name)
+    w = oracle.gen_weights(dtype, seed, rows, cols)
+    xs = oracle.quantize_act(dtype, oracle.Rng(seed ^ 0x77).normal(64 * cols))
+    want = oracle.matmul(dtype, 0, w, xs, rows, cols, 64, threads=THREADS)
+    assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, 64), want, name)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_matmul_batches_past_64(gpu, oracle, dtype):
+    """The reference's matmul takes any batch; a launch covers it in 64-token
+    tiles (batch 65 and 130: a one-token tile and a partial tile)."""
+    qk = oracle.QK[dtype]
+    rows, cols = 50, 3 * qk
+    w = oracle.gen_weights(dtype, 91, rows, cols)
+    for batch in (65, 130):
+        xs = oracle.quantize_act(dtype, oracle.Rng(92 + batch).normal(batch * cols))
+        assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, batch),
+                       oracle.matmul(dtype, 0, w, xs, rows, cols, batch, threads=THREADS), f"batch {batch}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_matmul_adversarial_and_saturated(gpu, oracle, dtype):
+    """Adversarial activations, the reference quantizers' weights, and the
+    saturated blocks of tests/kquant.rs:210-245 through the MFMA path."""
+    qk = oracle.QK[dtype]
+    rows, cols, batch = 33, 4 * qk, 19
+    rng = oracle.Rng(400 + dtype)
+    w = oracle.quantize_weights_ref(dtype, rng.adversarial(rows * cols))
+    xs = oracle.quantize_act(dtype, rng.adversarial(batch * cols))
+    assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, batch), oracle.matmul(dtype, 0, w, xs, rows, cols, batch))
+    if dtype != 1:
+        from tests.test_oracle import saturated_blocks
+
+        q4, q6 = saturated_blocks(oracle)
+        ws = np.repeat(q4 if dtype == 2 else q6, rows * 4, axis=0)
+        assert_bitwise(gpu_matmul(dtype, 0, ws, xs, rows, cols, batch),
+                       oracle.matmul(dtype, 0, ws, xs, rows, cols, batch))
