@@ -121,8 +121,67 @@ int nrq_dev_quantize_q8k(const float *src, size_t n, void *out, void *stream);
  * out is [rows][cols/QK][1|9|16] int32. Diagnostic path for parity tests. */
 int nrq_dev_block_sums(int dtype, const void *w, const void *x, int32_t *out, size_t rows, size_t cols,
                        void *stream);
+/* The forward pass's math functions over n f32 values in HBM, for parity
+ * tests: fn 0 = expf, 1 = the sine and 2 = the cosine of sincosf (restating
+ * the musl algorithms the reference's libm crate ports; vec.rs:30-52,
+ * rope.rs:49-65 call them). Diagnostic path. */
+int nrq_dev_mathf(int fn, const float *x, float *y, size_t n, void *stream);
 /* Waits for all work on `stream` (NULL = library stream). */
 int nrq_sync(void *stream);
+
+/* ---- Llama-family decode on one GPU ----------------------------------------------
+ * The forward pass of crates/nr-model/src/infer.rs (InferCtx) for the Llama
+ * recipe (no qk-norm, adjacent-pair RoPE without frequency scaling, neutral
+ * embed/residual/logit scales), every tensor resident in HBM, bit-identical to
+ * the reference's scalar kernels, with greedy sampling (sample.rs:32-35). The
+ * KV cache holds f16 bits, as the reference's does (infer.rs:297-299). */
+
+#define NRQ_F32 0 /* dtype of f32 tensors (norm weights) */
+
+/* tensor kinds: TensorKind ids (crates/nr-model/src/format.rs:53-69) */
+#define NRQ_TENSOR_TOK_EMBED 1
+#define NRQ_TENSOR_OUTPUT_NORM 2
+#define NRQ_TENSOR_OUTPUT 3
+#define NRQ_TENSOR_ATTN_NORM 10
+#define NRQ_TENSOR_ATTN_Q 11
+#define NRQ_TENSOR_ATTN_K 12
+#define NRQ_TENSOR_ATTN_V 13
+#define NRQ_TENSOR_ATTN_O 14
+#define NRQ_TENSOR_FFN_NORM 15
+#define NRQ_TENSOR_FFN_GATE 16
+#define NRQ_TENSOR_FFN_UP 17
+#define NRQ_TENSOR_FFN_DOWN 18
+
+typedef struct nrq_model nrq_model;
+
+/* Dims (crates/nr-model/src/infer.rs:60-73 Dims, format.rs:126-156 Meta). */
+typedef struct {
+  int dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, vocab, ctx;
+  float norm_eps, rope_theta;
+} nrq_model_config;
+
+/* InferCtx::new (infer.rs:352-492): device KV cache, scratch, rope table. */
+int nrq_model_create(const nrq_model_config *cfg, nrq_model **out);
+/* Binds one tensor already in HBM (matrices Q8_0/Q4_K/Q6_K in their block
+ * layout, 16-byte aligned; norms NRQ_F32). The output head is tied to the
+ * embedding until an NRQ_TENSOR_OUTPUT is set (infer.rs:415-419). The
+ * embedding must be Q8_0. */
+int nrq_model_set_tensor(nrq_model *m, int kind, int layer, int dtype, const void *dev_ptr);
+/* InferCtx::reset (infer.rs:494-496). */
+int nrq_model_reset(nrq_model *m);
+/* InferCtx::pos. */
+int nrq_model_pos(const nrq_model *m);
+/* InferCtx::forward (infer.rs:510-595): one token at the current position;
+ * copies the logits to host `logits` (vocab floats) unless NULL. */
+int nrq_model_forward(nrq_model *m, uint32_t token, float *logits);
+/* Greedy generation: n steps of forward + argmax (sample.rs:33-35), each
+ * step's token feeding the next, device-resident (one HIP graph per step).
+ * out_tokens gets the n sampled ids; last_logits (optional) the last step's
+ * logits. */
+int nrq_model_generate(nrq_model *m, uint32_t token, int n, uint32_t *out_tokens, float *last_logits);
+/* Copies the f16 KV cache ([n_layers][ctx][kv_dim] each) to host buffers. */
+int nrq_model_kv_cache(nrq_model *m, void *k, void *v, size_t bytes);
+int nrq_model_destroy(nrq_model *m);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,15 @@ SIGNATURES = {
     "nrq_dev_quantize_q8k": ([_vp, _sz, _vp, _vp], _i),
     "nrq_dev_block_sums": ([_i, _vp, _vp, _vp, _sz, _sz, _vp], _i),
     "nrq_sync": ([_vp], _i),
+    "nrq_dev_mathf": ([_i, _vp, _vp, _sz, _vp], _i),
+    "nrq_model_create": ([_vp, C.POINTER(_vp)], _i),
+    "nrq_model_set_tensor": ([_vp, _i, _i, _i, _vp], _i),
+    "nrq_model_reset": ([_vp], _i),
+    "nrq_model_pos": ([_vp], _i),
+    "nrq_model_forward": ([_vp, C.c_uint32, _vp], _i),
+    "nrq_model_generate": ([_vp, C.c_uint32, _i, _vp, _vp], _i),
+    "nrq_model_kv_cache": ([_vp, _vp, _vp, _sz], _i),
+    "nrq_model_destroy": ([_vp], _i),
 }
 
 

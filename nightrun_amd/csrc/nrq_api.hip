@@ -205,6 +205,10 @@ int dev_check(const char* name, int dtype, int order) {
 
 }  // namespace
 
+namespace nrq {
+void set_last_error(const char* msg) { g_err = msg; }
+}  // namespace nrq
+
 extern "C" {
 
 int nrq_init(int device) {

@@ -95,4 +95,34 @@ __device__ __forceinline__ void q6k_planes(uint32_t qlA, uint32_t qlB, uint32_t 
   q6[3] = ((qlB >> 4) & m4) | ((qh >> 2) & m2h);
 }
 
+// f16.rs:25-56
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float v) {
+  uint32_t bits = __float_as_uint(v);
+  uint32_t sign = (bits >> 31) << 15;
+  int exp = (int)((bits >> 23) & 0xffu);
+  uint32_t frac = bits & 0x7fffffu;
+  if (exp == 0xff) return sign | 0x7c00u | (frac != 0 ? 0x200u : 0u);
+  int e = exp - 127 + 15;
+  if (e >= 0x1f) return sign | 0x7c00u;
+  if (e <= 0) {
+    if (e < -10) return sign;
+    uint32_t f = frac | 0x800000u;
+    uint32_t shift = (uint32_t)(14 - e);
+    uint32_t half = 1u << (shift - 1);
+    return (sign | ((f + half) >> shift)) & 0xffffu;
+  }
+  uint32_t out = sign | ((uint32_t)e << 10) | (frac >> 13);
+  uint32_t round = frac & 0x1fffu;
+  if (round > 0x1000u || (round == 0x1000u && (out & 1u) != 0)) out += 1;
+  return out & 0xffffu;
+}
+
+// Rust `f as i32`: truncate, saturate, NaN -> 0.
+__device__ __forceinline__ int rust_f32_to_i32(float f) {
+  if (f != f) return 0;
+  if (f >= 2147483648.0f) return 2147483647;
+  if (f <= -2147483648.0f) return (-2147483647 - 1);
+  return (int)f;
+}
+
 }  // namespace nrq

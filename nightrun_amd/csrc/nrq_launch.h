@@ -61,4 +61,7 @@ int launch_quantize_q8k(const QuantLaunch& L);
 // Q4_K/Q6_K/Q8_0 per-(row, block) exact integer sums (test/diagnostic path).
 int launch_block_sums(int dtype, const void* w, const void* x, int32_t* out, int rows, int bpr, void* stream);
 
+// Sets the message nrq_last_error() returns on this thread (nrq_api.hip).
+void set_last_error(const char* msg);
+
 }  // namespace nrq

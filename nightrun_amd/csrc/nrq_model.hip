@@ -1,0 +1,849 @@
+// Llama-family decode on one GPU, every tensor resident in HBM: the forward
+// pass of crates/nr-model/src/infer.rs (InferCtx::forward, infer.rs:510-595)
+// with greedy sampling (sample.rs:32-35), bit-identical to the reference's
+// scalar kernels. The quantized matvecs are libnrq's decode kernels; this file
+// holds the f32 steps between them, each written in the reference's order:
+//   rmsnorm   (crates/nr-tensor/src/vec.rs:4-14): sequential sum of squares
+//   rope      (crates/nr-tensor/src/rope.rs:49-65): adjacent pairs, sincosf
+//   KV append (infer.rs:547-551): f32 -> f16 softfloat (f16.rs:25-56)
+//   attention (infer.rs:553-572): dot_f16 / softmax / axpy_f16 in position order
+//   swiglu    (vec.rs:45-52), residual saxpy (vec.rs:63-67), argmax (vec.rs:80-90)
+// expf and sincosf restate the published musl single-precision algorithms that
+// the reference's libm crate (0.2.16) ports.
+//
+// The step is device-driven: the current token and position live in device
+// memory, the embedding kernel reads the token and the argmax kernel writes
+// the next one and advances the position, so a whole greedy step is one fixed
+// kernel sequence (replayed as a HIP graph by nrq_model_generate).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/nrq.h"
+#include "nrq_device.h"
+#include "nrq_launch.h"
+
+namespace nrq {
+
+// ---- libm restatements (device) -------------------------------------------------
+
+namespace {
+
+// musl scalbnf
+__device__ __forceinline__ float dev_scalbnf(float x, int n) {
+  float y = x;
+  if (n > 127) {
+    y *= __uint_as_float(0x7f000000u);
+    n -= 127;
+    if (n > 127) {
+      y *= __uint_as_float(0x7f000000u);
+      n -= 127;
+      if (n > 127) n = 127;
+    }
+  } else if (n < -126) {
+    y *= __uint_as_float(0x00800000u) * __uint_as_float(0x4b800000u);
+    n += 126 - 24;
+    if (n < -126) {
+      y *= __uint_as_float(0x00800000u) * __uint_as_float(0x4b800000u);
+      n += 126 - 24;
+      if (n < -126) n = -126;
+    }
+  }
+  return y * __uint_as_float((uint32_t)(0x7f + n) << 23);
+}
+
+// musl expf (FreeBSD e_expf.c algorithm): x = k ln2 + r, exp(r) from the
+// two-term Remez form, scaled by 2^k.
+__device__ float dev_expf(float x) {
+  const float ln2hi = 6.9314575195e-01f, ln2lo = 1.4286067653e-06f, invln2 = 1.4426950216e+00f;
+  const float P1 = 1.6666625440e-1f, P2 = -2.7667332906e-3f;
+  uint32_t hx = __float_as_uint(x);
+  const int sign = (int)(hx >> 31);
+  hx &= 0x7fffffffu;
+  if (hx >= 0x42aeac50u) {
+    if (hx > 0x7f800000u) return x;
+    if (hx >= 0x42b17218u && !sign) return x * __uint_as_float(0x7f000000u);
+    if (sign && hx >= 0x42cff1b5u) return 0.0f;
+  }
+  int k;
+  float hi, lo;
+  if (hx > 0x3eb17218u) {
+    if (hx > 0x3f851592u)
+      k = (int)(invln2 * x + (sign ? -0.5f : 0.5f));
+    else
+      k = 1 - sign - sign;
+    const float kf = (float)k;
+    hi = x - kf * ln2hi;
+    lo = kf * ln2lo;
+    x = hi - lo;
+  } else if (hx > 0x39000000u) {
+    k = 0;
+    hi = x;
+    lo = 0.0f;
+  } else {
+    return 1.0f + x;
+  }
+  const float xx = x * x;
+  const float c = x - xx * (P1 + xx * P2);
+  const float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
+  return k == 0 ? y : dev_scalbnf(y, k);
+}
+
+// __sindf / __cosdf: double polynomials on [-pi/4, pi/4]
+__device__ __forceinline__ float dev_sindf(double x) {
+  const double S1 = -0x15555554cbac77.0p-55, S2 = 0x111110896efbb2.0p-59;
+  const double S3 = -0x1a00f9e2cae774.0p-65, S4 = 0x16cd878c3b46a7.0p-71;
+  const double z = x * x, w = z * z, r = S3 + z * S4, s = z * x;
+  return (float)((x + s * (S1 + z * S2)) + s * w * r);
+}
+__device__ __forceinline__ float dev_cosdf(double x) {
+  const double C0 = -0x1ffffffd0c5e81.0p-54, C1 = 0x155553e1053a42.0p-57;
+  const double C2 = -0x16c087e80f1e27.0p-62, C3 = 0x199342e0ee5069.0p-68;
+  const double z = x * x, w = z * z, r = C2 + z * C3;
+  return (float)(((1.0 + z * C0) + w * C1) + (w * z) * r);
+}
+
+// __rem_pio2f, medium path (|x| < 2^28 pi/2; rope angles stay far below)
+__device__ __forceinline__ int dev_rem_pio2f(float x, double* y) {
+  const double toint = 1.5 / 2.220446049250313e-16, pio4 = 0x1.921fb6p-1;
+  const double invpio2 = 6.36619772367581382433e-01, pio2_1 = 1.57079631090164184570e+00;
+  const double pio2_1t = 1.58932547735281966916e-08;
+  if ((__float_as_uint(x) & 0x7fffffffu) < 0x4dc90fdbu) {
+    double fn = (double)x * invpio2 + toint - toint;
+    int n = (int)fn;
+    *y = x - fn * pio2_1 - fn * pio2_1t;
+    if (*y < -pio4) {
+      n--;
+      fn--;
+      *y = x - fn * pio2_1 - fn * pio2_1t;
+    } else if (*y > pio4) {
+      n++;
+      fn++;
+      *y = x - fn * pio2_1 - fn * pio2_1t;
+    }
+    return n;
+  }
+  *y = __builtin_nan("");
+  return 0;
+}
+
+// musl sincosf
+__device__ void dev_sincosf(float x, float* sn, float* cs) {
+  const double s1pio2 = 1 * 1.57079632679489661923, s2pio2 = 2 * 1.57079632679489661923;
+  const double s3pio2 = 3 * 1.57079632679489661923, s4pio2 = 4 * 1.57079632679489661923;
+  uint32_t ix = __float_as_uint(x);
+  const unsigned sign = ix >> 31;
+  ix &= 0x7fffffffu;
+  if (ix <= 0x3f490fdau) {
+    if (ix < 0x39800000u) {
+      *sn = x;
+      *cs = 1.0f;
+      return;
+    }
+    *sn = dev_sindf(x);
+    *cs = dev_cosdf(x);
+    return;
+  }
+  if (ix <= 0x407b53d1u) {
+    if (ix <= 0x4016cbe3u) {
+      if (sign) {
+        *sn = -dev_cosdf(x + s1pio2);
+        *cs = dev_sindf(x + s1pio2);
+      } else {
+        *sn = dev_cosdf(s1pio2 - x);
+        *cs = dev_sindf(s1pio2 - x);
+      }
+      return;
+    }
+    *sn = -dev_sindf(sign ? x + s2pio2 : x - s2pio2);
+    *cs = -dev_cosdf(sign ? x + s2pio2 : x - s2pio2);
+    return;
+  }
+  if (ix <= 0x40e231d5u) {
+    if (ix <= 0x40afeddfu) {
+      if (sign) {
+        *sn = dev_cosdf(x + s3pio2);
+        *cs = -dev_sindf(x + s3pio2);
+      } else {
+        *sn = -dev_cosdf(x - s3pio2);
+        *cs = dev_sindf(x - s3pio2);
+      }
+      return;
+    }
+    *sn = dev_sindf(sign ? x + s4pio2 : x - s4pio2);
+    *cs = dev_cosdf(sign ? x + s4pio2 : x - s4pio2);
+    return;
+  }
+  if (ix >= 0x7f800000u) {
+    *sn = *cs = x - x;
+    return;
+  }
+  double y;
+  const unsigned n = (unsigned)dev_rem_pio2f(x, &y);
+  const float s = dev_sindf(y), c = dev_cosdf(y);
+  switch (n & 3) {
+    case 0: *sn = s; *cs = c; break;
+    case 1: *sn = c; *cs = -s; break;
+    case 2: *sn = -s; *cs = -c; break;
+    default: *sn = -c; *cs = s; break;
+  }
+}
+
+// Control words in device memory.
+enum { CTL_TOKEN = 0, CTL_POS = 1, CTL_STEP = 2, CTL_WORDS = 4 };
+
+// ---- kernels ------------------------------------------------------------------------
+
+// QMat::dequant_row for Q8_0 (infer.rs:37-42, q8.rs:47-55): x[i] = f32(q) * d
+__global__ void embed_q8_0_kernel(const uint8_t* __restrict__ E, const int* __restrict__ ctl, int dim,
+                                  float* __restrict__ x) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= dim) return;
+  const size_t tok = (size_t)(uint32_t)ctl[CTL_TOKEN];
+  const uint8_t* blk = E + (tok * (dim / 32) + i / 32) * kQ8_0Bytes;
+  const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+  x[i] = (float)(int8_t)blk[2 + (i & 31)] * d;
+}
+
+constexpr int kNormNT = 256;
+
+// Optional residual x += 1.0 * add (vec.rs:63-67, residual_scale 1), then
+// rmsnorm (vec.rs:4-14): ss += v*v in element order, scale = 1/sqrtf(ss/n + eps),
+// out = x * scale * w. Writes out (f32) and, when xq != null, its Q8_0 blocks
+// (q8.rs:27-44). One workgroup; n <= kNormMax.
+constexpr int kNormMax = 8192;
+__global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, const float* __restrict__ add,
+                                                       const float* __restrict__ w, int n, float eps,
+                                                       float* __restrict__ out, uint8_t* __restrict__ xq) {
+  __shared__ float sq[kNormMax];
+  __shared__ float s_scale;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < n; i += kNormNT) {
+    float v = x[i];
+    if (add) {
+      v = v + 1.0f * add[i];
+      x[i] = v;
+    }
+    sq[i] = v * v;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float ss = 0.0f;
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+      const float4 s4 = *(const float4*)(sq + i);
+      ss = ss + s4.x;
+      ss = ss + s4.y;
+      ss = ss + s4.z;
+      ss = ss + s4.w;
+    }
+    for (; i < n; i++) ss = ss + sq[i];
+    s_scale = 1.0f / sqrtf(ss / (float)n + eps);
+  }
+  __syncthreads();
+  const float scale = s_scale;
+  // 32-lane groups: one Q8_0 block per group per pass
+  const int lane32 = tid & 31;
+  for (int i0 = tid - lane32; i0 < n; i0 += kNormNT) {
+    const int i = i0 + lane32;
+    const float v = x[i] * scale * w[i];
+    out[i] = v;
+    if (xq) {
+      float amax = fabsf(v);
+#pragma unroll
+      for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+      amax = fmaxf(0.0f, amax);
+      const uint32_t d_bits = f32_to_f16_bits(amax / 127.0f);
+      const float d = f16_bits_to_f32(d_bits);
+      const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+      const float xi = v * inv;
+      const float r = xi >= 0.0f ? xi + 0.5f : xi - 0.5f;
+      int q = rust_f32_to_i32(r);
+      q = q < -127 ? -127 : (q > 127 ? 127 : q);
+      uint8_t* blk = xq + (size_t)(i >> 5) * kQ8_0Bytes;
+      blk[2 + lane32] = (uint8_t)(int8_t)q;
+      if (lane32 == 0) {
+        blk[0] = (uint8_t)(d_bits & 0xff);
+        blk[1] = (uint8_t)(d_bits >> 8);
+      }
+    }
+  }
+}
+
+// rope::apply on q and k at the current position (rope.rs:49-65, adjacent
+// pairs), then the KV append as f16 (infer.rs:547-551).
+__global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, const float* __restrict__ k,
+                                                      const float* __restrict__ v, const float* __restrict__ freqs,
+                                                      const int* __restrict__ ctl, int n_heads, int n_kv_heads,
+                                                      int hd, int ctx, int layer, uint16_t* __restrict__ kc,
+                                                      uint16_t* __restrict__ vc) {
+  const int pos = ctl[CTL_POS];
+  const int half = hd / 2, kvd = n_kv_heads * hd;
+  const size_t row = ((size_t)layer * ctx + pos) * kvd;
+  const int total = (n_heads + n_kv_heads) * half;
+  for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+    const int head = idx / half, i = idx - head * half;
+    const float angle = (float)pos * freqs[i];
+    float s, c;
+    dev_sincosf(angle, &s, &c);
+    if (head < n_heads) {
+      float* h = q + (size_t)head * hd;
+      const float a = h[2 * i], b = h[2 * i + 1];
+      h[2 * i] = a * c - b * s;
+      h[2 * i + 1] = a * s + b * c;
+    } else {
+      const int kh = head - n_heads;
+      const float* h = k + (size_t)kh * hd;
+      const float a = h[2 * i], b = h[2 * i + 1];
+      kc[row + kh * hd + 2 * i] = (uint16_t)f32_to_f16_bits(a * c - b * s);
+      kc[row + kh * hd + 2 * i + 1] = (uint16_t)f32_to_f16_bits(a * s + b * c);
+    }
+  }
+  for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < kvd; idx += gridDim.x * blockDim.x)
+    vc[row + idx] = (uint16_t)f32_to_f16_bits(v[idx]);
+}
+
+constexpr int kAttNT = 256;
+constexpr int kAttMaxCtx = 8192;
+
+// One workgroup per query head (infer.rs:553-572): scores dot_f16(k_t, q) *
+// scale in dimension order (kernels.rs:146-160), softmax (vec.rs:30-42; the
+// exp-sum in position order), then out[i] += a_t * v_t[i] in position order
+// (kernels.rs:163-173).
+__global__ __launch_bounds__(kAttNT) void attention_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
+                                                           const uint16_t* __restrict__ vc,
+                                                           const int* __restrict__ ctl, int n_heads, int n_kv_heads,
+                                                           int hd, int ctx, int layer, float scale,
+                                                           float* __restrict__ out) {
+  __shared__ float att[kAttMaxCtx];
+  __shared__ float qs[256];
+  __shared__ float red[kAttNT / 64];
+  __shared__ float s_inv;
+  const int h = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int n = ctl[CTL_POS] + 1;
+  const int gqa = n_heads / n_kv_heads;
+  const int kvd = n_kv_heads * hd;
+  const size_t base = (size_t)layer * ctx * kvd + (size_t)(h / gqa) * hd;
+  for (int i = tid; i < hd; i += kAttNT) qs[i] = q[(size_t)h * hd + i];
+  __syncthreads();
+  float mx = -INFINITY;
+  for (int t = tid; t < n; t += kAttNT) {
+    const uint16_t* kr = kc + base + (size_t)t * kvd;
+    float s = 0.0f;
+    for (int i0 = 0; i0 < hd; i0 += 8) {
+      const uint4 kv8 = *(const uint4*)(kr + i0);
+      const uint32_t kw[4] = {kv8.x, kv8.y, kv8.z, kv8.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        s = s + f16_bits_to_f32(kw[j] & 0xffffu) * qs[i0 + 2 * j];
+        s = s + f16_bits_to_f32(kw[j] >> 16) * qs[i0 + 2 * j + 1];
+      }
+    }
+    const float a = s * scale;
+    att[t] = a;
+    mx = fmaxf(mx, a);
+  }
+  // max is order-independent (and the sign of a zero maximum cannot change
+  // any exp(v - max))
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int wv = 1; wv < kAttNT / 64; wv++) mx = fmaxf(mx, red[wv]);
+  for (int t = tid; t < n; t += kAttNT) att[t] = dev_expf(att[t] - mx);
+  __syncthreads();
+  if (tid == 0) {
+    float sum = 0.0f;
+    int t = 0;
+    for (; t + 4 <= n; t += 4) {
+      const float4 e = *(const float4*)(att + t);
+      sum = sum + e.x;
+      sum = sum + e.y;
+      sum = sum + e.z;
+      sum = sum + e.w;
+    }
+    for (; t < n; t++) sum = sum + att[t];
+    s_inv = 1.0f / sum;
+  }
+  __syncthreads();
+  const float inv = s_inv;
+  for (int t = tid; t < n; t += kAttNT) att[t] = att[t] * inv;
+  __syncthreads();
+  for (int i = tid; i < hd; i += kAttNT) {
+    const uint16_t* vcol = vc + base + i;
+    float o = 0.0f;
+    int t = 0;
+    for (; t + 8 <= n; t += 8) {
+      float vv[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) vv[j] = f16_bits_to_f32(vcol[(size_t)(t + j) * kvd]);
+#pragma unroll
+      for (int j = 0; j < 8; j++) o = o + att[t + j] * vv[j];
+    }
+    for (; t < n; t++) o = o + att[t] * f16_bits_to_f32(vcol[(size_t)t * kvd]);
+    out[(size_t)h * hd + i] = o;
+  }
+}
+
+// vec.rs:45-52: gate = gate / (1 + expf(-gate)) * up
+__global__ void swiglu_kernel(float* __restrict__ gate, const float* __restrict__ up, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float g = gate[i];
+  const float silu = g / (1.0f + dev_expf(-g));
+  gate[i] = silu * up[i];
+}
+
+constexpr int kArgNT = 1024;
+
+// vec.rs:80-90 (first index of the largest value; NaN never wins), then the
+// step's bookkeeping: next token, output slot, position + 1.
+__global__ __launch_bounds__(kArgNT) void argmax_kernel(const float* __restrict__ x, int n, int* __restrict__ ctl,
+                                                        uint32_t* __restrict__ out_tokens, int max_out) {
+  __shared__ float sv[kArgNT / 64];
+  __shared__ int si[kArgNT / 64];
+  const int tid = threadIdx.x;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = tid; i < n; i += kArgNT) {
+    const float v = x[i];
+    if (v > bv) {
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(bv, m);
+    const int oi = __shfl_xor(bi, m);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if ((tid & 63) == 0) {
+    sv[tid >> 6] = bv;
+    si[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int wv = 1; wv < kArgNT / 64; wv++)
+      if (sv[wv] > bv || (sv[wv] == bv && si[wv] < bi)) {
+        bv = sv[wv];
+        bi = si[wv];
+      }
+    const int best = bi == 0x7fffffff ? 0 : bi;
+    ctl[CTL_TOKEN] = best;
+    const int step = ctl[CTL_STEP];
+    if (out_tokens && step < max_out) out_tokens[step] = (uint32_t)best;
+    ctl[CTL_STEP] = step + 1;
+    ctl[CTL_POS] = ctl[CTL_POS] + 1;
+  }
+}
+
+__global__ void mathf_kernel(int fn, const float* __restrict__ x, float* __restrict__ y, long long n) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  if (fn == 0) {
+    y[i] = dev_expf(x[i]);
+  } else {
+    float s, c;
+    dev_sincosf(x[i], &s, &c);
+    y[i] = fn == 1 ? s : c;
+  }
+}
+
+}  // namespace
+}  // namespace nrq
+
+// ---- host side -----------------------------------------------------------------------
+
+namespace {
+
+int mfail(int code, const char* msg) {
+  nrq::set_last_error(msg);
+  return code;
+}
+
+#define MHIP(expr)                                                                  \
+  do {                                                                              \
+    hipError_t e_ = (expr);                                                         \
+    if (e_ != hipSuccess) {                                                         \
+      nrq::set_last_error((std::string(#expr) + ": " + hipGetErrorString(e_)).c_str()); \
+      return NRQ_ERR_DEVICE;                                                        \
+    }                                                                               \
+  } while (0)
+
+struct Mat {
+  const void* w = nullptr;
+  int dt = 0;
+};
+
+struct Layer {
+  Mat m[7];  // q, k, v, o, gate, up, down
+  const float* attn_norm = nullptr;
+  const float* ffn_norm = nullptr;
+};
+
+size_t act_bytes(int dt, size_t n) { return dt == NRQ_Q8_0 ? n / 32 * 34 : n / 256 * 292; }
+int qk_of(int dt) { return dt == NRQ_Q8_0 ? 32 : 256; }
+
+}  // namespace
+
+struct nrq_model {
+  nrq_model_config cfg{};
+  int kv_dim = 0, att_dim = 0, maxd = 0;
+  hipStream_t stream = nullptr;
+  Mat embed, output;
+  const float* out_norm = nullptr;
+  std::vector<Layer> L;
+  float* freqs = nullptr;
+  uint16_t *kc = nullptr, *vc = nullptr;
+  float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
+  float *gate = nullptr, *up = nullptr, *xb2 = nullptr, *logits = nullptr;
+  uint8_t *xq = nullptr, *xq2 = nullptr;
+  int* ctl = nullptr;
+  uint32_t* out_tokens = nullptr;
+  int max_out = 0;
+  hipGraphExec_t exec = nullptr;
+  hipGraph_t graph = nullptr;
+  int host_pos = 0;
+};
+
+namespace {
+
+// Quantize `src` (n floats) into the activation format of weight dtype dt.
+int quantize_for(nrq_model* m, int dt, const float* src, int n, uint8_t* dst) {
+  nrq::QuantLaunch Q{src, dst, (long long)n, m->stream};
+  const int rc = dt == NRQ_Q8_0 ? nrq::launch_quantize_q8_0(Q) : nrq::launch_quantize_q8k(Q);
+  return rc ? mfail(NRQ_ERR_DEVICE, "model: activation quantize launch failed") : NRQ_OK;
+}
+
+int matvec(nrq_model* m, const Mat& w, const uint8_t* xq, float* y, int rows, int cols) {
+  nrq::MatvecLaunch L;
+  L.w = w.w;
+  L.x = xq;
+  L.y = y;
+  L.rows = rows;
+  L.bpr = cols / qk_of(w.dt);
+  L.tile_rows = 0;
+  L.stream = m->stream;
+  const int rc = nrq::launch_matvec(w.dt, nrq::kOrderScalar, L);
+  return rc ? mfail(rc == nrq::NRQ_LAUNCH_TOO_WIDE ? NRQ_ERR_UNSUPPORTED : NRQ_ERR_DEVICE, "model: matvec launch failed")
+            : NRQ_OK;
+}
+
+// Normalize x (after the pending residual `add`), quantize for dtype dt.
+int norm_quant(nrq_model* m, const float* add, const float* w, int dt) {
+  const auto& c = m->cfg;
+  hipLaunchKernelGGL(nrq::norm_kernel, dim3(1), dim3(nrq::kNormNT), 0, m->stream, m->x, add, w, c.dim, c.norm_eps,
+                     m->xb, dt == NRQ_Q8_0 ? m->xq : nullptr);
+  if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: norm launch failed");
+  if (dt != NRQ_Q8_0) return quantize_for(m, dt, m->xb, c.dim, m->xq);
+  return NRQ_OK;
+}
+
+// Matvecs sharing one input vector: the activation is quantized once per
+// format (infer.rs:232-261); `xb` holds the f32 input, m->xq its blocks for
+// the first matrix's format.
+int matvec_group(nrq_model* m, const Mat* const* ws, float* const* ys, const int* rows, int n, int cols) {
+  const int first = ws[0]->dt == NRQ_Q8_0 ? 0 : 1;
+  bool other_ready = false;
+  for (int i = 0; i < n; i++) {
+    const int fmt = ws[i]->dt == NRQ_Q8_0 ? 0 : 1;
+    const uint8_t* xq = m->xq;
+    if (fmt != first) {
+      if (!other_ready) {
+        int rc = quantize_for(m, ws[i]->dt, m->xb, cols, m->xq2);
+        if (rc) return rc;
+        other_ready = true;
+      }
+      xq = m->xq2;
+    }
+    int rc = matvec(m, *ws[i], xq, ys[i], rows[i], cols);
+    if (rc) return rc;
+  }
+  return NRQ_OK;
+}
+
+// One decode step, enqueued on m->stream (infer.rs:510-595 + argmax).
+int enqueue_step(nrq_model* m) {
+  const auto& c = m->cfg;
+  const int d = c.dim, kvd = m->kv_dim, att = m->att_dim, ffn = c.ffn_dim;
+  hipLaunchKernelGGL(nrq::embed_q8_0_kernel, dim3((d + 255) / 256), dim3(256), 0, m->stream,
+                     (const uint8_t*)m->embed.w, m->ctl, d, m->x);
+  if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: embed launch failed");
+  const float scale = 1.0f / sqrtf((float)c.head_dim);
+  const float* pending = nullptr;  // residual not yet added into x
+  int rc;
+  for (int l = 0; l < c.n_layers; l++) {
+    const Layer& Ly = m->L[l];
+    if ((rc = norm_quant(m, pending, Ly.attn_norm, Ly.m[0].dt))) return rc;
+    {
+      const Mat* ws[3] = {&Ly.m[0], &Ly.m[1], &Ly.m[2]};
+      float* ys[3] = {m->q, m->k, m->v};
+      const int rows[3] = {att, kvd, kvd};
+      if ((rc = matvec_group(m, ws, ys, rows, 3, d))) return rc;
+    }
+    hipLaunchKernelGGL(nrq::rope_kv_kernel, dim3(4), dim3(256), 0, m->stream, m->q, m->k, m->v, m->freqs, m->ctl,
+                       c.n_heads, c.n_kv_heads, c.head_dim, c.ctx, l, m->kc, m->vc);
+    hipLaunchKernelGGL(nrq::attention_kernel, dim3(c.n_heads), dim3(nrq::kAttNT), 0, m->stream, m->q, m->kc, m->vc,
+                       m->ctl, c.n_heads, c.n_kv_heads, c.head_dim, c.ctx, l, scale, m->attn);
+    if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: attention launch failed");
+    if ((rc = quantize_for(m, Ly.m[3].dt, m->attn, att, m->xq))) return rc;
+    if ((rc = matvec(m, Ly.m[3], m->xq, m->xb2, d, att))) return rc;
+    if ((rc = norm_quant(m, m->xb2, Ly.ffn_norm, Ly.m[4].dt))) return rc;
+    {
+      const Mat* ws[2] = {&Ly.m[4], &Ly.m[5]};
+      float* ys[2] = {m->gate, m->up};
+      const int rows[2] = {ffn, ffn};
+      if ((rc = matvec_group(m, ws, ys, rows, 2, d))) return rc;
+    }
+    hipLaunchKernelGGL(nrq::swiglu_kernel, dim3((ffn + 255) / 256), dim3(256), 0, m->stream, m->gate, m->up, ffn);
+    if ((rc = quantize_for(m, Ly.m[6].dt, m->gate, ffn, m->xq))) return rc;
+    if ((rc = matvec(m, Ly.m[6], m->xq, m->xb2, d, ffn))) return rc;
+    pending = m->xb2;
+  }
+  if ((rc = norm_quant(m, pending, m->out_norm, m->output.dt))) return rc;
+  if ((rc = matvec(m, m->output, m->xq, m->logits, c.vocab, d))) return rc;
+  hipLaunchKernelGGL(nrq::argmax_kernel, dim3(1), dim3(nrq::kArgNT), 0, m->stream, m->logits, c.vocab, m->ctl,
+                     m->out_tokens, m->max_out);
+  if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: argmax launch failed");
+  return NRQ_OK;
+}
+
+int check_ready(nrq_model* m, const char* name) {
+  if (!m) return mfail(NRQ_ERR_ARG, "model: null handle");
+  if (!m->embed.w || !m->out_norm || !m->output.w) return mfail(NRQ_ERR_ARG, "model: embedding/output tensors not set");
+  for (int l = 0; l < m->cfg.n_layers; l++) {
+    const Layer& Ly = m->L[l];
+    for (int i = 0; i < 7; i++)
+      if (!Ly.m[i].w) return mfail(NRQ_ERR_ARG, "model: a layer matrix is not set");
+    if (!Ly.attn_norm || !Ly.ffn_norm) return mfail(NRQ_ERR_ARG, "model: a layer norm is not set");
+  }
+  (void)name;
+  return NRQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
+  if (!cfg || !out) return mfail(NRQ_ERR_ARG, "nrq_model_create: null argument");
+  const nrq_model_config& c = *cfg;
+  if (c.dim <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 || c.ffn_dim <= 0 ||
+      c.vocab <= 0 || c.ctx <= 0)
+    return mfail(NRQ_ERR_SHAPE, "nrq_model_create: non-positive dimension");
+  if (c.n_heads % c.n_kv_heads || c.head_dim % 16 || c.head_dim > 256 || c.dim % 256 || c.ffn_dim % 256 ||
+      (c.n_heads * c.head_dim) % 256)
+    return mfail(NRQ_ERR_UNSUPPORTED, "nrq_model_create: head or width layout not supported");
+  if (c.dim > nrq::kNormMax || c.ctx > nrq::kAttMaxCtx)
+    return mfail(NRQ_ERR_UNSUPPORTED, "nrq_model_create: dim or context larger than the kernels' LDS buffers");
+  nrq_model* m = new nrq_model();
+  m->cfg = c;
+  m->kv_dim = c.n_kv_heads * c.head_dim;
+  m->att_dim = c.n_heads * c.head_dim;
+  m->maxd = std::max(std::max(c.dim, m->att_dim), c.ffn_dim);
+  m->L.resize(c.n_layers);
+  auto bail = [&](hipError_t e, const char* what) {
+    nrq::set_last_error((std::string(what) + ": " + hipGetErrorString(e)).c_str());
+    nrq_model_destroy(m);
+    return NRQ_ERR_DEVICE;
+  };
+  hipError_t e;
+  if ((e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking)) != hipSuccess) return bail(e, "stream");
+  const size_t kvn = (size_t)c.n_layers * c.ctx * m->kv_dim;
+  struct {
+    void** p;
+    size_t bytes;
+  } allocs[] = {
+      {(void**)&m->freqs, (size_t)c.head_dim / 2 * 4}, {(void**)&m->kc, kvn * 2}, {(void**)&m->vc, kvn * 2},
+      {(void**)&m->x, (size_t)c.dim * 4}, {(void**)&m->xb, (size_t)m->maxd * 4},
+      {(void**)&m->q, (size_t)m->att_dim * 4}, {(void**)&m->k, (size_t)m->kv_dim * 4},
+      {(void**)&m->v, (size_t)m->kv_dim * 4}, {(void**)&m->attn, (size_t)m->att_dim * 4},
+      {(void**)&m->gate, (size_t)c.ffn_dim * 4}, {(void**)&m->up, (size_t)c.ffn_dim * 4},
+      {(void**)&m->xb2, (size_t)c.dim * 4}, {(void**)&m->logits, (size_t)c.vocab * 4},
+      {(void**)&m->xq, act_bytes(NRQ_Q8_0, m->maxd) + act_bytes(NRQ_Q4_K, m->maxd) + 64},
+      {(void**)&m->xq2, act_bytes(NRQ_Q8_0, m->maxd) + act_bytes(NRQ_Q4_K, m->maxd) + 64},
+      {(void**)&m->ctl, nrq::CTL_WORDS * 4},
+  };
+  for (auto& a : allocs) {
+    if ((e = hipMalloc(a.p, a.bytes)) != hipSuccess) return bail(e, "hipMalloc");
+    if ((e = hipMemset(*a.p, 0, a.bytes)) != hipSuccess) return bail(e, "hipMemset");
+  }
+  // rope_freqs (rope.rs:14-34, no scaling): theta^(-2i/head_dim), on the host
+  std::vector<float> f(c.head_dim / 2);
+  for (int i = 0; i < c.head_dim / 2; i++) {
+    const float exponent = -2.0f * (float)i / (float)c.head_dim;
+    f[i] = powf(c.rope_theta, exponent);
+  }
+  if ((e = hipMemcpy(m->freqs, f.data(), f.size() * 4, hipMemcpyHostToDevice)) != hipSuccess) return bail(e, "freqs");
+  *out = m;
+  return NRQ_OK;
+}
+
+int nrq_model_set_tensor(nrq_model* m, int kind, int layer, int dtype, const void* dev_ptr) {
+  if (!m || !dev_ptr) return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: null argument");
+  const bool is_norm = kind == NRQ_TENSOR_ATTN_NORM || kind == NRQ_TENSOR_FFN_NORM || kind == NRQ_TENSOR_OUTPUT_NORM;
+  if (is_norm) {
+    if (dtype != NRQ_F32) return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: norms are f32");
+  } else {
+    if (dtype != NRQ_Q8_0 && dtype != NRQ_Q4_K && dtype != NRQ_Q6_K)
+      return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: unknown matrix dtype");
+    if (((uintptr_t)dev_ptr & 15) != 0) return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: matrix not 16-byte aligned");
+  }
+  const bool layered = kind >= NRQ_TENSOR_ATTN_NORM && kind <= NRQ_TENSOR_FFN_DOWN;
+  if (layered && (layer < 0 || layer >= m->cfg.n_layers))
+    return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: layer out of range");
+  const Mat mat{dev_ptr, dtype};
+  switch (kind) {
+    case NRQ_TENSOR_TOK_EMBED:
+      if (dtype != NRQ_Q8_0) return mfail(NRQ_ERR_UNSUPPORTED, "nrq_model_set_tensor: embedding must be Q8_0");
+      m->embed = mat;
+      if (!m->output.w) m->output = mat;  // tied head until an output tensor is set
+      break;
+    case NRQ_TENSOR_OUTPUT: m->output = mat; break;
+    case NRQ_TENSOR_OUTPUT_NORM: m->out_norm = (const float*)dev_ptr; break;
+    case NRQ_TENSOR_ATTN_NORM: m->L[layer].attn_norm = (const float*)dev_ptr; break;
+    case NRQ_TENSOR_FFN_NORM: m->L[layer].ffn_norm = (const float*)dev_ptr; break;
+    case NRQ_TENSOR_ATTN_Q: m->L[layer].m[0] = mat; break;
+    case NRQ_TENSOR_ATTN_K: m->L[layer].m[1] = mat; break;
+    case NRQ_TENSOR_ATTN_V: m->L[layer].m[2] = mat; break;
+    case NRQ_TENSOR_ATTN_O: m->L[layer].m[3] = mat; break;
+    case NRQ_TENSOR_FFN_GATE: m->L[layer].m[4] = mat; break;
+    case NRQ_TENSOR_FFN_UP: m->L[layer].m[5] = mat; break;
+    case NRQ_TENSOR_FFN_DOWN: m->L[layer].m[6] = mat; break;
+    default: return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: unknown tensor kind");
+  }
+  if (m->exec) {  // tensors changed: the captured step is stale
+    hipGraphExecDestroy(m->exec);
+    hipGraphDestroy(m->graph);
+    m->exec = nullptr;
+    m->graph = nullptr;
+  }
+  return NRQ_OK;
+}
+
+int nrq_model_reset(nrq_model* m) {
+  if (!m) return mfail(NRQ_ERR_ARG, "nrq_model_reset: null handle");
+  MHIP(hipStreamSynchronize(m->stream));
+  MHIP(hipMemset(m->ctl, 0, nrq::CTL_WORDS * 4));
+  m->host_pos = 0;
+  return NRQ_OK;
+}
+
+int nrq_model_pos(const nrq_model* m) { return m ? m->host_pos : -1; }
+
+int nrq_model_forward(nrq_model* m, uint32_t token, float* logits_host) {
+  int rc = check_ready(m, "nrq_model_forward");
+  if (rc) return rc;
+  // infer.rs:513: assert!(pos < d.ctx, "context window exhausted")
+  if (m->host_pos >= m->cfg.ctx) return mfail(NRQ_ERR_SHAPE, "assertion failed: pos < d.ctx: context window exhausted");
+  if (token >= (uint32_t)m->cfg.vocab) return mfail(NRQ_ERR_ARG, "nrq_model_forward: token out of vocabulary");
+  const int tok = (int)token;
+  MHIP(hipMemcpyAsync(m->ctl + nrq::CTL_TOKEN, &tok, 4, hipMemcpyHostToDevice, m->stream));
+  uint32_t* keep = m->out_tokens;
+  m->out_tokens = nullptr;
+  rc = enqueue_step(m);
+  m->out_tokens = keep;
+  if (rc) return rc;
+  if (logits_host)
+    MHIP(hipMemcpyAsync(logits_host, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost, m->stream));
+  MHIP(hipStreamSynchronize(m->stream));
+  m->host_pos += 1;
+  return NRQ_OK;
+}
+
+int nrq_model_generate(nrq_model* m, uint32_t token, int n, uint32_t* out_tokens, float* last_logits) {
+  int rc = check_ready(m, "nrq_model_generate");
+  if (rc) return rc;
+  if (n <= 0) return NRQ_OK;
+  if (!out_tokens) return mfail(NRQ_ERR_ARG, "nrq_model_generate: null output");
+  if (m->host_pos + n > m->cfg.ctx) return mfail(NRQ_ERR_SHAPE, "assertion failed: pos < d.ctx: context window exhausted");
+  if (token >= (uint32_t)m->cfg.vocab) return mfail(NRQ_ERR_ARG, "nrq_model_generate: token out of vocabulary");
+  if (n > m->max_out) {
+    if (m->out_tokens) hipFree(m->out_tokens);
+    m->out_tokens = nullptr;
+    m->max_out = 0;
+    MHIP(hipMalloc(&m->out_tokens, (size_t)n * 4));
+    m->max_out = n;
+    if (m->exec) {  // the captured step points at the old buffer
+      hipGraphExecDestroy(m->exec);
+      hipGraphDestroy(m->graph);
+      m->exec = nullptr;
+      m->graph = nullptr;
+    }
+  }
+  const int tok = (int)token;
+  MHIP(hipMemcpyAsync(m->ctl + nrq::CTL_TOKEN, &tok, 4, hipMemcpyHostToDevice, m->stream));
+  const int zero = 0;
+  MHIP(hipMemcpyAsync(m->ctl + nrq::CTL_STEP, &zero, 4, hipMemcpyHostToDevice, m->stream));
+  if (!m->exec) {
+    MHIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    rc = enqueue_step(m);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(m->stream, &g);
+    if (rc) {
+      if (g) hipGraphDestroy(g);
+      return rc;
+    }
+    if (e != hipSuccess) return mfail(NRQ_ERR_DEVICE, "nrq_model_generate: graph capture failed");
+    hipGraphExec_t x = nullptr;
+    if (hipGraphInstantiate(&x, g, nullptr, nullptr, 0) != hipSuccess) {
+      hipGraphDestroy(g);
+      return mfail(NRQ_ERR_DEVICE, "nrq_model_generate: graph instantiate failed");
+    }
+    m->graph = g;
+    m->exec = x;
+  }
+  for (int i = 0; i < n; i++) MHIP(hipGraphLaunch(m->exec, m->stream));
+  MHIP(hipMemcpyAsync(out_tokens, m->out_tokens, (size_t)n * 4, hipMemcpyDeviceToHost, m->stream));
+  if (last_logits)
+    MHIP(hipMemcpyAsync(last_logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost, m->stream));
+  MHIP(hipStreamSynchronize(m->stream));
+  m->host_pos += n;
+  return NRQ_OK;
+}
+
+int nrq_model_kv_cache(nrq_model* m, void* k_host, void* v_host, size_t bytes) {
+  if (!m) return mfail(NRQ_ERR_ARG, "nrq_model_kv_cache: null handle");
+  const size_t kvb = (size_t)m->cfg.n_layers * m->cfg.ctx * m->kv_dim * 2;
+  if (bytes != kvb) return mfail(NRQ_ERR_SHAPE, "nrq_model_kv_cache: size mismatch");
+  MHIP(hipStreamSynchronize(m->stream));
+  if (k_host) MHIP(hipMemcpy(k_host, m->kc, kvb, hipMemcpyDeviceToHost));
+  if (v_host) MHIP(hipMemcpy(v_host, m->vc, kvb, hipMemcpyDeviceToHost));
+  return NRQ_OK;
+}
+
+int nrq_dev_mathf(int fn, const float* x, float* y, size_t n, void* stream) {
+  if (fn < 0 || fn > 2) return mfail(NRQ_ERR_ARG, "nrq_dev_mathf: unknown function");
+  if (n == 0) return NRQ_OK;
+  if (!x || !y) return mfail(NRQ_ERR_ARG, "nrq_dev_mathf: null pointer");
+  hipLaunchKernelGGL(nrq::mathf_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, fn, x, y,
+                     (long long)n);
+  return hipGetLastError() == hipSuccess ? NRQ_OK : mfail(NRQ_ERR_DEVICE, "nrq_dev_mathf: launch failed");
+}
+
+int nrq_model_destroy(nrq_model* m) {
+  if (!m) return NRQ_OK;
+  if (m->stream) hipStreamSynchronize(m->stream);
+  if (m->exec) hipGraphExecDestroy(m->exec);
+  if (m->graph) hipGraphDestroy(m->graph);
+  void* bufs[] = {m->freqs, m->kc, m->vc, m->x, m->xb, m->q, m->k, m->v, m->attn, m->gate, m->up, m->xb2,
+                  m->logits, m->xq, m->xq2, m->ctl, m->out_tokens};
+  for (void* p : bufs)
+    if (p) hipFree(p);
+  if (m->stream) hipStreamDestroy(m->stream);
+  delete m;
+  return NRQ_OK;
+}
+
+}  // extern "C"

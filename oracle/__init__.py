@@ -254,3 +254,183 @@ def gen_weights(dtype: int, seed: int, rows: int, cols: int) -> np.ndarray:
     out = np.zeros((nb, WBYTES[dtype]), dtype=np.uint8)
     lib().nro_gen_weights(dtype, seed, _p(out), nb)
     return out
+
+
+# ---- forward pass (nrq_model_oracle.c) -------------------------------------------
+
+_model_sigs_done = False
+
+
+def _model_lib():
+    global _model_sigs_done
+    L = lib()
+    if not _model_sigs_done:
+        vp, sz, f32p = C.c_void_p, C.c_size_t, C.POINTER(C.c_float)
+        L.nro_expf.argtypes, L.nro_expf.restype = [C.c_float], C.c_float
+        L.nro_sincosf.argtypes = [C.c_float, f32p, f32p]
+        L.nro_expf_n.argtypes = [vp, vp, sz]
+        L.nro_sincosf_n.argtypes = [vp, vp, vp, sz]
+        L.nro_rmsnorm.argtypes = [vp, vp, vp, sz, C.c_float]
+        L.nro_softmax.argtypes = [vp, sz]
+        L.nro_swiglu.argtypes = [vp, vp, sz]
+        L.nro_argmax.argtypes, L.nro_argmax.restype = [vp, sz], C.c_uint32
+        L.nro_rope_freqs.argtypes = [vp, sz, C.c_float]
+        L.nro_rope_apply.argtypes = [vp, sz, sz, vp, sz]
+        L.nro_model_new.argtypes, L.nro_model_new.restype = [C.POINTER(C.c_int), C.c_float, C.c_float, C.c_int], vp
+        L.nro_model_free.argtypes = [vp]
+        L.nro_model_set_globals.argtypes = [vp, vp, C.c_int, vp, C.c_int, vp]
+        L.nro_model_set_layer.argtypes = [vp, C.c_int, C.POINTER(vp), C.POINTER(C.c_int), vp, vp]
+        L.nro_model_forward.argtypes, L.nro_model_forward.restype = [vp, C.c_uint32], f32p
+        L.nro_model_prefill_chunk.argtypes, L.nro_model_prefill_chunk.restype = [vp, C.POINTER(C.c_uint32), C.c_int], f32p
+        L.nro_model_pos.argtypes, L.nro_model_pos.restype = [vp], C.c_int
+        L.nro_model_reset.argtypes = [vp]
+        L.nro_model_kcache.argtypes, L.nro_model_kcache.restype = [vp], C.POINTER(C.c_uint16)
+        L.nro_model_vcache.argtypes, L.nro_model_vcache.restype = [vp], C.POINTER(C.c_uint16)
+        _model_sigs_done = True
+    return L
+
+
+def expf(x: float) -> float:
+    return _model_lib().nro_expf(x)
+
+
+def expf_array(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    y = np.empty_like(x)
+    _model_lib().nro_expf_n(_p(x), _p(y), x.size)
+    return y
+
+
+def sincosf_array(x: np.ndarray):
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    s, c = np.empty_like(x), np.empty_like(x)
+    _model_lib().nro_sincosf_n(_p(x), _p(s), _p(c), x.size)
+    return s, c
+
+
+def sincosf(x: float):
+    s, c = C.c_float(), C.c_float()
+    _model_lib().nro_sincosf(x, C.byref(s), C.byref(c))
+    return s.value, c.value
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.zeros_like(x)
+    _model_lib().nro_rmsnorm(_p(out), _p(x), _p(w), x.size, eps)
+    return out
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    x = np.array(x, dtype=np.float32)
+    _model_lib().nro_softmax(_p(x), x.size)
+    return x
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    g = np.array(gate, dtype=np.float32)
+    u = np.ascontiguousarray(up, np.float32)
+    _model_lib().nro_swiglu(_p(g), _p(u), g.size)
+    return g
+
+
+def argmax(x: np.ndarray) -> int:
+    x = np.ascontiguousarray(x, np.float32)
+    return _model_lib().nro_argmax(_p(x), x.size)
+
+
+def rope_freqs(head_dim: int, theta: float) -> np.ndarray:
+    out = np.zeros(head_dim // 2, np.float32)
+    _model_lib().nro_rope_freqs(_p(out), head_dim, theta)
+    return out
+
+
+def rope_apply(x: np.ndarray, head_dim: int, freqs: np.ndarray, pos: int) -> np.ndarray:
+    x = np.array(x, dtype=np.float32)
+    f = np.ascontiguousarray(freqs, np.float32)
+    _model_lib().nro_rope_apply(_p(x), x.size, head_dim, _p(f), pos)
+    return x
+
+
+# Llama-3.2-1B architecture (the full-model benchmark shape)
+LLAMA_1B = dict(dim=2048, n_layers=16, n_heads=32, n_kv_heads=8, head_dim=64, ffn_dim=8192, vocab=128256,
+                norm_eps=1e-5, rope_theta=500000.0)
+# tensor order of a layer's matrices
+LAYER_MATS = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
+
+
+def layer_shapes(cfg: dict):
+    d, hd = cfg["dim"], cfg["head_dim"]
+    att, kv, ffn = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd, cfg["ffn_dim"]
+    return {"wq": (att, d), "wk": (kv, d), "wv": (kv, d), "wo": (d, att), "w_gate": (ffn, d), "w_up": (ffn, d),
+            "w_down": (d, ffn)}
+
+
+def gen_model(cfg: dict, seed: int, dtype: int = Q8_0) -> dict:
+    """Random-init weights of the given architecture: every matrix with the
+    synthetic generator of its dtype (distinct seed per tensor), RMSNorm
+    weights 1.0, output head tied to the embedding."""
+    w = {"embed": gen_weights(dtype, seed, cfg["vocab"], cfg["dim"]), "embed_dtype": dtype,
+         "out_norm": np.ones(cfg["dim"], np.float32), "layers": []}
+    shapes = layer_shapes(cfg)
+    for l in range(cfg["n_layers"]):
+        lw = {"attn_norm": np.ones(cfg["dim"], np.float32), "ffn_norm": np.ones(cfg["dim"], np.float32),
+              "dtypes": {}}
+        for i, name in enumerate(LAYER_MATS):
+            rows, cols = shapes[name]
+            lw[name] = gen_weights(dtype, seed + 1 + 16 * l + i, rows, cols)
+            lw["dtypes"][name] = dtype
+        w["layers"].append(lw)
+    return w
+
+
+class Model:
+    """InferCtx restated on the CPU (scalar f32 order throughout)."""
+
+    def __init__(self, cfg: dict, weights: dict, ctx: int, threads: int = 1):
+        L = _model_lib()
+        dims = (C.c_int * 8)(cfg["dim"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"],
+                             cfg["ffn_dim"], cfg["vocab"], ctx)
+        self.cfg, self.w, self.ctx = cfg, weights, ctx
+        self.h = L.nro_model_new(dims, cfg["norm_eps"], cfg["rope_theta"], threads)
+        L.nro_model_set_globals(self.h, _p(weights["embed"]), weights["embed_dtype"], _p(weights["embed"]),
+                                weights["embed_dtype"], _p(weights["out_norm"]))
+        for l, lw in enumerate(weights["layers"]):
+            ptrs = (C.c_void_p * 7)(*[lw[n].ctypes.data for n in LAYER_MATS])
+            dts = (C.c_int * 7)(*[lw["dtypes"][n] for n in LAYER_MATS])
+            L.nro_model_set_layer(self.h, l, ptrs, dts, _p(lw["attn_norm"]), _p(lw["ffn_norm"]))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _model_lib().nro_model_free(self.h)
+            self.h = None
+
+    @property
+    def pos(self) -> int:
+        return _model_lib().nro_model_pos(self.h)
+
+    def forward(self, token: int) -> np.ndarray:
+        p = _model_lib().nro_model_forward(self.h, token)
+        return np.ctypeslib.as_array(p, shape=(self.cfg["vocab"],)).copy()
+
+    def prefill_chunk(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, np.uint32)
+        assert 1 <= t.size <= 64
+        p = _model_lib().nro_model_prefill_chunk(self.h, t.ctypes.data_as(C.POINTER(C.c_uint32)), t.size)
+        return np.ctypeslib.as_array(p, shape=(self.cfg["vocab"],)).copy()
+
+    def prefill(self, tokens) -> np.ndarray:
+        """InferCtx::prefill (infer.rs:753-759): chunks of MAX_BATCH = 64."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        out = None
+        for i in range(0, t.size, 64):
+            out = self.prefill_chunk(t[i:i + 64])
+        return out
+
+    def kv_cache(self):
+        L = _model_lib()
+        n = self.cfg["n_layers"] * self.ctx * self.cfg["n_kv_heads"] * self.cfg["head_dim"]
+        k = np.ctypeslib.as_array(L.nro_model_kcache(self.h), shape=(n,)).copy()
+        v = np.ctypeslib.as_array(L.nro_model_vcache(self.h), shape=(n,)).copy()
+        return k, v

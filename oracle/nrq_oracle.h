@@ -117,6 +117,40 @@ void nro_rng_bytes(uint64_t *state, uint8_t *out, size_t n);
  */
 void nro_gen_weights(int dtype, uint64_t seed, void *out, size_t nblocks);
 
+/* ---- forward pass (nrq_model_oracle.c) ----------------------------------------- */
+
+/* libm restatements (musl algorithms the reference's libm crate ports) */
+float nro_expf(float x);
+void nro_sincosf(float x, float *s, float *c);
+void nro_expf_n(const float *x, float *y, size_t n);
+void nro_sincosf_n(const float *x, float *s, float *c, size_t n);
+/* crates/nr-tensor/src/vec.rs:4-14, 30-42, 45-52, 80-90 */
+void nro_rmsnorm(float *out, const float *x, const float *w, size_t n, float eps);
+void nro_softmax(float *x, size_t n);
+void nro_swiglu(float *gate, const float *up, size_t n);
+uint32_t nro_argmax(const float *x, size_t n);
+/* crates/nr-tensor/src/rope.rs:14-34 (no scaling), 49-65 (adjacent pairs) */
+void nro_rope_freqs(float *out, size_t head_dim, float theta);
+void nro_rope_apply(float *x, size_t n, size_t head_dim, const float *freqs, size_t pos);
+
+/* InferCtx (crates/nr-model/src/infer.rs) for the Llama recipe.
+ * dims = {dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, vocab, ctx};
+ * weights w[7] = {q, k, v, o, gate, up, down} with their dtype ids. */
+typedef struct nro_model nro_model;
+nro_model *nro_model_new(const int dims[8], float eps, float theta, int threads);
+void nro_model_free(nro_model *m);
+void nro_model_set_globals(nro_model *m, const void *embed, int embed_dt, const void *output, int output_dt,
+                           const float *out_norm);
+void nro_model_set_layer(nro_model *m, int l, const void *const w[7], const int dt[7], const float *attn_norm,
+                         const float *ffn_norm);
+const float *nro_model_forward(nro_model *m, uint32_t token);                        /* infer.rs:510-595 */
+const float *nro_model_prefill_chunk(nro_model *m, const uint32_t *tokens, int n);   /* infer.rs:601-750 */
+int nro_model_pos(const nro_model *m);
+void nro_model_reset(nro_model *m);
+const float *nro_model_logits(const nro_model *m);
+const uint16_t *nro_model_kcache(const nro_model *m);
+const uint16_t *nro_model_vcache(const nro_model *m);
+
 #ifdef __cplusplus
 }
 #endif

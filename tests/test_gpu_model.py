@@ -1,0 +1,168 @@
+"""GPU parity of the device-resident Llama-family decode (nrq_model_*) and of
+its math functions against the CPU oracle's restatement of
+crates/nr-model/src/infer.rs, bit for bit.
+
+The full-size case is the Llama-3.2-1B architecture, all Q8_0, random init
+(16 layers, hidden 2048, 32 query / 8 KV heads of 64, SwiGLU 8192, tied
+128256-token head, RMSNorm eps 1e-5, adjacent RoPE theta 500000, norms 1.0):
+the KV cache is filled with 1024 seeded random token ids, then 128 tokens are
+generated greedily; the tokens, the last logits and the f16 KV cache must be
+identical to the oracle's.
+"""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+THREADS = min(16, os.cpu_count() or 1)
+TINY = dict(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=1000, norm_eps=1e-5,
+            rope_theta=500000.0)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def assert_bitwise(got, want, what=""):
+    g, w = bits(got), bits(want)
+    if not np.array_equal(g, w):
+        bad = np.nonzero(g != w)[0]
+        i = bad[0]
+        raise AssertionError(f"{what}: {bad.size} of {g.size} differ; first at {i}: "
+                             f"{g[i:i + 1].view(np.float32)} vs {w[i:i + 1].view(np.float32)}")
+
+
+def math_inputs():
+    rng = np.random.default_rng(11)
+    xs = [rng.uniform(-110, 95, 400000), rng.uniform(-3, 3, 200000), rng.uniform(-1e-3, 1e-3, 50000),
+          rng.uniform(-1200, 1200, 300000),
+          np.array([0.0, -0.0, 1e-45, -1e-45, 1e-38, 88.72283, 88.7229, -87.33655, -103.97208, -104.0, 1e30, -1e30,
+                    np.inf, -np.inf, np.nan, 0.5 * np.log(2), 1.5 * np.log(2), np.pi / 4, 3 * np.pi / 4,
+                    5 * np.pi / 4, 7 * np.pi / 4, 9 * np.pi / 4])]
+    return np.concatenate(xs).astype(np.float32)
+
+
+def test_device_expf_sincosf_bitexact(gpu, oracle):
+    """The device restatements of expf and sincosf return the oracle's bits
+    on ~1M inputs: the range softmax/swiglu/rope use, extremes, the branch
+    boundaries, zeros, subnormals, inf and NaN."""
+    import torch
+
+    from nightrun_amd import model
+
+    x = math_inputs()
+    xd = torch.from_numpy(x).cuda()
+    e = model.mathf(0, xd).cpu().numpy()
+    s = model.mathf(1, xd).cpu().numpy()
+    c = model.mathf(2, xd).cpu().numpy()
+    we = oracle.expf_array(x)
+    ws, wc = oracle.sincosf_array(x)
+    for got, want, name in ((e, we, "expf"), (s, ws, "sin"), (c, wc, "cos")):
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan), name
+        assert_bitwise(got[~nan], want[~nan], name)
+
+
+def run_pair(oracle, cfg, weights, ctx, prompt, n_gen, check_kv=True):
+    """Feeds `prompt` then generates n_gen tokens greedily on both sides.
+    The GPU takes the prompt one forward step at a time, the oracle in
+    64-token prefill chunks (bitwise equal by the reference's prefill
+    invariant, crates/nr-model/tests/prefill.rs)."""
+    from nightrun_amd.model import Model
+
+    ref = oracle.Model(cfg, weights, ctx=ctx, threads=THREADS)
+    want_logits = ref.prefill(prompt)
+    tok = oracle.argmax(want_logits)
+    want_tokens = []
+    for _ in range(n_gen):
+        want_tokens.append(tok)
+        want_logits = ref.forward(tok)
+        tok = oracle.argmax(want_logits)
+    want_tokens.append(tok)
+
+    m = Model(cfg, ctx)
+    try:
+        m.set_weights(weights)
+        for i, t in enumerate(prompt):
+            lg = m.forward(int(t), logits=(i == len(prompt) - 1))
+        first = int(np.argmax(lg)) if lg is not None else None
+        # the first generated token comes from the prompt's last logits
+        assert first == want_tokens[0], (first, want_tokens[0])
+        got_tokens, last = m.generate(first, n_gen, logits=True)
+        assert m.pos == len(prompt) + n_gen
+        assert [first] + list(got_tokens) == want_tokens, "greedy tokens differ"
+        assert_bitwise(last, want_logits, "last logits")
+        if check_kv:
+            k, v = m.kv_cache()
+            rk, rv = ref.kv_cache()
+            assert np.array_equal(k, rk) and np.array_equal(v, rv), "KV cache differs"
+    finally:
+        m.close()
+
+
+def test_tiny_model_forward_and_generate(gpu, oracle):
+    """2 layers, GQA 4:2, 70 prompt tokens across a 64-token chunk boundary,
+    20 greedy steps, all Q8_0."""
+    w = oracle.gen_model(TINY, 1234)
+    prompt = np.random.default_rng(1).integers(0, TINY["vocab"], 70).astype(np.uint32)
+    run_pair(oracle, TINY, w, 128, prompt, 20)
+
+
+def test_tiny_model_logits_every_step(gpu, oracle):
+    """Logits of every forward step equal the oracle's (not only the argmax)."""
+    from nightrun_amd.model import Model
+
+    w = oracle.gen_model(TINY, 99)
+    ref = oracle.Model(TINY, w, ctx=64, threads=THREADS)
+    m = Model(TINY, 64)
+    try:
+        m.set_weights(w)
+        for i, t in enumerate(np.random.default_rng(3).integers(0, TINY["vocab"], 40)):
+            assert_bitwise(m.forward(int(t)), ref.forward(int(t)), f"step {i}")
+    finally:
+        m.close()
+
+
+def test_tiny_model_kquant_weights(gpu, oracle):
+    """Q4_K attention/gate/up and Q6_K down weights (Q8_K activations), Q8_0
+    embedding and head: the Qwen3 / Granite Q4_K_M weight mix on the Llama
+    recipe."""
+    w = oracle.gen_model(TINY, 4321)
+    shapes = oracle.layer_shapes(TINY)
+    for l, lw in enumerate(w["layers"]):
+        for i, name in enumerate(oracle.LAYER_MATS):
+            dt = 3 if name == "w_down" else 2
+            rows, cols = shapes[name]
+            lw[name] = oracle.gen_weights(dt, 777 + 16 * l + i, rows, cols)
+            lw["dtypes"][name] = dt
+    prompt = np.random.default_rng(2).integers(0, TINY["vocab"], 9).astype(np.uint32)
+    run_pair(oracle, TINY, w, 64, prompt, 12)
+
+
+def test_context_exhausted_panics(gpu, oracle):
+    """infer.rs:513: forward past the context asserts."""
+    from nightrun_amd import NrPanic
+    from nightrun_amd.model import Model
+
+    w = oracle.gen_model(TINY, 5)
+    m = Model(TINY, 3)
+    try:
+        m.set_weights(w)
+        for t in (1, 2, 3):
+            m.forward(t, logits=False)
+        with pytest.raises(NrPanic, match="context window exhausted"):
+            m.forward(4, logits=False)
+    finally:
+        m.close()
+
+
+def test_llama_1b_greedy_token_identical(gpu, oracle):
+    """The full-model benchmark: Llama-3.2-1B architecture, all Q8_0, KV
+    filled to 1024 positions, 128 greedy tokens identical to the oracle's,
+    with the same last logits and KV cache."""
+    cfg = oracle.LLAMA_1B
+    w = oracle.gen_model(cfg, 0x5EED0005)
+    prompt = np.random.default_rng(0x5EED0005).integers(0, cfg["vocab"], 1024).astype(np.uint32)
+    run_pair(oracle, cfg, w, 1152, prompt, 128)
