@@ -1,19 +1,26 @@
-"""Benchmark of the quantized decode matvec on one MI355X.
+"""Benchmark of NightRun's quantized matrix path on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--config cfg2] [--order scalar|avx2]
+                    [--no-decode] [--no-prefill] [--no-cpu-baseline]
 
-A step is one decode matvec (one kernel launch) over one weight matrix whose
-bytes are already resident in HBM. Steps rotate over enough distinct copies
-of the weights (> 512 MiB in total) that the 256 MiB MALL cannot serve them,
-so every step streams its weights from HBM. The default workload is the
-Q4_K matvec 8192 x 3072 (Llama-3.2-3B FFN shape) against a runtime-quantized
-Q8_K activation.
+Headline (`value`): the decode matvec of the Q4_K 8192 x 3072 matrix
+(Llama-3.2-3B FFN shape) against a runtime-quantized Q8_K activation. A step
+is one matvec launch over weights already resident in HBM; the K timed steps
+run back to back as one captured HIP graph and rotate over more than 512 MiB
+of weight copies, so the 256 MiB MALL cannot serve them. `value` is
+algorithmic bytes x K / the graph's wall time (HIP events on the launch
+stream); `roofline.achieved` is algorithmic bytes / the mean time per launch
+inside that graph.
 
-Prints one JSON line: `value` is the whole-job weight-streaming throughput
-(algorithmic bytes of all K steps / wall time of the timed region);
-`roofline` gives the kernel's own bandwidth from per-launch HIP events;
-`cpu_baseline` times the CPU oracle's restatement of the reference's AVX2
-kernel on a bounded sample of the same workload on the host cores.
+Beside it, in the same JSON line:
+  other_configs  the Q8_0 8192x2048 and Q6_K 128256x3072 matvecs, same method
+  prefill        one Qwen3-4B layer's seven matmuls at M = 64 tokens (int8 MFMA)
+  decode         greedy tokens/s of a Llama-3.2-1B-shape Q8_0 model (random
+                 init) with the KV cache filled to 1024 positions, each step one
+                 HIP graph replay (nrq_model_generate)
+  cpu_baseline   the CPU oracle's AVX2 restatement of the matvec, and its
+                 scalar-order restatement of the full decode step, timed on a
+                 bounded sample on the host cores
 """
 from __future__ import annotations
 
@@ -29,7 +36,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "Q-matvec HBM GB/s (% of peak); decode tok/s, Llama-3.2-1B-shape Q8_0"
-HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor peak
+HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, vendor peak
+INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, vendor peak
 MALL_BYTES = 256 << 20
 
 # name -> (dtype, rows, cols, seed, description)
@@ -41,6 +49,11 @@ CONFIGS = {
 WBYTES = {1: 34, 2: 144, 3: 210}
 XBYTES = {1: 34, 2: 292, 3: 292}
 QK = {1: 32, 2: 256, 3: 256}
+# Qwen3-4B layer: hidden 2560, attention 4096, ffn 9728, KV width 1024 (8 heads x 128)
+QWEN3_4B_LAYER = [("wq", 2, 4096, 2560), ("wk", 2, 1024, 2560), ("wv", 2, 1024, 2560), ("wo", 2, 2560, 4096),
+                  ("w_gate", 2, 9728, 2560), ("w_up", 2, 9728, 2560), ("w_down", 3, 2560, 9728)]
+LLAMA_1B = dict(dim=2048, n_layers=16, n_heads=32, n_kv_heads=8, head_dim=64, ffn_dim=8192, vocab=128256,
+                norm_eps=1e-5, rope_theta=500000.0)
 
 
 def synth_weights(dtype, rows, cols, seed):
@@ -66,13 +79,39 @@ def synth_weights(dtype, rows, cols, seed):
     return w
 
 
-def algorithmic_bytes(dtype, rows, cols):
-    """Weights + quantized activation + f32 output, each touched once."""
+def algorithmic_bytes(dtype, rows, cols, batch=1):
+    """Weights + quantized activations + f32 outputs, each touched once."""
     bpr = cols // QK[dtype]
-    return rows * bpr * WBYTES[dtype] + bpr * XBYTES[dtype] + rows * 4
+    return rows * bpr * WBYTES[dtype] + batch * bpr * XBYTES[dtype] + batch * rows * 4
 
 
-def measure_gpu(name, steps, warmup, order):
+def graph_time(stream, launch, k):
+    """Captures k launches (launch(i)) into one HIP graph, replays it once
+    untimed, then times one replay with HIP events on `stream`. Returns
+    (seconds per replay, seconds per launch)."""
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        g.capture_begin()
+        for i in range(k):
+            launch(i)
+        g.capture_end()
+    with torch.cuda.stream(stream):  # replay() launches on the current stream
+        g.replay()
+    stream.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        a.record(stream)
+        g.replay()
+        b.record(stream)
+    b.synchronize()
+    s = a.elapsed_time(b) / 1e3
+    del g
+    return s, s / k
+
+
+def measure_matvec(name, steps, warmup, order):
     import torch
 
     import nightrun_amd
@@ -82,8 +121,7 @@ def measure_gpu(name, steps, warmup, order):
     nightrun_amd.init(0)
     w = synth_weights(dtype, rows, cols, seed)
     xf = np.random.default_rng(seed + 1).normal(0, 1, cols).astype(np.float32)
-    wbytes = w.nbytes
-    copies = max(2, -(-(2 * MALL_BYTES) // wbytes))
+    copies = max(2, -(-(2 * MALL_BYTES) // w.nbytes))
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         w0 = torch.from_numpy(w).cuda()
@@ -101,50 +139,134 @@ def measure_gpu(name, steps, warmup, order):
     for i in range(warmup):
         step(i)
     stream.synchronize()
-    # whole-job throughput: K launches back to back
-    t0 = time.perf_counter()
-    for i in range(steps):
-        step(i)
-    stream.synchronize()
-    wall = time.perf_counter() - t0
-    # per-launch kernel time: HIP events on the launch stream around each launch
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for i in range(steps):
-        ev[i][0].record(stream)
-        step(i)
-        ev[i][1].record(stream)
-    stream.synchronize()
-    kern_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
-    # quantizer cost (activation f32 -> Q8_0/Q8_K), reported beside
+    wall, per = graph_time(stream, step, steps)
+    nbytes = algorithmic_bytes(dtype, rows, cols)
+    # the activation quantizer, reported beside
     q0, q1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     q0.record(stream)
     for _ in range(20):
         (device.quantize_q8_0 if dtype == 1 else device.quantize_q8k)(xd, xq, stream=stream)
     q1.record(stream)
     stream.synchronize()
-    quant_us = q0.elapsed_time(q1) / 20 * 1e3
-    nbytes = algorithmic_bytes(dtype, rows, cols)
-    return {
-        "name": name,
-        "bytes": nbytes,
-        "copies": copies,
-        "wall_s": wall,
-        "ms_per_step": wall / steps * 1e3,
-        "value_gbs": nbytes * steps / wall / 1e9,
-        "kernel_us": kern_ms * 1e3,
-        "kernel_gbs": nbytes / (kern_ms * 1e-3) / 1e9,
-        "quant_us": quant_us,
-    }
+    out = {"bytes": nbytes, "copies": copies, "wall_s": wall, "ms_per_step": wall / steps * 1e3,
+           "value_gbs": nbytes * steps / wall / 1e9, "kernel_us": per * 1e6, "kernel_gbs": nbytes / per / 1e9,
+           "quant_us": q0.elapsed_time(q1) / 20 * 1e3}
+    del ws, w0
+    torch.cuda.empty_cache()
+    return out
 
 
-def cpu_baseline(name, seconds=10.0):
-    """The oracle's AVX2 restatement (the reference's timed host path) with a
-    parallel.rs-style row pool over all usable host cores, on a bounded number
-    of full matvecs of the same workload, weights rotated beyond the LLC."""
+def measure_prefill(reps=3):
+    """One Qwen3-4B layer's seven matmuls at M = 64 (Q8_K activations), as one
+    graph of `reps` layers over rotating weight copies."""
+    import torch
+
+    import nightrun_amd
+    from nightrun_amd import device
+
+    nightrun_amd.init(0)
+    stream = torch.cuda.Stream()
+    mats, tot_bytes, tot_ops = [], 0, 0.0
+    copies = 4  # 4 x 73 MB per layer > MALL
+    with torch.cuda.stream(stream):
+        for j, (name, dt, rows, cols) in enumerate(QWEN3_4B_LAYER):
+            w = torch.from_numpy(synth_weights(dt, rows, cols, 0x5EED0004 + j)).cuda()
+            ws = [w] + [w.clone() for _ in range(copies - 1)]
+            xf = torch.from_numpy(np.random.default_rng(40 + j).normal(0, 1, 64 * cols).astype(np.float32)).cuda()
+            xq = torch.empty(64 * cols // 256 * 292, dtype=torch.uint8, device="cuda")
+            device.quantize_q8k(xf, xq, stream=stream)
+            y = torch.empty(64 * rows, dtype=torch.float32, device="cuda")
+            mats.append((dt, rows, cols, ws, xq, y))
+            tot_bytes += algorithmic_bytes(dt, rows, cols, 64)
+            tot_ops += 2.0 * 64 * rows * cols
+    stream.synchronize()
+
+    def layer(i):
+        for dt, rows, cols, ws, xq, y in mats:
+            device.matmul(dt, 0, y, ws[i % copies], xq, rows, cols, 64, stream=stream)
+
+    layer(0)
+    stream.synchronize()
+    wall, per = graph_time(stream, layer, reps)
+    del mats
+    torch.cuda.empty_cache()
+    return {"workload": "Qwen3-4B layer at M=64: Q/K/V/O/gate/up Q4_K, down Q6_K (hidden 2560, attention 4096, "
+                        "KV 1024, ffn 9728), per-row Q8_K activations",
+            "us_per_layer": round(per * 1e6, 2), "tok_s_36_layers": round(64 / (36 * per), 1),
+            "gbs": round(tot_bytes / per / 1e9, 1), "int8_tops": round(tot_ops / per / 1e12, 2),
+            "mfma_frac_of_int8_peak": round(tot_ops / per / 1e12 / INT8_PEAK_TOPS, 4),
+            "algorithmic_bytes_per_layer": tot_bytes}
+
+
+def synth_model(cfg, seed):
+    """Llama-family random-init weights with the numpy generator: all Q8_0,
+    norms 1.0, head tied to the embedding."""
+    d, hd = cfg["dim"], cfg["head_dim"]
+    att, kv, ffn = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd, cfg["ffn_dim"]
+    shapes = {"wq": (att, d), "wk": (kv, d), "wv": (kv, d), "wo": (d, att), "w_gate": (ffn, d), "w_up": (ffn, d),
+              "w_down": (d, ffn)}
+    w = {"embed": synth_weights(1, cfg["vocab"], d, seed), "embed_dtype": 1, "out_norm": np.ones(d, np.float32),
+         "layers": []}
+    for l in range(cfg["n_layers"]):
+        lw = {"attn_norm": np.ones(d, np.float32), "ffn_norm": np.ones(d, np.float32), "dtypes": {}}
+        for i, (name, (rows, cols)) in enumerate(shapes.items()):
+            lw[name] = synth_weights(1, rows, cols, seed + 1 + 16 * l + i)
+            lw["dtypes"][name] = 1
+        w["layers"].append(lw)
+    return w
+
+
+def model_bytes_per_token(cfg, kv_pos):
+    d, hd = cfg["dim"], cfg["head_dim"]
+    att, kv, ffn = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd, cfg["ffn_dim"]
+    per_layer = (att * d + 2 * kv * d + d * att + 3 * ffn * d) // 32 * 34
+    head = cfg["vocab"] * d // 32 * 34
+    kv_bytes = cfg["n_layers"] * kv_pos * kv * 2 * 2
+    return cfg["n_layers"] * per_layer + head + kv_bytes
+
+
+def measure_decode(fill=1024, n=128):
+    import torch
+
+    import nightrun_amd
+    from nightrun_amd.model import Model
+
+    nightrun_amd.init(0)
+    cfg = LLAMA_1B
+    w = synth_model(cfg, 0x5EED0005)
+    m = Model(cfg, ctx=fill + n + 8)
+    m.set_weights(w)
+    del w
+    first = int(np.random.default_rng(5).integers(0, cfg["vocab"]))
+    # fill the KV cache (greedy continuation of one random token)
+    toks = m.generate(first, fill)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = m.generate(int(toks[-1]), n)
+    dt = time.perf_counter() - t0
+    m.close()
+    torch.cuda.empty_cache()
+    mid = fill + n // 2
+    return {"workload": "Llama-3.2-1B architecture, all Q8_0, random init (16 layers, hidden 2048, 32/8 heads x 64, "
+                        f"ffn 8192, tied 128256 head), f16 KV cache at positions {fill}..{fill + n - 1}, greedy",
+            "tok_s": round(n / dt, 1), "ms_per_token": round(dt / n * 1e3, 4),
+            "bytes_per_token": model_bytes_per_token(cfg, mid),
+            "gbs": round(model_bytes_per_token(cfg, mid) * n / dt / 1e9, 1), "tokens": int(n),
+            "first_tokens": [int(t) for t in out[:4]]}
+
+
+def host_cores():
+    return min(16, len(os.sched_getaffinity(0)))
+
+
+def cpu_baseline_matvec(name, seconds):
+    """The oracle's AVX2 restatement (the reference's timed x86 host path)
+    with a parallel.rs-style row pool, on full matvecs of the same workload,
+    weights rotated beyond the LLC."""
     import oracle as O
 
     dtype, rows, cols, seed, _ = CONFIGS[name]
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads = host_cores()
     w = O.gen_weights(dtype, seed, rows, cols)
     copies = max(1, min(8, -(-(256 << 20) // w.nbytes)))
     ws = [w] + [w.copy() for _ in range(copies - 1)]
@@ -156,14 +278,33 @@ def cpu_baseline(name, seconds=10.0):
         O.matvec(dtype, O.ORDER_AVX2, ws[n % copies], x, rows, cols, threads)
         n += 1
     dt = time.perf_counter() - t0
-    return {
-        "value": round(algorithmic_bytes(dtype, rows, cols) * n / dt / 1e9, 3),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"{n} full {name} matvecs (AVX2 order, {threads} threads, {copies} rotating weight copies) "
-                  f"in {dt:.1f} s",
-    }
+    return {"value": round(algorithmic_bytes(dtype, rows, cols) * n / dt / 1e9, 3), "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{n} full {name} matvecs (AVX2 order, {threads} threads, {copies} rotating weight copies) "
+                      f"in {dt:.1f} s"}
+
+
+def cpu_baseline_decode(seconds):
+    """The oracle's restatement of InferCtx::forward (scalar-order kernels,
+    parallel.rs-style pool) on the same architecture: one 64-token prefill
+    chunk, then greedy decode steps for about `seconds`."""
+    import oracle as O
+
+    threads = host_cores()
+    cfg = dict(O.LLAMA_1B)
+    w = O.gen_model(cfg, 0x5EED0005)
+    m = O.Model(cfg, w, ctx=256, threads=threads)
+    logits = m.prefill(np.random.default_rng(5).integers(0, cfg["vocab"], 64).astype(np.uint32))
+    tok = O.argmax(logits)
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds and m.pos < 256:
+        tok = O.argmax(m.forward(tok))
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} greedy decode steps at KV positions 64..{63 + n} of the Llama-3.2-1B-shape Q8_0 model "
+                      f"(scalar-order kernels, {threads} threads) in {dt:.1f} s"}
 
 
 def main():
@@ -175,18 +316,26 @@ def main():
     ap.add_argument("--order", default="scalar", choices=["scalar", "avx2"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--also", default="cfg1,cfg3", help="other matvec configs reported beside (comma list)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding of the path is design-only"}))
         sys.exit(2)
     order = 0 if args.order == "scalar" else 1
-    r = measure_gpu(args.config, args.steps, args.warmup, order)
+    r = measure_matvec(args.config, args.steps, args.warmup, order)
     others = {}
     for name in [s for s in args.also.split(",") if s and s != args.config]:
-        o = measure_gpu(name, max(20, args.steps // 4), max(5, args.warmup // 2), order)
-        others[name] = {k: round(v, 3) if isinstance(v, float) else v for k, v in o.items() if k != "name"}
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args.config, args.cpu_seconds)
+        o = measure_matvec(name, max(20, args.steps // 4), max(5, args.warmup // 2), order)
+        others[name] = {k: round(v, 3) if isinstance(v, float) else v for k, v in o.items()}
+    prefill = None if args.no_prefill else measure_prefill()
+    decode = None if args.no_decode else measure_decode()
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_matvec(args.config, args.cpu_seconds)
+        if decode is not None:
+            cpu["decode"] = cpu_baseline_decode(args.cpu_seconds)
     dtype, rows, cols, _, desc = CONFIGS[args.config]
     out = {
         "metric": METRIC,
@@ -200,13 +349,14 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded xorshift64 weights, N(0,1) activation)",
+        "data": "synthetic (seeded random weights, N(0,1) activation)",
         "config": {
             "workload": desc,
             "order": args.order,
             "rotating_weight_copies": r["copies"],
             "algorithmic_bytes_per_step": r["bytes"],
             "activation_quantize_us": round(r["quant_us"], 3),
+            "timing": "K launches captured in one HIP graph, HIP events on the launch stream",
             "parallelism": "single GPU",
         },
         "roofline": {
@@ -220,6 +370,8 @@ def main():
         },
         "cpu_baseline": cpu,
         "other_configs": others,
+        "prefill": prefill,
+        "decode": decode,
     }
     print(json.dumps(out))
 

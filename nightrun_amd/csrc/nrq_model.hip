@@ -194,6 +194,89 @@ __device__ void dev_sincosf(float x, float* sn, float* cs) {
   }
 }
 
+// Sequential f32 sum a[0] + a[1] + ... + a[n-1] from +0.0, in index order, by
+// one lane: the reference's `s += v` loops. LDS is read 32 values ahead in
+// 16-byte loads so the dependent adds do not wait on a load. a is 16-byte
+// aligned.
+__device__ float chain_sum(const float* __restrict__ a, int n) {
+  float s = 0.0f;
+  int i = 0;
+  if (n >= 64) {
+    float4 A[8], B[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) A[k] = ((const float4*)a)[k];
+    for (; i + 64 <= n; i += 32) {  // A holds a[i .. i+32)
+#pragma unroll
+      for (int k = 0; k < 8; k++) B[k] = ((const float4*)(a + i + 32))[k];
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        s = s + A[k].x;
+        s = s + A[k].y;
+        s = s + A[k].z;
+        s = s + A[k].w;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++) A[k] = B[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      s = s + A[k].x;
+      s = s + A[k].y;
+      s = s + A[k].z;
+      s = s + A[k].w;
+    }
+    i += 32;
+  }
+  for (; i < n; i++) s = s + a[i];
+  return s;
+}
+
+// s + p[0] + p[stride] + ... + p[(n-1)*stride] in order, each lane its own
+// chain (lane-consecutive p), 16 values read ahead.
+__device__ float chain_sum_strided(const float* __restrict__ p, int stride, int n, float s) {
+  int t = 0;
+  if (n >= 32) {
+    float A[16], B[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) A[k] = p[(size_t)k * stride];
+    for (; t + 32 <= n; t += 16) {  // A holds terms t .. t+16
+#pragma unroll
+      for (int k = 0; k < 16; k++) B[k] = p[(size_t)(t + 16 + k) * stride];
+#pragma unroll
+      for (int k = 0; k < 16; k++) s = s + A[k];
+#pragma unroll
+      for (int k = 0; k < 16; k++) A[k] = B[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 16; k++) s = s + A[k];
+    t += 16;
+  }
+  for (; t < n; t++) s = s + p[(size_t)t * stride];
+  return s;
+}
+
+// q8::quantize (q8.rs:27-44) of one 32-value block held one value per lane of
+// a 32-lane group: amax over the group, d = f16(amax/127), round half away,
+// clamp to [-127, 127].
+__device__ __forceinline__ void quant_q8_0_lane(float v, int lane32, uint8_t* __restrict__ blk) {
+  float amax = fabsf(v);
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+  amax = fmaxf(0.0f, amax);
+  const uint32_t d_bits = f32_to_f16_bits(amax / 127.0f);
+  const float d = f16_bits_to_f32(d_bits);
+  const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+  const float xi = v * inv;
+  const float r = xi >= 0.0f ? xi + 0.5f : xi - 0.5f;
+  int q = rust_f32_to_i32(r);
+  q = q < -127 ? -127 : (q > 127 ? 127 : q);
+  blk[2 + lane32] = (uint8_t)(int8_t)q;
+  if (lane32 == 0) {
+    blk[0] = (uint8_t)(d_bits & 0xff);
+    blk[1] = (uint8_t)(d_bits >> 8);
+  }
+}
+
 // Control words in device memory.
 enum { CTL_TOKEN = 0, CTL_POS = 1, CTL_STEP = 2, CTL_WORDS = 4 };
 
@@ -211,194 +294,237 @@ __global__ void embed_q8_0_kernel(const uint8_t* __restrict__ E, const int* __re
 }
 
 constexpr int kNormNT = 256;
+constexpr int kNormMax = 8192;
+constexpr int kNormPT = kNormMax / kNormNT;  // values per thread
 
 // Optional residual x += 1.0 * add (vec.rs:63-67, residual_scale 1), then
 // rmsnorm (vec.rs:4-14): ss += v*v in element order, scale = 1/sqrtf(ss/n + eps),
 // out = x * scale * w. Writes out (f32) and, when xq != null, its Q8_0 blocks
-// (q8.rs:27-44). One workgroup; n <= kNormMax.
-constexpr int kNormMax = 8192;
+// (q8.rs:27-44). One workgroup; n <= kNormMax, a multiple of 256. Thread t
+// owns elements t + 256k, loaded once, all loads issued before the first use.
 __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, const float* __restrict__ add,
                                                        const float* __restrict__ w, int n, float eps,
                                                        float* __restrict__ out, uint8_t* __restrict__ xq) {
-  __shared__ float sq[kNormMax];
+  __shared__ __align__(16) float sq[kNormMax];
   __shared__ float s_scale;
   const int tid = threadIdx.x;
-  for (int i = tid; i < n; i += kNormNT) {
-    float v = x[i];
-    if (add) {
-      v = v + 1.0f * add[i];
-      x[i] = v;
+  const int cnt = n / kNormNT;
+  float v[kNormPT], a[kNormPT], wv[kNormPT];
+#pragma unroll
+  for (int k = 0; k < kNormPT; k++)
+    if (k < cnt) {
+      v[k] = x[tid + kNormNT * k];
+      wv[k] = w[tid + kNormNT * k];
+      a[k] = add ? add[tid + kNormNT * k] : 0.0f;
     }
-    sq[i] = v * v;
-  }
+#pragma unroll
+  for (int k = 0; k < kNormPT; k++)
+    if (k < cnt) {
+      if (add) {
+        v[k] = v[k] + 1.0f * a[k];
+        x[tid + kNormNT * k] = v[k];
+      }
+      sq[tid + kNormNT * k] = v[k] * v[k];
+    }
   __syncthreads();
   if (tid == 0) {
-    float ss = 0.0f;
-    int i = 0;
-    for (; i + 4 <= n; i += 4) {
-      const float4 s4 = *(const float4*)(sq + i);
-      ss = ss + s4.x;
-      ss = ss + s4.y;
-      ss = ss + s4.z;
-      ss = ss + s4.w;
-    }
-    for (; i < n; i++) ss = ss + sq[i];
+    const float ss = chain_sum(sq, n);
     s_scale = 1.0f / sqrtf(ss / (float)n + eps);
   }
   __syncthreads();
   const float scale = s_scale;
-  // 32-lane groups: one Q8_0 block per group per pass
   const int lane32 = tid & 31;
-  for (int i0 = tid - lane32; i0 < n; i0 += kNormNT) {
-    const int i = i0 + lane32;
-    const float v = x[i] * scale * w[i];
-    out[i] = v;
-    if (xq) {
-      float amax = fabsf(v);
 #pragma unroll
-      for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-      amax = fmaxf(0.0f, amax);
-      const uint32_t d_bits = f32_to_f16_bits(amax / 127.0f);
-      const float d = f16_bits_to_f32(d_bits);
-      const float inv = d > 0.0f ? 1.0f / d : 0.0f;
-      const float xi = v * inv;
-      const float r = xi >= 0.0f ? xi + 0.5f : xi - 0.5f;
-      int q = rust_f32_to_i32(r);
-      q = q < -127 ? -127 : (q > 127 ? 127 : q);
-      uint8_t* blk = xq + (size_t)(i >> 5) * kQ8_0Bytes;
-      blk[2 + lane32] = (uint8_t)(int8_t)q;
-      if (lane32 == 0) {
-        blk[0] = (uint8_t)(d_bits & 0xff);
-        blk[1] = (uint8_t)(d_bits >> 8);
-      }
+  for (int k = 0; k < kNormPT; k++)
+    if (k < cnt) {
+      const int i = tid + kNormNT * k;
+      const float o = v[k] * scale * wv[k];
+      out[i] = o;
+      if (xq) quant_q8_0_lane(o, lane32, xq + (size_t)(i >> 5) * kQ8_0Bytes);
     }
-  }
-}
-
-// rope::apply on q and k at the current position (rope.rs:49-65, adjacent
-// pairs), then the KV append as f16 (infer.rs:547-551).
-__global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ q, const float* __restrict__ k,
-                                                      const float* __restrict__ v, const float* __restrict__ freqs,
-                                                      const int* __restrict__ ctl, int n_heads, int n_kv_heads,
-                                                      int hd, int ctx, int layer, uint16_t* __restrict__ kc,
-                                                      uint16_t* __restrict__ vc) {
-  const int pos = ctl[CTL_POS];
-  const int half = hd / 2, kvd = n_kv_heads * hd;
-  const size_t row = ((size_t)layer * ctx + pos) * kvd;
-  const int total = (n_heads + n_kv_heads) * half;
-  for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
-    const int head = idx / half, i = idx - head * half;
-    const float angle = (float)pos * freqs[i];
-    float s, c;
-    dev_sincosf(angle, &s, &c);
-    if (head < n_heads) {
-      float* h = q + (size_t)head * hd;
-      const float a = h[2 * i], b = h[2 * i + 1];
-      h[2 * i] = a * c - b * s;
-      h[2 * i + 1] = a * s + b * c;
-    } else {
-      const int kh = head - n_heads;
-      const float* h = k + (size_t)kh * hd;
-      const float a = h[2 * i], b = h[2 * i + 1];
-      kc[row + kh * hd + 2 * i] = (uint16_t)f32_to_f16_bits(a * c - b * s);
-      kc[row + kh * hd + 2 * i + 1] = (uint16_t)f32_to_f16_bits(a * s + b * c);
-    }
-  }
-  for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < kvd; idx += gridDim.x * blockDim.x)
-    vc[row + idx] = (uint16_t)f32_to_f16_bits(v[idx]);
 }
 
 constexpr int kAttNT = 256;
 constexpr int kAttMaxCtx = 8192;
+constexpr int kAttProd = 8192;  // floats per product stage: kAttProd / head_dim positions
 
-// One workgroup per query head (infer.rs:553-572): scores dot_f16(k_t, q) *
-// scale in dimension order (kernels.rs:146-160), softmax (vec.rs:30-42; the
-// exp-sum in position order), then out[i] += a_t * v_t[i] in position order
-// (kernels.rs:163-173).
-__global__ __launch_bounds__(kAttNT) void attention_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
-                                                           const uint16_t* __restrict__ vc,
-                                                           const int* __restrict__ ctl, int n_heads, int n_kv_heads,
-                                                           int hd, int ctx, int layer, float scale,
-                                                           float* __restrict__ out) {
-  __shared__ float att[kAttMaxCtx];
-  __shared__ float qs[256];
-  __shared__ float red[kAttNT / 64];
-  __shared__ float s_inv;
-  const int h = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int n = ctl[CTL_POS] + 1;
-  const int gqa = n_heads / n_kv_heads;
-  const int kvd = n_kv_heads * hd;
-  const size_t base = (size_t)layer * ctx * kvd + (size_t)(h / gqa) * hd;
-  for (int i = tid; i < hd; i += kAttNT) qs[i] = q[(size_t)h * hd + i];
-  __syncthreads();
-  float mx = -INFINITY;
-  for (int t = tid; t < n; t += kAttNT) {
-    const uint16_t* kr = kc + base + (size_t)t * kvd;
-    float s = 0.0f;
-    for (int i0 = 0; i0 < hd; i0 += 8) {
-      const uint4 kv8 = *(const uint4*)(kr + i0);
-      const uint32_t kw[4] = {kv8.x, kv8.y, kv8.z, kv8.w};
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        s = s + f16_bits_to_f32(kw[j] & 0xffffu) * qs[i0 + 2 * j];
-        s = s + f16_bits_to_f32(kw[j] >> 16) * qs[i0 + 2 * j + 1];
-      }
+// One workgroup per query head: the attention block of infer.rs:540-572.
+//  1. rope::apply (rope.rs:49-65) on the head's q and on its KV head's k at
+//     the current position; the KV append as f16 (infer.rs:547-551) by the
+//     first query head of each KV group. The fresh key/value are used from
+//     LDS, so the other heads of the group never read the row being written.
+//  2. scores: dot_f16(k_t, q) * scale (kernels.rs:146-160, dimension order).
+//  3. softmax (vec.rs:30-42): max, exp, the exp-sum in position order (one
+//     lane), inv, a_t = e_t * inv.
+//  4. out[i] += a_t * v_t[i] in position order (kernels.rs:163-173): the
+//     other waves form the products a_t * v_t[i] of the next chunk of
+//     positions in LDS while the chain lanes (one per dimension) add the
+//     current chunk.
+//  5. out (f32) and, when out_q8 != null, its Q8_0 blocks for the output
+//     projection.
+// LDS: att[ctx] | prod[2][kAttProd] | q[hd] | kcur[hd] | vcur[hd] | red[8]
+__global__ __launch_bounds__(kAttNT) void attention_kernel(
+    const float* __restrict__ q_in, const float* __restrict__ k_in, const float* __restrict__ v_in,
+    const float* __restrict__ freqs, const int* __restrict__ ctl, int n_heads, int n_kv_heads, int hd, int ctx,
+    int layer, float scale, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, float* __restrict__ out,
+    uint8_t* __restrict__ out_q8) {
+  extern __shared__ __align__(16) float sm[];
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int pos = ctl[CTL_POS], n = pos + 1;
+  const int gqa = n_heads / n_kv_heads, g = h / gqa, kvd = n_kv_heads * hd, half = hd / 2;
+  const bool writer = (h % gqa) == 0;
+  float* att = sm;
+  float* prod = sm + ((ctx + 3) & ~3);
+  float* qs = prod + 2 * kAttProd;
+  float* kcur = qs + hd;
+  float* vcur = kcur + hd;
+  float* red = vcur + hd;
+  const size_t row = ((size_t)layer * ctx + pos) * kvd + (size_t)g * hd;
+  const size_t base = (size_t)layer * ctx * kvd + (size_t)g * hd;
+  for (int i = tid; i < half; i += kAttNT) {
+    float sn, cs;
+    dev_sincosf((float)pos * freqs[i], &sn, &cs);
+    const float qa = q_in[(size_t)h * hd + 2 * i], qb = q_in[(size_t)h * hd + 2 * i + 1];
+    qs[2 * i] = qa * cs - qb * sn;
+    qs[2 * i + 1] = qa * sn + qb * cs;
+    const float ka = k_in[(size_t)g * hd + 2 * i], kb = k_in[(size_t)g * hd + 2 * i + 1];
+    const uint32_t k0 = f32_to_f16_bits(ka * cs - kb * sn), k1 = f32_to_f16_bits(ka * sn + kb * cs);
+    kcur[2 * i] = f16_bits_to_f32(k0);
+    kcur[2 * i + 1] = f16_bits_to_f32(k1);
+    if (writer) {
+      kc[row + 2 * i] = (uint16_t)k0;
+      kc[row + 2 * i + 1] = (uint16_t)k1;
     }
-    const float a = s * scale;
-    att[t] = a;
-    mx = fmaxf(mx, a);
   }
-  // max is order-independent (and the sign of a zero maximum cannot change
-  // any exp(v - max))
+  for (int i = tid; i < hd; i += kAttNT) {
+    const uint32_t vb = f32_to_f16_bits(v_in[(size_t)g * hd + i]);
+    vcur[i] = f16_bits_to_f32(vb);
+    if (writer) vc[row + i] = (uint16_t)vb;
+  }
+  __syncthreads();
+  // Scores: thread tid takes positions tid, tid + kAttNT, ...; the key row of
+  // its next position is loaded into registers while the current one is
+  // scored, so each iteration waits on a load issued one iteration earlier.
+  // Position `pos` uses the fresh key from LDS.
+  float mx = -INFINITY;
+  {
+    const int g8 = hd / 8;  // 16-byte pieces per key row (<= 16)
+    uint4 cur[16], nxt[16];
+    auto load_row = [&](int t, uint4* r) {
+      if (t < n && t != pos) {
+        const uint4* src = (const uint4*)(kc + base + (size_t)t * kvd);
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+          if (j < g8) r[j] = src[j];
+      }
+    };
+    load_row(tid, cur);
+    for (int t = tid; t < n; t += kAttNT) {
+      load_row(t + kAttNT, nxt);
+      float s = 0.0f;
+      if (t == pos) {
+        for (int i = 0; i < hd; i++) s = s + kcur[i] * qs[i];
+      } else {
+#pragma unroll
+        for (int p8 = 0; p8 < 16; p8++)
+          if (p8 < g8) {
+            const uint32_t kw[4] = {cur[p8].x, cur[p8].y, cur[p8].z, cur[p8].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              s = s + f16_bits_to_f32(kw[j] & 0xffffu) * qs[8 * p8 + 2 * j];
+              s = s + f16_bits_to_f32(kw[j] >> 16) * qs[8 * p8 + 2 * j + 1];
+            }
+          }
+      }
+      const float a = s * scale;
+      att[t] = a;
+      mx = fmaxf(mx, a);
+#pragma unroll
+      for (int j = 0; j < 16; j++) cur[j] = nxt[j];
+    }
+  }
+  // the max is order-independent, and the sign of a zero maximum cannot change
+  // any exp(v - max)
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
   mx = red[0];
-  for (int wv = 1; wv < kAttNT / 64; wv++) mx = fmaxf(mx, red[wv]);
+  for (int w = 1; w < kAttNT / 64; w++) mx = fmaxf(mx, red[w]);
   for (int t = tid; t < n; t += kAttNT) att[t] = dev_expf(att[t] - mx);
   __syncthreads();
-  if (tid == 0) {
-    float sum = 0.0f;
-    int t = 0;
-    for (; t + 4 <= n; t += 4) {
-      const float4 e = *(const float4*)(att + t);
-      sum = sum + e.x;
-      sum = sum + e.y;
-      sum = sum + e.z;
-      sum = sum + e.w;
-    }
-    for (; t < n; t++) sum = sum + att[t];
-    s_inv = 1.0f / sum;
-  }
+  if (tid == 0) red[4] = 1.0f / chain_sum(att, n);
   __syncthreads();
-  const float inv = s_inv;
+  const float inv = red[4];
   for (int t = tid; t < n; t += kAttNT) att[t] = att[t] * inv;
   __syncthreads();
-  for (int i = tid; i < hd; i += kAttNT) {
-    const uint16_t* vcol = vc + base + i;
-    float o = 0.0f;
-    int t = 0;
-    for (; t + 8 <= n; t += 8) {
-      float vv[8];
+  // position chunks of C; chain lanes tid < hd, the rest produce
+  const int C = kAttProd / hd, nprod = kAttNT - hd, ptid = tid - hd, g8 = hd / 8;
+  const int nchunks = (n + C - 1) / C;
+  auto produce = [&](int c) {
+    float* pb = prod + (c & 1) * kAttProd;
+    // all of this thread's value loads first, then the products
+    constexpr int kMaxPer = 8;
+    uint4 vr[kMaxPer];
 #pragma unroll
-      for (int j = 0; j < 8; j++) vv[j] = f16_bits_to_f32(vcol[(size_t)(t + j) * kvd]);
-#pragma unroll
-      for (int j = 0; j < 8; j++) o = o + att[t + j] * vv[j];
+    for (int j = 0; j < kMaxPer; j++) {
+      const int idx = ptid + nprod * j;
+      const int tl = idx / g8, i0 = (idx - tl * g8) * 8;
+      const int t = c * C + tl;
+      if (idx < C * g8 && t < n && t != pos) vr[j] = *(const uint4*)(vc + base + (size_t)t * kvd + i0);
     }
-    for (; t < n; t++) o = o + att[t] * f16_bits_to_f32(vcol[(size_t)t * kvd]);
-    out[(size_t)h * hd + i] = o;
+#pragma unroll
+    for (int j = 0; j < kMaxPer; j++) {
+      const int idx = ptid + nprod * j;
+      const int tl = idx / g8, i0 = (idx - tl * g8) * 8;
+      const int t = c * C + tl;
+      if (idx >= C * g8 || t >= n) continue;
+      const float a = att[t];
+      float vv[8];
+      if (t == pos) {
+#pragma unroll
+        for (int q = 0; q < 8; q++) vv[q] = vcur[i0 + q];
+      } else {
+        const uint32_t vw[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          vv[2 * q] = f16_bits_to_f32(vw[q] & 0xffffu);
+          vv[2 * q + 1] = f16_bits_to_f32(vw[q] >> 16);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 8; q++) pb[tl * hd + i0 + q] = a * vv[q];
+    }
+  };
+  if (tid >= hd) produce(0);
+  __syncthreads();
+  float o = 0.0f;
+  for (int c = 0; c < nchunks; c++) {
+    if (tid >= hd) {
+      if (c + 1 < nchunks) produce(c + 1);
+    } else {
+      const int cnt = min(C, n - c * C);
+      o = chain_sum_strided(prod + (c & 1) * kAttProd + tid, hd, cnt, o);
+    }
+    __syncthreads();
+  }
+  if (tid < hd) {
+    out[(size_t)h * hd + tid] = o;
+    if (out_q8) quant_q8_0_lane(o, tid & 31, out_q8 + (size_t)((h * hd + tid) >> 5) * kQ8_0Bytes);
   }
 }
 
-// vec.rs:45-52: gate = gate / (1 + expf(-gate)) * up
-__global__ void swiglu_kernel(float* __restrict__ gate, const float* __restrict__ up, int n) {
+// vec.rs:45-52: gate = gate / (1 + expf(-gate)) * up; with xq != null also its
+// Q8_0 blocks (n is a multiple of 256).
+__global__ __launch_bounds__(256) void swiglu_kernel(float* __restrict__ gate, const float* __restrict__ up, int n,
+                                                     uint8_t* __restrict__ xq) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const float g = gate[i];
   const float silu = g / (1.0f + dev_expf(-g));
-  gate[i] = silu * up[i];
+  const float v = silu * up[i];
+  gate[i] = v;
+  if (xq) quant_q8_0_lane(v, threadIdx.x & 31, xq + (size_t)(i >> 5) * kQ8_0Bytes);
 }
 
 constexpr int kArgNT = 1024;
@@ -412,13 +538,36 @@ __global__ __launch_bounds__(kArgNT) void argmax_kernel(const float* __restrict_
   const int tid = threadIdx.x;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = tid; i < n; i += kArgNT) {
-    const float v = x[i];
-    if (v > bv) {
-      bv = v;
-      bi = i;
+  // each thread scans its indices in increasing order (strict >), 4 at a time
+  const int n4 = n >> 2;
+  const float4* x4 = (const float4*)x;
+  int j = tid;
+  for (; j + 3 * kArgNT < n4; j += 4 * kArgNT) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) v[u] = x4[j + u * kArgNT];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int b = 4 * (j + u * kArgNT);
+      if (v[u].x > bv) { bv = v[u].x; bi = b; }
+      if (v[u].y > bv) { bv = v[u].y; bi = b + 1; }
+      if (v[u].z > bv) { bv = v[u].z; bi = b + 2; }
+      if (v[u].w > bv) { bv = v[u].w; bi = b + 3; }
     }
   }
+  for (; j < n4; j += kArgNT) {
+    const float4 v = x4[j];
+    const int b = 4 * j;
+    if (v.x > bv) { bv = v.x; bi = b; }
+    if (v.y > bv) { bv = v.y; bi = b + 1; }
+    if (v.z > bv) { bv = v.z; bi = b + 2; }
+    if (v.w > bv) { bv = v.w; bi = b + 3; }
+  }
+  for (int i = 4 * n4 + tid; i < n; i += kArgNT)
+    if (x[i] > bv) {
+      bv = x[i];
+      bi = i;
+    }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
     const float ov = __shfl_xor(bv, m);
@@ -515,6 +664,7 @@ struct nrq_model {
   hipGraphExec_t exec = nullptr;
   hipGraph_t graph = nullptr;
   int host_pos = 0;
+  size_t att_lds = 0;
 };
 
 namespace {
@@ -592,12 +742,14 @@ int enqueue_step(nrq_model* m) {
       const int rows[3] = {att, kvd, kvd};
       if ((rc = matvec_group(m, ws, ys, rows, 3, d))) return rc;
     }
-    hipLaunchKernelGGL(nrq::rope_kv_kernel, dim3(4), dim3(256), 0, m->stream, m->q, m->k, m->v, m->freqs, m->ctl,
-                       c.n_heads, c.n_kv_heads, c.head_dim, c.ctx, l, m->kc, m->vc);
-    hipLaunchKernelGGL(nrq::attention_kernel, dim3(c.n_heads), dim3(nrq::kAttNT), 0, m->stream, m->q, m->kc, m->vc,
-                       m->ctl, c.n_heads, c.n_kv_heads, c.head_dim, c.ctx, l, scale, m->attn);
-    if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: attention launch failed");
-    if ((rc = quantize_for(m, Ly.m[3].dt, m->attn, att, m->xq))) return rc;
+    {
+      const bool q8 = Ly.m[3].dt == NRQ_Q8_0;
+      hipLaunchKernelGGL(nrq::attention_kernel, dim3(c.n_heads), dim3(nrq::kAttNT), m->att_lds, m->stream, m->q, m->k,
+                         m->v, m->freqs, m->ctl, c.n_heads, c.n_kv_heads, c.head_dim, c.ctx, l, scale, m->kc, m->vc,
+                         m->attn, q8 ? m->xq : nullptr);
+      if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: attention launch failed");
+      if (!q8 && (rc = quantize_for(m, Ly.m[3].dt, m->attn, att, m->xq))) return rc;
+    }
     if ((rc = matvec(m, Ly.m[3], m->xq, m->xb2, d, att))) return rc;
     if ((rc = norm_quant(m, m->xb2, Ly.ffn_norm, Ly.m[4].dt))) return rc;
     {
@@ -606,8 +758,13 @@ int enqueue_step(nrq_model* m) {
       const int rows[2] = {ffn, ffn};
       if ((rc = matvec_group(m, ws, ys, rows, 2, d))) return rc;
     }
-    hipLaunchKernelGGL(nrq::swiglu_kernel, dim3((ffn + 255) / 256), dim3(256), 0, m->stream, m->gate, m->up, ffn);
-    if ((rc = quantize_for(m, Ly.m[6].dt, m->gate, ffn, m->xq))) return rc;
+    {
+      const bool q8 = Ly.m[6].dt == NRQ_Q8_0;
+      hipLaunchKernelGGL(nrq::swiglu_kernel, dim3((ffn + 255) / 256), dim3(256), 0, m->stream, m->gate, m->up, ffn,
+                         q8 ? m->xq : nullptr);
+      if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: swiglu launch failed");
+      if (!q8 && (rc = quantize_for(m, Ly.m[6].dt, m->gate, ffn, m->xq))) return rc;
+    }
     if ((rc = matvec(m, Ly.m[6], m->xq, m->xb2, d, ffn))) return rc;
     pending = m->xb2;
   }
@@ -642,7 +799,7 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
   if (c.dim <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 || c.ffn_dim <= 0 ||
       c.vocab <= 0 || c.ctx <= 0)
     return mfail(NRQ_ERR_SHAPE, "nrq_model_create: non-positive dimension");
-  if (c.n_heads % c.n_kv_heads || c.head_dim % 16 || c.head_dim > 256 || c.dim % 256 || c.ffn_dim % 256 ||
+  if (c.n_heads % c.n_kv_heads || c.head_dim % 32 || c.head_dim > 128 || c.dim % 256 || c.ffn_dim % 256 ||
       (c.n_heads * c.head_dim) % 256)
     return mfail(NRQ_ERR_UNSUPPORTED, "nrq_model_create: head or width layout not supported");
   if (c.dim > nrq::kNormMax || c.ctx > nrq::kAttMaxCtx)
@@ -653,6 +810,7 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
   m->att_dim = c.n_heads * c.head_dim;
   m->maxd = std::max(std::max(c.dim, m->att_dim), c.ffn_dim);
   m->L.resize(c.n_layers);
+  m->att_lds = ((size_t)((c.ctx + 3) & ~3) + 2 * nrq::kAttProd + 3 * (size_t)c.head_dim + 8) * 4;
   auto bail = [&](hipError_t e, const char* what) {
     nrq::set_last_error((std::string(what) + ": " + hipGetErrorString(e)).c_str());
     nrq_model_destroy(m);
