@@ -327,7 +327,7 @@ def main():
     r = measure_matvec(args.config, args.steps, args.warmup, order)
     others = {}
     for name in [s for s in args.also.split(",") if s and s != args.config]:
-        o = measure_matvec(name, max(20, args.steps // 4), max(5, args.warmup // 2), order)
+        o = measure_matvec(name, args.steps, args.warmup, order)
         others[name] = {k: round(v, 3) if isinstance(v, float) else v for k, v in o.items()}
     prefill = None if args.no_prefill else measure_prefill()
     decode = None if args.no_decode else measure_decode()

@@ -171,14 +171,16 @@ __device__ __forceinline__ float ws_q4k(const uint8_t* lds_w, uint32_t o, const 
     sub[2 * c] = lo;
     sub[2 * c + 1] = hi;
   }
-  float sum_q = (float)((int)(scA & 0xffu) * sub[0]);
-  sum_q = sum_q + (float)((int)((scA >> 8) & 0xffu) * sub[1]);
-  sum_q = sum_q + (float)((int)((scA >> 16) & 0xffu) * sub[2]);
-  sum_q = sum_q + (float)((int)(scA >> 24) * sub[3]);
-  sum_q = sum_q + (float)((int)(scB & 0xffu) * sub[4]);
-  sum_q = sum_q + (float)((int)((scB >> 8) & 0xffu) * sub[5]);
-  sum_q = sum_q + (float)((int)((scB >> 16) & 0xffu) * sub[6]);
-  sum_q = sum_q + (float)((int)(scB >> 24) * sub[7]);
+  // sc_j * sub_j on the 24-bit multiplier: |sc| < 64, |sub| <= 61440, so both
+  // operands and the product fit 24 bits and the result is the exact product.
+  float sum_q = (float)__mul24((int)(scA & 0xffu), sub[0]);
+  sum_q = sum_q + (float)__mul24((int)((scA >> 8) & 0xffu), sub[1]);
+  sum_q = sum_q + (float)__mul24((int)((scA >> 16) & 0xffu), sub[2]);
+  sum_q = sum_q + (float)__mul24((int)(scA >> 24), sub[3]);
+  sum_q = sum_q + (float)__mul24((int)(scB & 0xffu), sub[4]);
+  sum_q = sum_q + (float)__mul24((int)((scB >> 8) & 0xffu), sub[5]);
+  sum_q = sum_q + (float)__mul24((int)((scB >> 16) & 0xffu), sub[6]);
+  sum_q = sum_q + (float)__mul24((int)(scB >> 24), sub[7]);
   // sum_m: m_j zero-extended into i16 pairs, dotted with the i16 pair sums.
   const u32x4 bs = *(const u32x4*)(xb + 64);
   int sum_m = sdot2(__builtin_amdgcn_perm(0u, mnA, 0x0c010c00u), bs.x, 0);
@@ -247,7 +249,7 @@ __device__ __forceinline__ float ws_q6k(const uint32_t* w32, uint32_t o, const u
 #pragma unroll
   for (int g = 0; g < 16; g++) {
     const int s = (int)(int8_t)((S[g >> 2] >> (8 * (g & 3))) & 0xffu);
-    sum = sum + (float)(s * gs[g]);
+    sum = sum + (float)__mul24(s, gs[g]);  // |s| <= 128, |gs| <= 65536: exact in 24 bits
   }
   const uint32_t dw = w32[(o + 208) >> 2];
   const uint32_t dbits = ((o + 208) & 2) ? (dw >> 16) : (dw & 0xffffu);
@@ -279,6 +281,7 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(const uint8_t* __restr
                                                           int nstages) {
   using F = WS<FMT>;
   constexpr int NI = F::NI, BS = F::BS, TBK = 64 * F::BPL, STAGE = NI * 1024;
+  static_assert(NS >= 1 && NS <= 4, "the vmcnt waits cover up to 4 stages");
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -327,7 +330,8 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(const uint8_t* __restr
     case 0: ws_wait_vm<0>(); break;
     case 1: ws_wait_vm<NI>(); break;
     case 2: ws_wait_vm<2 * NI>(); break;
-    default: ws_wait_vm<3 * NI>(); break;
+    case 3: ws_wait_vm<3 * NI>(); break;
+    default: ws_wait_vm<4 * NI>(); break;
   }
   ws_lds_barrier();
   ws_repack<FMT>((const uint32_t*)xraw, (uint32_t)((uintptr_t)X & 15), bpr, xl, tid, 64 * NW);
@@ -345,9 +349,12 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(const uint8_t* __restr
 
   for (int t = 0; t < ntiles; t++) {
     const int after = min(nstages - 1, ntiles - 1 - t);  // tiles issued after t
-    if (after >= 2) ws_wait_vm<2 * NI>();
-    else if (after == 1) ws_wait_vm<NI>();
-    else ws_wait_vm<0>();
+    switch (after) {  // tile t landed once `after` tiles' loads are outstanding
+      case 0: ws_wait_vm<0>(); break;
+      case 1: ws_wait_vm<NI>(); break;
+      case 2: ws_wait_vm<2 * NI>(); break;
+      default: ws_wait_vm<3 * NI>(); break;
+    }
     asm volatile("" ::: "memory");
     const uint8_t* cur = stages + (t % nstages) * STAGE;
     const int tb0 = t * TBK;
@@ -356,13 +363,14 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(const uint8_t* __restr
     for (int k = 0; k < F::BPL; k++) {
       const int i = lane + 64 * k;
       if (tb0 + i < nb) {
-        const uint32_t o = skew + (uint32_t)i * BS;
-        const uint32_t* xb = xl + bb[k] * F::XS;
+        // LDS offsets stay below 160 KiB, so the 24-bit multiplier is exact here
+        const uint32_t o = skew + __umul24((uint32_t)i, (uint32_t)BS);
+        const uint32_t* xb = xl + __umul24((uint32_t)bb[k], (uint32_t)F::XS);
         float c;
         if constexpr (FMT == kQ8_0) c = ws_q80((const uint32_t*)cur, o, xb);
         else if constexpr (FMT == kQ4K) c = ws_q4k(cur, o, xb);
         else c = ws_q6k((const uint32_t*)cur, o, xb);
-        u[bb[k] * rpw + rr[k]] = c;
+        u[__umul24((uint32_t)bb[k], (uint32_t)rpw) + rr[k]] = c;
       }
       rr[k] += step_r;
       bb[k] += step_b;
