@@ -39,6 +39,10 @@ METRIC = "Q-matvec HBM GB/s (% of peak); decode tok/s, Llama-3.2-1B-shape Q8_0"
 HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, vendor peak
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, vendor peak
 MALL_BYTES = 256 << 20
+# HBM bytes per launch of the headline kernel: rocprofv3 FETCH_SIZE and WRITE_SIZE passes over this
+# script, each scaled by the same counter's reading for a 256 MiB device copy
+# (profiles/wstream_matvec_q4k_8192x3072.md). Workloads not counted report None.
+MEASURED_TRAFFIC = {("cfg2", "scalar"): 14312636}
 
 # name -> (dtype, rows, cols, seed, description)
 CONFIGS = {
@@ -307,6 +311,20 @@ def cpu_baseline_decode(seconds):
                       f"(scalar-order kernels, {threads} threads) in {dt:.1f} s"}
 
 
+def copy_calibration(nbytes):
+    """Five device-to-device copies of `nbytes` (reads nbytes, writes nbytes):
+    the reference kernel for scaling FETCH_SIZE / WRITE_SIZE counter readings."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": nbytes, "copies": 5}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -319,7 +337,12 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--also", default="cfg1,cfg3", help="other matvec configs reported beside (comma list)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 device-to-device copies of MIB MiB (a known-size kernel for HBM counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration << 20)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding of the path is design-only"}))
         sys.exit(2)
@@ -365,7 +388,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC.get((args.config, args.order)),
             "kernel_us": round(r["kernel_us"], 3),
         },
         "cpu_baseline": cpu,
