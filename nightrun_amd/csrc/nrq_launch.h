@@ -34,7 +34,8 @@ struct MatmulLaunch {
   int bpr;
   int batch;
   void* stream;
-  int variant = 0;  // scalar order: 0 int8-MFMA tile kernel, 1 one decode launch per token
+  int variant = 0;  // scalar order: 0 int8-MFMA kernel (LDS-staged for Q4_K/Q6_K), 1 one decode
+                    // launch per token, 2 int8-MFMA kernel with direct loads
 };
 
 struct QuantLaunch {

@@ -11,7 +11,7 @@ namespace nrq {
 
 int launch_matmul(int dtype, int order, const MatmulLaunch& L) {
   if (L.rows <= 0 || L.bpr <= 0 || L.batch <= 0) return 0;
-  if (order == kOrderScalar && L.variant == 0) return launch_mmq(dtype, L);
+  if (order == kOrderScalar && (L.variant == 0 || L.variant == 2)) return launch_mmq(dtype, L);
   const size_t xb = dtype == kQ8_0 ? (size_t)kQ8_0Bytes : (size_t)kQ8KBytes;
   for (int b = 0; b < L.batch; b++) {
     MatvecLaunch M;

@@ -390,6 +390,22 @@ def test_matmul_batches_past_64(gpu, oracle, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+def test_matmul_long_rows_and_odd_block_counts(gpu, oracle, dtype):
+    """Rows longer than a split holds (70 blocks, 5 tokens: one split, idle
+    token tiles), an odd block count at a full 64-token batch (Q6_K blocks of
+    one row then alternate their 4-byte alignment), and a row count that is
+    not a multiple of 16."""
+    qk = oracle.QK[dtype]
+    for rows, bpr, batch in ((20, 70, 5), (40, 37, 64)):
+        cols = bpr * qk
+        w = oracle.gen_weights(dtype, 700 + bpr, rows, cols)
+        xs = oracle.quantize_act(dtype, oracle.Rng(701 + bpr).normal(batch * cols))
+        assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, batch),
+                       oracle.matmul(dtype, 0, w, xs, rows, cols, batch, threads=THREADS),
+                       f"rows {rows} bpr {bpr} batch {batch}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_matmul_adversarial_and_saturated(gpu, oracle, dtype):
     """Adversarial activations, the reference quantizers' weights, and the
     saturated blocks of tests/kquant.rs:210-245 through the MFMA path."""
