@@ -31,6 +31,8 @@ HIP_FLAGS = [
     "-ffp-contract=off",
     "-fno-gpu-rdc",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs (gfx950 allows it): no v_accvgpr_read per result
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-function",
 ]

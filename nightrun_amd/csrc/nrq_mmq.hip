@@ -283,31 +283,34 @@ __global__ __launch_bounds__(256) void mmq_kernel(const uint8_t* __restrict__ W,
 // continuing from the previous split's partial sum (handed over in LDS).
 //
 // Workgroup: 4 waves = T token tiles x S splits (T * S = 4), one 16-row tile.
-constexpr int kMqStage = 2208;   // dwords per wave stage
-constexpr int kMqAct = 0;        // [16 tokens][73 dwords] (+48 written by clamped lanes)
-constexpr int kMqScal = 1216;    // [5][16]: tokens' bsum pair sums P0..P3, then d
-constexpr int kMqWt = 1296;      // Q4_K [16][36] (+192) | Q6_K [16][53] (+48)
-constexpr int kMqActInst = 19;   // 64-lane dword DMAs for 16 x 73 dwords
-constexpr int kMqMaxPer = 16;    // blocks per split held in registers when S > 1
+// Stage layout (dwords). Every DMA moves 16 bytes per lane from a 16-byte
+// aligned address; a Q8_K token block (292 B, 4-byte aligned) lands in a
+// 19-piece window and starts s4 dwords in; a Q6_K block (210 B, 2-byte
+// aligned) lands in a 14-piece window and starts `skew` bytes in.
+constexpr int kMqAct = 0;       // [16 tokens][76]: 5 DMAs of 64 pieces (+64 pieces of clamped lanes)
+constexpr int kMqScal = 1280;   // [5][16]: tokens' bsum pair sums P0..P3, then d
+constexpr int kMqWt = 1360;     // Q4_K [16 rows][36], 3 DMAs | Q6_K [16 rows][56], 4 DMAs
+constexpr int kMqActInst = 5;
+constexpr int kMqMaxPer = 16;   // blocks per split held in registers when S > 1
 
 template <int FMT>
 struct MQ;
 template <>
 struct MQ<kQ4K> {
-  static constexpr int WI = 3;  // 16 rows x 9 16-byte pieces, dwordx4 DMA
+  static constexpr int WI = 3, WROW = 36, STAGE = kMqWt + 3 * 256;
   static constexpr int NI = kMqActInst + WI;
 };
 template <>
 struct MQ<kQ6K> {
-  static constexpr int WI = 14;  // 16 rows x 53-dword windows, dword DMA
+  static constexpr int WI = 4, WROW = 56, STAGE = kMqWt + 4 * 256;
   static constexpr int NI = kMqActInst + WI;
 };
 
-__device__ __forceinline__ void mq_dma4(const uint8_t* sbase, uint32_t voff, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" : : "s"(m0), "v"(voff), "s"(sbase) : "memory");
-}
 __device__ __forceinline__ void mq_dma16(const uint8_t* sbase, uint32_t voff, uint32_t m0) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" : : "s"(m0), "v"(voff), "s"(sbase) : "memory");
+}
+__device__ __forceinline__ void mq_dma16v(const void* g, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(g) : "memory");
 }
 template <int N>
 __device__ __forceinline__ void mq_wait_vm() {
@@ -320,17 +323,16 @@ __device__ __forceinline__ uint32_t mq_lds_addr(const void* p) {
 }
 
 // Contribution of the staged block to this lane's 4 elements (tokens 4g + i, row n).
-__device__ __forceinline__ void mq_block_q4k(const uint32_t* st, int n, int g, float c[4]) {
-  {  // tokens' bsum pair sums (sub-blocks 2g, 2g+1 of token n) and d
-    const uint32_t* tok = st + kMqAct + n * 73;
-    const uint32_t v0 = tok[65 + 2 * g], v1 = tok[66 + 2 * g];
+// `A` is token n's Q8_K block in LDS.
+__device__ __forceinline__ void mq_block_q4k(const uint32_t* st, const uint32_t* A, int n, int g, float c[4]) {
+  {  // token n's bsum pair sums for sub-blocks 2g, 2g+1, and its d
+    const uint32_t v0 = A[65 + 2 * g], v1 = A[66 + 2 * g];
     const int s0 = (int)(int16_t)(v0 & 0xffffu) + (int)(int16_t)(v0 >> 16);
     const int s1 = (int)(int16_t)(v1 & 0xffffu) + (int)(int16_t)(v1 >> 16);
     uint32_t* scal = (uint32_t*)st + kMqScal;
     scal[g * 16 + n] = ((uint32_t)s0 & 0xffffu) | ((uint32_t)s1 << 16);
-    if (g == 0) scal[64 + n] = tok[0];
+    if (g == 0) scal[64 + n] = A[0];
   }
-  const uint32_t* A = st + kMqAct + n * 73;
   const uint32_t* Wr = st + kMqWt + n * 36;
   const u32x4 h = *(const u32x4*)Wr;
   // kquant.rs:83-92, four scales or mins per word
@@ -377,10 +379,10 @@ __device__ __forceinline__ void mq_block_q4k(const uint32_t* st, int n, int g, f
   }
 }
 
-__device__ __forceinline__ void mq_block_q6k(const uint32_t* st, int n, int g, uint32_t sh, float c[4]) {
-  if (g == 0) ((uint32_t*)st)[kMqScal + 64 + n] = st[kMqAct + n * 73];  // token n's d
-  const uint32_t* A = st + kMqAct + n * 73;
-  const uint32_t* Wr = st + kMqWt + n * 53;  // the row's block starts `sh` bytes in
+// `Wr` is row n's window, the block starting `sh` (0 or 2) bytes into Wr[0].
+__device__ __forceinline__ void mq_block_q6k(const uint32_t* st, const uint32_t* A, const uint32_t* Wr, uint32_t sh,
+                                             int n, int g, float c[4]) {
+  if (g == 0) ((uint32_t*)st)[kMqScal + 64 + n] = A[0];  // token n's d
   const int gh = g & 1;
   const bool zh = g >= 2;  // k-groups 2-3: the -32 half
   uint32_t S[4];
@@ -405,8 +407,8 @@ __device__ __forceinline__ void mq_block_q6k(const uint32_t* st, int n, int g, u
       q6k_planes(a1, b1, h1, p1);
 #pragma unroll
       for (int pn = 0; pn < 4; pn++) {
-        q6[u][pn][0] = p0[pn];
-        q6[u][pn][1] = p1[pn];
+        q6[u][pn][0] = zh ? 0xe0e0e0e0u : p0[pn];
+        q6[u][pn][1] = zh ? 0xe0e0e0e0u : p1[pn];
       }
     }
 #pragma unroll
@@ -415,9 +417,7 @@ __device__ __forceinline__ void mq_block_q6k(const uint32_t* st, int n, int g, u
       for (int u = 0; u < 2; u++) {
         const int G = 8 * hh + 2 * pn + u;  // kquant.rs:232-246 group order
         const int a = 1 + 32 * hh + 8 * pn + 4 * u + 2 * gh;  // q8 bytes 128hh + 32pn + 16u + 8gh ..
-        const uint32_t bq0 = zh ? 0xe0e0e0e0u : q6[u][pn][0];
-        const uint32_t bq1 = zh ? 0xe0e0e0e0u : q6[u][pn][1];
-        const i32x4 gs = mfma16(A[a], A[a + 1], bq0, bq1);
+        const i32x4 gs = mfma16(A[a], A[a + 1], q6[u][pn][0], q6[u][pn][1]);
         const float sc = (float)(int)(int8_t)((S[G >> 2] >> (8 * (G & 3))) & 0xffu);
         // kquant.rs:244: sum += f32(sc) * f32(gs); |sc * gs| <= 128 * 65536, exact
 #pragma unroll
@@ -439,7 +439,7 @@ __global__ __launch_bounds__(256) void mmq_lds_kernel(const uint8_t* __restrict_
                                                       float* __restrict__ Y, int rows, int bpr, int batch, int ntg,
                                                       int nrt) {
   constexpr int T = 4 / S;
-  constexpr int NI = MQ<FMT>::NI, WI = MQ<FMT>::WI;
+  constexpr int NI = MQ<FMT>::NI, WI = MQ<FMT>::WI, STAGE = MQ<FMT>::STAGE;
   constexpr int NPER = S == 1 ? 1 : kMqMaxPer;
   extern __shared__ __align__(16) uint32_t lds[];
   // XCD-aware numbering: the token groups of one row tile share an XCD (and its L2)
@@ -453,81 +453,79 @@ __global__ __launch_bounds__(256) void mmq_lds_kernel(const uint8_t* __restrict_
   const int tw = wave % T, sp = wave / T;
   const int n = lane & 15, g = lane >> 4;
   const int t0 = (tg * T + tw) * 16, r0 = rt * 16;
-  uint32_t* stages = lds + wave * 2 * kMqStage;
+  uint32_t* stages = lds + wave * 2 * STAGE;
   const int per = (bpr + S - 1) / S;
   const int b_lo = sp * per;
   const int nmine = max(0, min(per, bpr - b_lo));
+  const uintptr_t xu = (uintptr_t)X;
 
-  // Per-lane DMA offsets, fixed over blocks (clamped rows / tokens load valid memory, store nothing).
-  uint32_t aoff[kMqActInst];
+  // Per-lane DMA sources, fixed over blocks (clamped rows / tokens load valid memory, store nothing):
+  // piece p of the activation = 16-byte piece p % 19 of token p / 19's window.
+  uint32_t aoff[kMqActInst], aq[kMqActInst];
 #pragma unroll
   for (int k = 0; k < kMqActInst; k++) {
-    const int d = min(64 * k + lane, 16 * 73 - 1);
-    const int tt = d / 73, w = d - tt * 73;
-    const int tok = min(t0 + tt, batch - 1);
-    aoff[k] = (uint32_t)tok * (uint32_t)bpr * (uint32_t)kQ8KBytes + 4u * (uint32_t)w;
+    const int p = min(64 * k + lane, 16 * 19 - 1);
+    const int tt = p / 19;
+    aq[k] = 16u * (uint32_t)(p - tt * 19);
+    aoff[k] = (uint32_t)min(t0 + tt, batch - 1) * (uint32_t)bpr * (uint32_t)kQ8KBytes;
   }
-  uint32_t woff[WI];
-  uint32_t wpar[WI];
+  uint32_t woff[WI];  // Q4_K: byte offset of the piece at block 0; Q6_K: the row's first block index
+  uint32_t wq[WI];
 #pragma unroll
   for (int k = 0; k < WI; k++) {
     if constexpr (FMT == kQ4K) {
       const int pc = min(64 * k + lane, 16 * 9 - 1);
-      const int rr = pc / 9, q = pc - rr * 9;
-      const uint32_t row = (uint32_t)min(r0 + rr, rows - 1);
-      woff[k] = row * (uint32_t)bpr * (uint32_t)kQ4KBytes + 16u * (uint32_t)q;
-      wpar[k] = 0;
+      const int rr = pc / 9;
+      woff[k] = (uint32_t)min(r0 + rr, rows - 1) * (uint32_t)bpr * (uint32_t)kQ4KBytes + 16u * (uint32_t)(pc - rr * 9);
+      wq[k] = 0;
     } else {
-      const int d = min(64 * k + lane, 16 * 53 - 1);
-      const int rr = d / 53, w = d - rr * 53;
-      const uint32_t m = (uint32_t)min(r0 + rr, rows - 1) * (uint32_t)bpr;
-      woff[k] = m * (uint32_t)kQ6KBytes + 4u * (uint32_t)w;
-      wpar[k] = m & 1u;
+      const int pc = min(64 * k + lane, 16 * 14 - 1);
+      const int rr = pc / 14;
+      woff[k] = (uint32_t)min(r0 + rr, rows - 1) * (uint32_t)bpr;
+      wq[k] = 16u * (uint32_t)(pc - rr * 14);
     }
   }
+  const uint32_t tok_n = (uint32_t)min(t0 + n, batch - 1) * (uint32_t)bpr * (uint32_t)kQ8KBytes;
   const uint32_t mrow = (uint32_t)min(r0 + n, rows - 1) * (uint32_t)bpr;  // this lane's row, in blocks
 
   auto issue = [&](int b, int stg) {
-    const uint32_t sb = mq_lds_addr(stages + stg * kMqStage);
-    const uint8_t* xb = X + (size_t)b * kQ8KBytes;
+    const uint32_t sb = mq_lds_addr(stages + stg * STAGE);
+    const uint32_t xb = (uint32_t)b * (uint32_t)kQ8KBytes;
 #pragma unroll
-    for (int k = 0; k < kMqActInst; k++) mq_dma4(xb, aoff[k], sb + (uint32_t)(kMqAct + 64 * k) * 4u);
+    for (int k = 0; k < kMqActInst; k++) {
+      const uintptr_t src = ((xu + aoff[k] + xb) & ~(uintptr_t)15) + aq[k];
+      mq_dma16v((const void*)src, sb + (uint32_t)(kMqAct + 256 * k) * 4u);
+    }
     if constexpr (FMT == kQ4K) {
       const uint8_t* wb = W + (size_t)b * kQ4KBytes;
 #pragma unroll
       for (int k = 0; k < WI; k++) mq_dma16(wb, woff[k], sb + (uint32_t)(kMqWt + 256 * k) * 4u);
     } else {
-      // block (m + b) of a Q6_K matrix starts at byte 210 (m + b); its 4-byte
-      // aligned window starts 2 ((m + b) & 1) bytes earlier
-      const uint32_t d0 = (uint32_t)b * kQ6KBytes - 2u * ((uint32_t)b & 1u);
-      const uint32_t d1 = (uint32_t)b * kQ6KBytes - 2u * (((uint32_t)b + 1u) & 1u);
 #pragma unroll
-      for (int k = 0; k < WI; k++) mq_dma4(W, woff[k] + (wpar[k] ? d1 : d0), sb + (uint32_t)(kMqWt + 64 * k) * 4u);
+      for (int k = 0; k < WI; k++) {
+        const uint32_t start = (woff[k] + (uint32_t)b) * (uint32_t)kQ6KBytes;
+        mq_dma16(W, (start & ~15u) + wq[k], sb + (uint32_t)(kMqWt + 256 * k) * 4u);
+      }
     }
   };
 
   float cb[NPER][4];
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  // at most 63 vector-memory instructions outstanding (the vmcnt range)
-  auto room = [&]() {
-    if constexpr (2 * NI > 63) mq_wait_vm<63 - NI>();
-  };
   if (nmine > 0) issue(b_lo, 0);
-  if (nmine > 1) {
-    room();
-    issue(b_lo + 1, 1);
-  }
+  if (nmine > 1) issue(b_lo + 1, 1);
   auto step = [&](int k) {
     if (k + 1 < nmine) mq_wait_vm<NI>();
     else mq_wait_vm<0>();
     asm volatile("" ::: "memory");
-    const uint32_t* st = stages + (k & 1) * kMqStage;
+    const uint32_t b = (uint32_t)(b_lo + k);
+    const uint32_t* st = stages + (k & 1) * STAGE;
+    const uint32_t* A = st + kMqAct + n * 76 + (((xu + tok_n + b * (uint32_t)kQ8KBytes) & 15) >> 2);
     float c[4];
     if constexpr (FMT == kQ4K) {
-      mq_block_q4k(st, n, g, c);
+      mq_block_q4k(st, A, n, g, c);
     } else {
-      const uint32_t sh = 2u * ((mrow + (uint32_t)(b_lo + k)) & 1u);
-      mq_block_q6k(st, n, g, sh, c);
+      const uint32_t skew = ((mrow + b) * (uint32_t)kQ6KBytes) & 15u;
+      mq_block_q6k(st, A, st + kMqWt + n * 56 + (skew >> 2), skew & 3u, n, g, c);
     }
     if constexpr (S == 1) {
 #pragma unroll
@@ -542,7 +540,6 @@ __global__ __launch_bounds__(256) void mmq_lds_kernel(const uint8_t* __restrict_
     }
     if (k + 2 < nmine) {
       mq_wait_lgkm0();  // this stage's LDS reads are done before the DMA refills it
-      room();
       asm volatile("" ::: "memory");
       issue(b_lo + k + 2, k & 1);
     }
@@ -554,7 +551,7 @@ __global__ __launch_bounds__(256) void mmq_lds_kernel(const uint8_t* __restrict_
     for (int k = 0; k < NPER; k++)
       if (k < nmine) step(k);
     // chain across splits, in block order: split s continues from split s - 1
-    float* hand = (float*)(lds + 4 * 2 * kMqStage) + tw * 256;
+    float* hand = (float*)(lds + 4 * 2 * STAGE) + tw * 256;
     for (int s = 0; s < S; s++) {
       if (sp == s) {
         if (s > 0) {
@@ -606,7 +603,7 @@ static int launch_mmq_lds(const MatmulLaunch& L) {
   const int ntg = (ntt + T - 1) / T;
   const long nwg = rt_pad * ntg;
   if (nwg > 0x7fffffffL) return NRQ_LAUNCH_BAD_ARG;
-  const size_t lds = (size_t)4 * 2 * kMqStage * 4 + (S > 1 ? (size_t)T * 256 * 4 : 0);
+  const size_t lds = (size_t)4 * 2 * MQ<FMT>::STAGE * 4 + (S > 1 ? (size_t)T * 256 * 4 : 0);
   hipStream_t st = (hipStream_t)L.stream;
   const uint8_t* w = (const uint8_t*)L.w;
   const uint8_t* x = (const uint8_t*)L.xs;
