@@ -194,66 +194,56 @@ __device__ void dev_sincosf(float x, float* sn, float* cs) {
   }
 }
 
-// Sequential f32 sum a[0] + a[1] + ... + a[n-1] from +0.0, in index order, by
-// one lane: the reference's `s += v` loops. LDS is read 32 values ahead in
-// 16-byte loads so the dependent adds do not wait on a load. a is 16-byte
-// aligned.
-__device__ float chain_sum(const float* __restrict__ a, int n) {
-  float s = 0.0f;
-  int i = 0;
-  if (n >= 64) {
-    float4 A[8], B[8];
+// Sequential f32 sum s + a[0] + a[1] + ... + a[n-1], in index order, by
+// one lane: the reference's `s += v` loops. Three banks of four 16-byte LDS
+// loads rotate: a bank is refilled 48 values ahead right after it is added, so
+// the dependent adds rarely wait on a load. a is 16-byte aligned.
+__device__ float chain_from(const float* __restrict__ a, int n, float s) {
+  const float4* a4 = (const float4*)a;
+  const int n16 = n >> 4;  // groups of 16 values
+  int g = 0;
+  if (n16 >= 3) {
+    float4 R0[4], R1[4], R2[4];
+    auto ld = [&](float4* R, int gg) {
 #pragma unroll
-    for (int k = 0; k < 8; k++) A[k] = ((const float4*)a)[k];
-    for (; i + 64 <= n; i += 32) {  // A holds a[i .. i+32)
+      for (int k = 0; k < 4; k++) R[k] = a4[4 * gg + k];
+    };
+    auto add = [&](const float4* R) {
 #pragma unroll
-      for (int k = 0; k < 8; k++) B[k] = ((const float4*)(a + i + 32))[k];
-#pragma unroll
-      for (int k = 0; k < 8; k++) {
-        s = s + A[k].x;
-        s = s + A[k].y;
-        s = s + A[k].z;
-        s = s + A[k].w;
+      for (int k = 0; k < 4; k++) {
+        s = s + R[k].x;
+        s = s + R[k].y;
+        s = s + R[k].z;
+        s = s + R[k].w;
       }
-#pragma unroll
-      for (int k = 0; k < 8; k++) A[k] = B[k];
+    };
+    ld(R0, 0);
+    ld(R1, 1);
+    ld(R2, 2);
+    for (; g + 6 <= n16; g += 3) {  // groups g .. g+2 are loaded
+      add(R0);
+      ld(R0, g + 3);
+      add(R1);
+      ld(R1, g + 4);
+      add(R2);
+      ld(R2, g + 5);
     }
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      s = s + A[k].x;
-      s = s + A[k].y;
-      s = s + A[k].z;
-      s = s + A[k].w;
-    }
-    i += 32;
+    // groups g .. g+2 loaded, fewer than three groups left after them
+    add(R0);
+    if (g + 3 < n16) ld(R0, g + 3);
+    add(R1);
+    if (g + 4 < n16) ld(R1, g + 4);
+    add(R2);
+    if (g + 5 < n16) ld(R2, g + 5);
+    if (g + 3 < n16) add(R0);
+    if (g + 4 < n16) add(R1);
+    if (g + 5 < n16) add(R2);
+    g = n16;
   }
-  for (; i < n; i++) s = s + a[i];
+  for (int i = 16 * g; i < n; i++) s = s + a[i];
   return s;
 }
-
-// s + p[0] + p[stride] + ... + p[(n-1)*stride] in order, each lane its own
-// chain (lane-consecutive p), 16 values read ahead.
-__device__ float chain_sum_strided(const float* __restrict__ p, int stride, int n, float s) {
-  int t = 0;
-  if (n >= 32) {
-    float A[16], B[16];
-#pragma unroll
-    for (int k = 0; k < 16; k++) A[k] = p[(size_t)k * stride];
-    for (; t + 32 <= n; t += 16) {  // A holds terms t .. t+16
-#pragma unroll
-      for (int k = 0; k < 16; k++) B[k] = p[(size_t)(t + 16 + k) * stride];
-#pragma unroll
-      for (int k = 0; k < 16; k++) s = s + A[k];
-#pragma unroll
-      for (int k = 0; k < 16; k++) A[k] = B[k];
-    }
-#pragma unroll
-    for (int k = 0; k < 16; k++) s = s + A[k];
-    t += 16;
-  }
-  for (; t < n; t++) s = s + p[(size_t)t * stride];
-  return s;
-}
+__device__ float chain_sum(const float* __restrict__ a, int n) { return chain_from(a, n, 0.0f); }
 
 // q8::quantize (q8.rs:27-44) of one 32-value block held one value per lane of
 // a 32-lane group: amax over the group, d = f16(amax/127), round half away,
@@ -344,25 +334,34 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
     }
 }
 
-constexpr int kAttNT = 256;
+constexpr int kAttNT = 1024;
 constexpr int kAttMaxCtx = 8192;
-constexpr int kAttProd = 8192;  // floats per product stage: kAttProd / head_dim positions
+constexpr int kAttProd = 8704;  // floats per product stage (head_dim x (chunk + 4) <= 8704)
+
+// Positions per product chunk: a multiple of 64 with head_dim x (chunk + 4) <= kAttProd.
+__host__ __device__ inline int att_chunk(int hd) {
+  const int c = (8192 / hd) & ~63;
+  return c < 64 ? 64 : c;
+}
 
 // One workgroup per query head: the attention block of infer.rs:540-572.
-//  1. rope::apply (rope.rs:49-65) on the head's q and on its KV head's k at
-//     the current position; the KV append as f16 (infer.rs:547-551) by the
-//     first query head of each KV group. The fresh key/value are used from
-//     LDS, so the other heads of the group never read the row being written.
+//  1. The key rows of the first kAttNT positions are requested first (every
+//     row but the current one is already in the cache), then rope::apply
+//     (rope.rs:49-65) on the head's q and on its KV head's k at the current
+//     position, and the KV append as f16 (infer.rs:547-551) by the first query
+//     head of each KV group. The fresh key/value are used from LDS, so the
+//     other heads of the group never read the row being written.
 //  2. scores: dot_f16(k_t, q) * scale (kernels.rs:146-160, dimension order).
 //  3. softmax (vec.rs:30-42): max, exp, the exp-sum in position order (one
 //     lane), inv, a_t = e_t * inv.
-//  4. out[i] += a_t * v_t[i] in position order (kernels.rs:163-173): the
-//     other waves form the products a_t * v_t[i] of the next chunk of
-//     positions in LDS while the chain lanes (one per dimension) add the
-//     current chunk.
+//  4. out[i] += a_t * v_t[i] in position order (kernels.rs:163-173). Chunks of
+//     C positions: the producer waves form the products a_t * v_t[i] of the
+//     next chunk in LDS, dimension-major (row stride C + 4 floats), from value
+//     rows they requested three chunks earlier; the chain lanes (one per
+//     dimension) add the current chunk, four positions per 16-byte LDS read.
 //  5. out (f32) and, when out_q8 != null, its Q8_0 blocks for the output
 //     projection.
-// LDS: att[ctx] | prod[2][kAttProd] | q[hd] | kcur[hd] | vcur[hd] | red[8]
+// LDS: att[ctx] | prod[2][kAttProd] | q[hd] | kcur[hd] | vcur[hd] | red[32]
 __global__ __launch_bounds__(kAttNT) void attention_kernel(
     const float* __restrict__ q_in, const float* __restrict__ k_in, const float* __restrict__ v_in,
     const float* __restrict__ freqs, const int* __restrict__ ctl, int n_heads, int n_kv_heads, int hd, int ctx,
@@ -371,7 +370,7 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   extern __shared__ __align__(16) float sm[];
   const int h = blockIdx.x, tid = threadIdx.x;
   const int pos = ctl[CTL_POS], n = pos + 1;
-  const int gqa = n_heads / n_kv_heads, g = h / gqa, kvd = n_kv_heads * hd, half = hd / 2;
+  const int gqa = n_heads / n_kv_heads, g = h / gqa, kvd = n_kv_heads * hd, half = hd / 2, g8 = hd / 8;
   const bool writer = (h % gqa) == 0;
   float* att = sm;
   float* prod = sm + ((ctx + 3) & ~3);
@@ -381,6 +380,16 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   float* red = vcur + hd;
   const size_t row = ((size_t)layer * ctx + pos) * kvd + (size_t)g * hd;
   const size_t base = (size_t)layer * ctx * kvd + (size_t)g * hd;
+  uint4 kr[16];  // key row of position tid (16-byte pieces, g8 <= 16 used)
+  auto load_key = [&](int t) {
+    if (t < n && t != pos) {
+      const uint4* src = (const uint4*)(kc + base + (size_t)t * kvd);
+#pragma unroll
+      for (int j = 0; j < 16; j++)
+        if (j < g8) kr[j] = src[j];
+    }
+  };
+  load_key(tid);
   for (int i = tid; i < half; i += kAttNT) {
     float sn, cs;
     dev_sincosf((float)pos * freqs[i], &sn, &cs);
@@ -402,46 +411,28 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
     if (writer) vc[row + i] = (uint16_t)vb;
   }
   __syncthreads();
-  // Scores: thread tid takes positions tid, tid + kAttNT, ...; the key row of
-  // its next position is loaded into registers while the current one is
-  // scored, so each iteration waits on a load issued one iteration earlier.
-  // Position `pos` uses the fresh key from LDS.
+  // Scores: thread tid takes positions tid, tid + kAttNT, ...
   float mx = -INFINITY;
-  {
-    const int g8 = hd / 8;  // 16-byte pieces per key row (<= 16)
-    uint4 cur[16], nxt[16];
-    auto load_row = [&](int t, uint4* r) {
-      if (t < n && t != pos) {
-        const uint4* src = (const uint4*)(kc + base + (size_t)t * kvd);
+  for (int t = tid; t < n; t += kAttNT) {
+    if (t != tid) load_key(t);
+    float s = 0.0f;
+    if (t == pos) {
+      for (int i = 0; i < hd; i++) s = s + kcur[i] * qs[i];
+    } else {
 #pragma unroll
-        for (int j = 0; j < 16; j++)
-          if (j < g8) r[j] = src[j];
-      }
-    };
-    load_row(tid, cur);
-    for (int t = tid; t < n; t += kAttNT) {
-      load_row(t + kAttNT, nxt);
-      float s = 0.0f;
-      if (t == pos) {
-        for (int i = 0; i < hd; i++) s = s + kcur[i] * qs[i];
-      } else {
+      for (int p8 = 0; p8 < 16; p8++)
+        if (p8 < g8) {
+          const uint32_t kw[4] = {kr[p8].x, kr[p8].y, kr[p8].z, kr[p8].w};
 #pragma unroll
-        for (int p8 = 0; p8 < 16; p8++)
-          if (p8 < g8) {
-            const uint32_t kw[4] = {cur[p8].x, cur[p8].y, cur[p8].z, cur[p8].w};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-              s = s + f16_bits_to_f32(kw[j] & 0xffffu) * qs[8 * p8 + 2 * j];
-              s = s + f16_bits_to_f32(kw[j] >> 16) * qs[8 * p8 + 2 * j + 1];
-            }
+          for (int j = 0; j < 4; j++) {
+            s = s + f16_bits_to_f32(kw[j] & 0xffffu) * qs[8 * p8 + 2 * j];
+            s = s + f16_bits_to_f32(kw[j] >> 16) * qs[8 * p8 + 2 * j + 1];
           }
-      }
-      const float a = s * scale;
-      att[t] = a;
-      mx = fmaxf(mx, a);
-#pragma unroll
-      for (int j = 0; j < 16; j++) cur[j] = nxt[j];
+        }
     }
+    const float a = s * scale;
+    att[t] = a;
+    mx = fmaxf(mx, a);
   }
   // the max is order-independent, and the sign of a zero maximum cannot change
   // any exp(v - max)
@@ -453,39 +444,42 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   for (int w = 1; w < kAttNT / 64; w++) mx = fmaxf(mx, red[w]);
   for (int t = tid; t < n; t += kAttNT) att[t] = dev_expf(att[t] - mx);
   __syncthreads();
-  if (tid == 0) red[4] = 1.0f / chain_sum(att, n);
+  if (tid == 0) red[16] = 1.0f / chain_sum(att, n);
   __syncthreads();
-  const float inv = red[4];
+  const float inv = red[16];
   for (int t = tid; t < n; t += kAttNT) att[t] = att[t] * inv;
-  __syncthreads();
-  // position chunks of C; chain lanes tid < hd, the rest produce
-  const int C = kAttProd / hd, nprod = kAttNT - hd, ptid = tid - hd, g8 = hd / 8;
+  // value products: chain waves hold lanes tid < hd, producers the waves after them
+  const int C = att_chunk(hd), CP = C + 4;
+  const int cw = (hd + 63) / 64;
+  const int nprod = kAttNT - 64 * cw, ptid = tid - 64 * cw;
+  const bool producer = ptid >= 0;
+  const int npc = C * g8;  // 16-byte value pieces per chunk (<= 2 * nprod)
   const int nchunks = (n + C - 1) / C;
-  auto produce = [&](int c) {
-    float* pb = prod + (c & 1) * kAttProd;
-    // all of this thread's value loads first, then the products
-    constexpr int kMaxPer = 8;
-    uint4 vr[kMaxPer];
+  // piece idx of a chunk: position idx % C (consecutive lanes, consecutive positions), dims 8 (idx / C) ..
+  auto vload = [&](int c, uint4 r[2]) {
 #pragma unroll
-    for (int j = 0; j < kMaxPer; j++) {
+    for (int j = 0; j < 2; j++) {
       const int idx = ptid + nprod * j;
-      const int tl = idx / g8, i0 = (idx - tl * g8) * 8;
+      const int tl = idx % C, i0 = 8 * (idx / C);
       const int t = c * C + tl;
-      if (idx < C * g8 && t < n && t != pos) vr[j] = *(const uint4*)(vc + base + (size_t)t * kvd + i0);
+      if (idx < npc && t < n && t != pos) r[j] = *(const uint4*)(vc + base + (size_t)t * kvd + i0);
     }
+  };
+  auto vprod = [&](int c, const uint4 r[2]) {
+    float* pb = prod + (c & 1) * kAttProd;
 #pragma unroll
-    for (int j = 0; j < kMaxPer; j++) {
+    for (int j = 0; j < 2; j++) {
       const int idx = ptid + nprod * j;
-      const int tl = idx / g8, i0 = (idx - tl * g8) * 8;
+      const int tl = idx % C, i0 = 8 * (idx / C);
       const int t = c * C + tl;
-      if (idx >= C * g8 || t >= n) continue;
+      if (idx >= npc || t >= n) continue;
       const float a = att[t];
       float vv[8];
       if (t == pos) {
 #pragma unroll
         for (int q = 0; q < 8; q++) vv[q] = vcur[i0 + q];
       } else {
-        const uint32_t vw[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+        const uint32_t vw[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           vv[2 * q] = f16_bits_to_f32(vw[q] & 0xffffu);
@@ -493,20 +487,39 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
         }
       }
 #pragma unroll
-      for (int q = 0; q < 8; q++) pb[tl * hd + i0 + q] = a * vv[q];
+      for (int q = 0; q < 8; q++) pb[(i0 + q) * CP + tl] = a * vv[q];
     }
   };
-  if (tid >= hd) produce(0);
+  uint4 s0[2], s1[2], s2[2];  // value rows of chunks k with k % 3 == 0, 1, 2
+  if (producer) {
+    vload(0, s0);
+    vload(1, s1);
+    vload(2, s2);
+  }
+  __syncthreads();  // att[] normalized
+  if (producer) {
+    vprod(0, s0);
+    vload(3, s0);
+  }
   __syncthreads();
   float o = 0.0f;
-  for (int c = 0; c < nchunks; c++) {
-    if (tid >= hd) {
-      if (c + 1 < nchunks) produce(c + 1);
-    } else {
-      const int cnt = min(C, n - c * C);
-      o = chain_sum_strided(prod + (c & 1) * kAttProd + tid, hd, cnt, o);
+  // chunk cc: the chain lanes add it while the producers fill chunk cc + 1 (from
+  // slot (cc + 1) % 3) and request chunk cc + 4 into that slot
+  auto step = [&](int cc, uint4 slot[2]) {
+    if (producer) {
+      if (cc + 1 < nchunks) {
+        vprod(cc + 1, slot);
+        vload(cc + 4, slot);
+      }
+    } else if (tid < hd) {
+      o = chain_from(prod + (cc & 1) * kAttProd + tid * CP, min(C, n - cc * C), o);
     }
     __syncthreads();
+  };
+  for (int c = 0; c < nchunks; c += 3) {
+    step(c, s1);
+    if (c + 1 < nchunks) step(c + 1, s2);
+    if (c + 2 < nchunks) step(c + 2, s0);
   }
   if (tid < hd) {
     out[(size_t)h * hd + tid] = o;
@@ -810,7 +823,7 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
   m->att_dim = c.n_heads * c.head_dim;
   m->maxd = std::max(std::max(c.dim, m->att_dim), c.ffn_dim);
   m->L.resize(c.n_layers);
-  m->att_lds = ((size_t)((c.ctx + 3) & ~3) + 2 * nrq::kAttProd + 3 * (size_t)c.head_dim + 8) * 4;
+  m->att_lds = ((size_t)((c.ctx + 3) & ~3) + 2 * nrq::kAttProd + 3 * (size_t)c.head_dim + 32) * 4;
   auto bail = [&](hipError_t e, const char* what) {
     nrq::set_last_error((std::string(what) + ": " + hipGetErrorString(e)).c_str());
     nrq_model_destroy(m);
