@@ -125,4 +125,74 @@ __device__ __forceinline__ int rust_f32_to_i32(float f) {
   return (int)f;
 }
 
+// q8::quantize (q8.rs:27-44) of one 32-value block held one value per lane of
+// a 32-lane group: amax over the group, d = f16(amax / 127), round half away
+// from zero, clamp to [-127, 127]. Returns this lane's quant and the f16 bits of d.
+__device__ __forceinline__ int q8_0_lane(float v, uint32_t* d_bits_out) {
+  float amax = fabsf(v);
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+  amax = fmaxf(0.0f, amax);
+  const uint32_t d_bits = f32_to_f16_bits(amax / 127.0f);
+  const float d = f16_bits_to_f32(d_bits);
+  const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+  const float xi = v * inv;
+  const float r = xi >= 0.0f ? xi + 0.5f : xi - 0.5f;
+  int q = rust_f32_to_i32(r);
+  q = q < -127 ? -127 : (q > 127 ? 127 : q);
+  *d_bits_out = d_bits;
+  return q;
+}
+
+// Sequential f32 sum s + a[0] + a[1] + ... + a[n-1], in index order, by
+// one lane: the reference's `s += v` loops. Three banks of four 16-byte LDS
+// loads rotate: a bank is refilled 48 values ahead right after it is added, so
+// the dependent adds rarely wait on a load. a is 16-byte aligned.
+__device__ inline float chain_from(const float* __restrict__ a, int n, float s) {
+  const float4* a4 = (const float4*)a;
+  const int n16 = n >> 4;  // groups of 16 values
+  int g = 0;
+  if (n16 >= 3) {
+    float4 R0[4], R1[4], R2[4];
+    auto ld = [&](float4* R, int gg) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) R[k] = a4[4 * gg + k];
+    };
+    auto add = [&](const float4* R) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        s = s + R[k].x;
+        s = s + R[k].y;
+        s = s + R[k].z;
+        s = s + R[k].w;
+      }
+    };
+    ld(R0, 0);
+    ld(R1, 1);
+    ld(R2, 2);
+    for (; g + 6 <= n16; g += 3) {  // groups g .. g+2 are loaded
+      add(R0);
+      ld(R0, g + 3);
+      add(R1);
+      ld(R1, g + 4);
+      add(R2);
+      ld(R2, g + 5);
+    }
+    // groups g .. g+2 loaded, fewer than three groups left after them
+    add(R0);
+    if (g + 3 < n16) ld(R0, g + 3);
+    add(R1);
+    if (g + 4 < n16) ld(R1, g + 4);
+    add(R2);
+    if (g + 5 < n16) ld(R2, g + 5);
+    if (g + 3 < n16) add(R0);
+    if (g + 4 < n16) add(R1);
+    if (g + 5 < n16) add(R2);
+    g = n16;
+  }
+  for (int i = 16 * g; i < n; i++) s = s + a[i];
+  return s;
+}
+__device__ inline float chain_sum(const float* __restrict__ a, int n) { return chain_from(a, n, 0.0f); }
+
 }  // namespace nrq

@@ -52,6 +52,24 @@ int launch_decode_scalar(int dtype, const MatvecLaunch& L);
 int launch_stream_scalar(int dtype, const MatvecLaunch& L);
 // Scalar-order decode, one lane per block, per-wave LDS streaming (nrq_wstream.hip).
 int launch_wstream_scalar(int dtype, const MatvecLaunch& L);
+// Rmsnorm of x (after x += add when add != null; the sum is written to x_out)
+// and its Q8_0 quantization, fused into one launch of up to three Q8_0 matvecs
+// over that activation (nrq_wstream.hip). n = cols, a multiple of 256 up to
+// 4096; returns NRQ_LAUNCH_TOO_WIDE when the shape is not supported.
+struct NormMatvecLaunch {
+  const float* x;
+  const float* add;
+  float* x_out;
+  const float* norm_w;
+  int n;
+  float eps;
+  int nmat;
+  const void* w[3];
+  float* y[3];
+  int rows[3];
+  void* stream;
+};
+int launch_norm_matvec_q8_0(const NormMatvecLaunch& L);
 int launch_matmul(int dtype, int order, const MatmulLaunch& L);
 // Scalar-order batched matmul on int8 MFMA (nrq_mmq.hip).
 int launch_mmq(int dtype, const MatmulLaunch& L);

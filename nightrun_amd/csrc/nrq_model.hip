@@ -22,6 +22,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/nrq.h"
@@ -194,72 +195,12 @@ __device__ void dev_sincosf(float x, float* sn, float* cs) {
   }
 }
 
-// Sequential f32 sum s + a[0] + a[1] + ... + a[n-1], in index order, by
-// one lane: the reference's `s += v` loops. Three banks of four 16-byte LDS
-// loads rotate: a bank is refilled 48 values ahead right after it is added, so
-// the dependent adds rarely wait on a load. a is 16-byte aligned.
-__device__ float chain_from(const float* __restrict__ a, int n, float s) {
-  const float4* a4 = (const float4*)a;
-  const int n16 = n >> 4;  // groups of 16 values
-  int g = 0;
-  if (n16 >= 3) {
-    float4 R0[4], R1[4], R2[4];
-    auto ld = [&](float4* R, int gg) {
-#pragma unroll
-      for (int k = 0; k < 4; k++) R[k] = a4[4 * gg + k];
-    };
-    auto add = [&](const float4* R) {
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        s = s + R[k].x;
-        s = s + R[k].y;
-        s = s + R[k].z;
-        s = s + R[k].w;
-      }
-    };
-    ld(R0, 0);
-    ld(R1, 1);
-    ld(R2, 2);
-    for (; g + 6 <= n16; g += 3) {  // groups g .. g+2 are loaded
-      add(R0);
-      ld(R0, g + 3);
-      add(R1);
-      ld(R1, g + 4);
-      add(R2);
-      ld(R2, g + 5);
-    }
-    // groups g .. g+2 loaded, fewer than three groups left after them
-    add(R0);
-    if (g + 3 < n16) ld(R0, g + 3);
-    add(R1);
-    if (g + 4 < n16) ld(R1, g + 4);
-    add(R2);
-    if (g + 5 < n16) ld(R2, g + 5);
-    if (g + 3 < n16) add(R0);
-    if (g + 4 < n16) add(R1);
-    if (g + 5 < n16) add(R2);
-    g = n16;
-  }
-  for (int i = 16 * g; i < n; i++) s = s + a[i];
-  return s;
-}
-__device__ float chain_sum(const float* __restrict__ a, int n) { return chain_from(a, n, 0.0f); }
 
-// q8::quantize (q8.rs:27-44) of one 32-value block held one value per lane of
-// a 32-lane group: amax over the group, d = f16(amax/127), round half away,
-// clamp to [-127, 127].
+// One 32-value Q8_0 block held one value per lane of a 32-lane group, written
+// to blk in the BlockQ8_0 layout.
 __device__ __forceinline__ void quant_q8_0_lane(float v, int lane32, uint8_t* __restrict__ blk) {
-  float amax = fabsf(v);
-#pragma unroll
-  for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-  amax = fmaxf(0.0f, amax);
-  const uint32_t d_bits = f32_to_f16_bits(amax / 127.0f);
-  const float d = f16_bits_to_f32(d_bits);
-  const float inv = d > 0.0f ? 1.0f / d : 0.0f;
-  const float xi = v * inv;
-  const float r = xi >= 0.0f ? xi + 0.5f : xi - 0.5f;
-  int q = rust_f32_to_i32(r);
-  q = q < -127 ? -127 : (q > 127 ? 127 : q);
+  uint32_t d_bits;
+  const int q = q8_0_lane(v, &d_bits);
   blk[2 + lane32] = (uint8_t)(int8_t)q;
   if (lane32 == 0) {
     blk[0] = (uint8_t)(d_bits & 0xff);
@@ -668,7 +609,7 @@ struct nrq_model {
   std::vector<Layer> L;
   float* freqs = nullptr;
   uint16_t *kc = nullptr, *vc = nullptr;
-  float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
+  float *x = nullptr, *x2 = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
   float *gate = nullptr, *up = nullptr, *xb2 = nullptr, *logits = nullptr;
   uint8_t *xq = nullptr, *xq2 = nullptr;
   int* ctl = nullptr;
@@ -703,10 +644,10 @@ int matvec(nrq_model* m, const Mat& w, const uint8_t* xq, float* y, int rows, in
             : NRQ_OK;
 }
 
-// Normalize x (after the pending residual `add`), quantize for dtype dt.
-int norm_quant(nrq_model* m, const float* add, const float* w, int dt) {
+// Normalize the residual xr (after xr += add, in place), quantize for dtype dt.
+int norm_quant(nrq_model* m, float* xr, const float* add, const float* w, int dt) {
   const auto& c = m->cfg;
-  hipLaunchKernelGGL(nrq::norm_kernel, dim3(1), dim3(nrq::kNormNT), 0, m->stream, m->x, add, w, c.dim, c.norm_eps,
+  hipLaunchKernelGGL(nrq::norm_kernel, dim3(1), dim3(nrq::kNormNT), 0, m->stream, xr, add, w, c.dim, c.norm_eps,
                      m->xb, dt == NRQ_Q8_0 ? m->xq : nullptr);
   if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: norm launch failed");
   if (dt != NRQ_Q8_0) return quantize_for(m, dt, m->xb, c.dim, m->xq);
@@ -736,6 +677,34 @@ int matvec_group(nrq_model* m, const Mat* const* ws, float* const* ys, const int
   return NRQ_OK;
 }
 
+// Norm + Q8_0 matvecs of one input in a single launch when every matrix is
+// Q8_0: the residual is read from *xr and, with a pending add, the sum goes to
+// *xo and the two buffers swap. Returns 1 when the shapes do not allow it.
+int fused_norm_group(nrq_model* m, float** xr, float** xo, const float* add, const float* normw,
+                     const Mat* const* ws, float* const* ys, const int* rows, int n) {
+  for (int i = 0; i < n; i++)
+    if (ws[i]->dt != NRQ_Q8_0) return 1;
+  nrq::NormMatvecLaunch L{};
+  L.x = *xr;
+  L.add = add;
+  L.x_out = add ? *xo : nullptr;
+  L.norm_w = normw;
+  L.n = m->cfg.dim;
+  L.eps = m->cfg.norm_eps;
+  L.nmat = n;
+  for (int i = 0; i < n; i++) {
+    L.w[i] = ws[i]->w;
+    L.y[i] = ys[i];
+    L.rows[i] = rows[i];
+  }
+  L.stream = m->stream;
+  const int rc = nrq::launch_norm_matvec_q8_0(L);
+  if (rc == nrq::NRQ_LAUNCH_TOO_WIDE) return 1;
+  if (rc) return mfail(NRQ_ERR_DEVICE, "model: norm + matvec launch failed");
+  if (add) std::swap(*xr, *xo);
+  return NRQ_OK;
+}
+
 // One decode step, enqueued on m->stream (infer.rs:510-595 + argmax).
 int enqueue_step(nrq_model* m) {
   const auto& c = m->cfg;
@@ -744,16 +713,22 @@ int enqueue_step(nrq_model* m) {
                      (const uint8_t*)m->embed.w, m->ctl, d, m->x);
   if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: embed launch failed");
   const float scale = 1.0f / sqrtf((float)c.head_dim);
-  const float* pending = nullptr;  // residual not yet added into x
+  const float* pending = nullptr;  // residual not yet added into *xr
+  float* xr = m->x;                // the residual stream
+  float* xo = m->x2;               // where a fused norm writes xr + pending
   int rc;
   for (int l = 0; l < c.n_layers; l++) {
     const Layer& Ly = m->L[l];
-    if ((rc = norm_quant(m, pending, Ly.attn_norm, Ly.m[0].dt))) return rc;
     {
       const Mat* ws[3] = {&Ly.m[0], &Ly.m[1], &Ly.m[2]};
       float* ys[3] = {m->q, m->k, m->v};
       const int rows[3] = {att, kvd, kvd};
-      if ((rc = matvec_group(m, ws, ys, rows, 3, d))) return rc;
+      rc = fused_norm_group(m, &xr, &xo, pending, Ly.attn_norm, ws, ys, rows, 3);
+      if (rc == 1) {
+        if ((rc = norm_quant(m, xr, pending, Ly.attn_norm, Ly.m[0].dt))) return rc;
+        rc = matvec_group(m, ws, ys, rows, 3, d);
+      }
+      if (rc) return rc;
     }
     {
       const bool q8 = Ly.m[3].dt == NRQ_Q8_0;
@@ -764,12 +739,16 @@ int enqueue_step(nrq_model* m) {
       if (!q8 && (rc = quantize_for(m, Ly.m[3].dt, m->attn, att, m->xq))) return rc;
     }
     if ((rc = matvec(m, Ly.m[3], m->xq, m->xb2, d, att))) return rc;
-    if ((rc = norm_quant(m, m->xb2, Ly.ffn_norm, Ly.m[4].dt))) return rc;
     {
       const Mat* ws[2] = {&Ly.m[4], &Ly.m[5]};
       float* ys[2] = {m->gate, m->up};
       const int rows[2] = {ffn, ffn};
-      if ((rc = matvec_group(m, ws, ys, rows, 2, d))) return rc;
+      rc = fused_norm_group(m, &xr, &xo, m->xb2, Ly.ffn_norm, ws, ys, rows, 2);
+      if (rc == 1) {
+        if ((rc = norm_quant(m, xr, m->xb2, Ly.ffn_norm, Ly.m[4].dt))) return rc;
+        rc = matvec_group(m, ws, ys, rows, 2, d);
+      }
+      if (rc) return rc;
     }
     {
       const bool q8 = Ly.m[6].dt == NRQ_Q8_0;
@@ -781,7 +760,7 @@ int enqueue_step(nrq_model* m) {
     if ((rc = matvec(m, Ly.m[6], m->xq, m->xb2, d, ffn))) return rc;
     pending = m->xb2;
   }
-  if ((rc = norm_quant(m, pending, m->out_norm, m->output.dt))) return rc;
+  if ((rc = norm_quant(m, xr, pending, m->out_norm, m->output.dt))) return rc;
   if ((rc = matvec(m, m->output, m->xq, m->logits, c.vocab, d))) return rc;
   hipLaunchKernelGGL(nrq::argmax_kernel, dim3(1), dim3(nrq::kArgNT), 0, m->stream, m->logits, c.vocab, m->ctl,
                      m->out_tokens, m->max_out);
@@ -837,7 +816,7 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
     size_t bytes;
   } allocs[] = {
       {(void**)&m->freqs, (size_t)c.head_dim / 2 * 4}, {(void**)&m->kc, kvn * 2}, {(void**)&m->vc, kvn * 2},
-      {(void**)&m->x, (size_t)c.dim * 4}, {(void**)&m->xb, (size_t)m->maxd * 4},
+      {(void**)&m->x, (size_t)c.dim * 4}, {(void**)&m->x2, (size_t)c.dim * 4}, {(void**)&m->xb, (size_t)m->maxd * 4},
       {(void**)&m->q, (size_t)m->att_dim * 4}, {(void**)&m->k, (size_t)m->kv_dim * 4},
       {(void**)&m->v, (size_t)m->kv_dim * 4}, {(void**)&m->attn, (size_t)m->att_dim * 4},
       {(void**)&m->gate, (size_t)c.ffn_dim * 4}, {(void**)&m->up, (size_t)c.ffn_dim * 4},
@@ -1008,7 +987,7 @@ int nrq_model_destroy(nrq_model* m) {
   if (m->stream) hipStreamSynchronize(m->stream);
   if (m->exec) hipGraphExecDestroy(m->exec);
   if (m->graph) hipGraphDestroy(m->graph);
-  void* bufs[] = {m->freqs, m->kc, m->vc, m->x, m->xb, m->q, m->k, m->v, m->attn, m->gate, m->up, m->xb2,
+  void* bufs[] = {m->freqs, m->kc, m->vc, m->x, m->x2, m->xb, m->q, m->k, m->v, m->attn, m->gate, m->up, m->xb2,
                   m->logits, m->xq, m->xq2, m->ctl, m->out_tokens};
   for (void* p : bufs)
     if (p) hipFree(p);

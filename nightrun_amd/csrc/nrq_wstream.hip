@@ -261,6 +261,23 @@ __device__ __forceinline__ float ws_q6k(const uint32_t* w32, uint32_t o, const u
 
 // LDS layout of one workgroup:
 //   [activation, padded: bpr*XS dwords][raw activation window][per wave: NS stages | u]
+// One launch: up to three matrices that share the activation.
+struct WsArgs {
+  const uint8_t* w[3];
+  float* y[3];
+  int rows[3];
+  int wg_end[3];
+  int nmat;
+  const uint8_t* x;  // activation blocks (no fused norm)
+  // fused norm (Q8_0 weights): residual in, pending residual (or null), their sum
+  // (written by workgroup 0 when nadd != null), norm weight, epsilon
+  const float* nx;
+  const float* nadd;
+  float* nx_out;
+  const float* nw;
+  float eps;
+};
+
 template <int FMT>
 struct WSGeom {
   size_t xl, xraw, stage, u, per_wave, total;
@@ -275,16 +292,33 @@ struct WSGeom {
   }
 };
 
-template <int FMT, int NW, int NS>
-__global__ __launch_bounds__(64 * NW) void wstream_matvec(const uint8_t* __restrict__ W, const uint8_t* __restrict__ X,
-                                                          float* __restrict__ Y, int rows, int bpr, int rpw,
-                                                          int nstages) {
+// Rmsnorm (vec.rs:4-14) after the pending residual add (vec.rs:63-67, scale
+// 1.0), fused into a Q8_0 matvec's prologue: LDS holds x, add and the norm
+// weight (DMA, issued before the weight tiles), then the squares; the result
+// is quantized to Q8_0 (q8.rs:27-44) straight into the activation layout.
+constexpr int kFusedNormMax = 4096;
+constexpr int kFusedNormPT = kFusedNormMax / 256;
+
+__device__ __forceinline__ void ws_dma16_g(const void* g, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(g) : "memory");
+}
+
+template <int FMT, int NW, int NS, bool NORM>
+__global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int rpw, int nstages) {
   using F = WS<FMT>;
-  constexpr int NI = F::NI, BS = F::BS, TBK = 64 * F::BPL, STAGE = NI * 1024;
+  constexpr int NI = F::NI, BS = F::BS, TBK = 64 * F::BPL, STAGE = NI * 1024, NT = 64 * NW;
   static_assert(NS >= 1 && NS <= 4, "the vmcnt waits cover up to 4 stages");
+  static_assert(!NORM || (FMT == kQ8_0 && NW == 4), "the fused norm feeds Q8_0 weights, 256 lanes");
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  // workgroups [wg_end[i-1], wg_end[i]) take matrix i
+  int mi = 0;
+  while (mi + 1 < A.nmat && (int)blockIdx.x >= A.wg_end[mi]) mi++;
+  const int lwg = (int)blockIdx.x - (mi ? A.wg_end[mi - 1] : 0);
+  const uint8_t* __restrict__ W = A.w[mi];
+  float* __restrict__ Y = A.y[mi];
+  const int rows = A.rows[mi];
   const WSGeom<FMT> G(bpr, rpw, nstages, NW);
   uint32_t* xl = (uint32_t*)smem;
   uint8_t* xraw = smem + G.xl;
@@ -292,7 +326,7 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(const uint8_t* __restr
   float* u = (float*)(stages + (size_t)nstages * STAGE);
   const uint32_t stage0 = ws_lds_addr(stages);
 
-  const int row0 = (blockIdx.x * NW + wave) * rpw;
+  const int row0 = (lwg * NW + wave) * rpw;
   const int nr = max(0, min(rpw, rows - row0));
   const int nb = nr * bpr;
   const size_t fbeg = (size_t)max(row0, 0) * bpr;  // first flat block of this wave
@@ -312,9 +346,20 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(const uint8_t* __restr
     }
   };
 
-  // Activation window first, so an in-order vmcnt wait below covers it.
-  {
-    const uintptr_t xa = (uintptr_t)X;
+  // The activation (or the norm's inputs) first, so an in-order vmcnt wait below covers it.
+  float* nxs = (float*)(smem + G.total);  // fused norm: x | add | weight | squares, n floats each
+  const int n = bpr * 32;
+  if constexpr (NORM) {
+    const int nk = n / 256;  // 1 KiB DMAs per array
+    const float* src[3] = {A.nx, A.nadd, A.nw};
+#pragma unroll
+    for (int a = 0; a < 3; a++) {
+      if (a == 1 && !A.nadd) continue;
+      const uint32_t dst = ws_lds_addr(nxs + (size_t)a * n);
+      for (int k = wave; k < nk; k += NW) ws_dma16_g(src[a] + 256 * k + 4 * lane, dst + (uint32_t)k * 1024u);
+    }
+  } else {
+    const uintptr_t xa = (uintptr_t)A.x;
     const uintptr_t xa0 = xa & ~(uintptr_t)15;
     const int n16x = (int)(((((xa + (size_t)bpr * F::XB) + 15) & ~(uintptr_t)15) - xa0) >> 4);
     const uint32_t rbase = ws_lds_addr(xraw);
@@ -334,7 +379,48 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(const uint8_t* __restr
     default: ws_wait_vm<4 * NI>(); break;
   }
   ws_lds_barrier();
-  ws_repack<FMT>((const uint32_t*)xraw, (uint32_t)((uintptr_t)X & 15), bpr, xl, tid, 64 * NW);
+  if constexpr (NORM) {
+    const float* xs = nxs;
+    const float* as = nxs + n;
+    const float* wsn = nxs + 2 * (size_t)n;
+    float* sq = nxs + 3 * (size_t)n;
+    const int cnt = n / NT;
+    float v[kFusedNormPT];
+#pragma unroll
+    for (int k = 0; k < kFusedNormPT; k++)
+      if (k < cnt) {
+        const int i = tid + NT * k;
+        float a = xs[i];
+        if (A.nadd) {
+          a = a + 1.0f * as[i];
+          if (blockIdx.x == 0) A.nx_out[i] = a;
+        }
+        v[k] = a;
+        sq[i] = a * a;
+      }
+    ws_lds_barrier();
+    float* scale_slot = sq + n;  // one float past the squares
+    if (tid == 0) {
+      const float ss = chain_sum(sq, n);
+      scale_slot[0] = 1.0f / sqrtf(ss / (float)n + A.eps);
+    }
+    ws_lds_barrier();
+    const float scale = scale_slot[0];
+    const int lane32 = tid & 31;
+#pragma unroll
+    for (int k = 0; k < kFusedNormPT; k++)
+      if (k < cnt) {
+        const int i = tid + NT * k;
+        const float o = v[k] * scale * wsn[i];
+        uint32_t d_bits;
+        const int q = q8_0_lane(o, &d_bits);
+        uint32_t* xb = xl + (i >> 5) * WS<kQ8_0>::XS;
+        ((uint8_t*)xb)[lane32] = (uint8_t)(int8_t)q;
+        if (lane32 == 0) xb[8] = __float_as_uint(f16_bits_to_f32(d_bits));
+      }
+  } else {
+    ws_repack<FMT>((const uint32_t*)xraw, (uint32_t)((uintptr_t)A.x & 15), bpr, xl, tid, NT);
+  }
   ws_lds_barrier();
 
   // Lane l's k-th block of tile t is flat block fbeg + t*TBK + l + 64k; track its (row, block).
@@ -397,18 +483,26 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(const uint8_t* __restr
 
 // ---- launch ----------------------------------------------------------------------------------
 
-template <int FMT, int NW, int NS>
-static int launch_ws_t(const MatvecLaunch& L, int rpw) {
+template <int FMT, int NW, int NS, bool NORM>
+static int launch_ws_t(WsArgs A, int bpr, int rpw, void* stream) {
   constexpr int TBK = 64 * WS<FMT>::BPL;
-  const int bpr = L.bpr;
-  const long waves = (L.rows + rpw - 1) / rpw;
+  int maxrows = 0, grid = 0;
+  for (int i = 0; i < A.nmat; i++) {
+    const long waves = (A.rows[i] + rpw - 1) / rpw;
+    grid += (int)((waves + NW - 1) / NW);
+    A.wg_end[i] = grid;
+    maxrows = A.rows[i] > maxrows ? A.rows[i] : maxrows;
+  }
+  (void)maxrows;
   const long tiles_per_wave = ((long)rpw * bpr + TBK - 1) / TBK;
   const int nstages = (int)(tiles_per_wave < NS ? tiles_per_wave : NS);
   const WSGeom<FMT> G(bpr, rpw, nstages, NW);
-  if (G.total > 160 * 1024) return NRQ_LAUNCH_TOO_WIDE;
-  const int grid = (int)((waves + NW - 1) / NW);
-  hipLaunchKernelGGL((wstream_matvec<FMT, NW, NS>), dim3(grid), dim3(64 * NW), G.total, (hipStream_t)L.stream,
-                     (const uint8_t*)L.w, (const uint8_t*)L.x, L.y, L.rows, bpr, rpw, nstages);
+  // fused norm: x, add, weight, squares (n floats each) and the scale
+  const size_t lds = G.total + (NORM ? (size_t)4 * bpr * 32 * 4 + 16 : 0);
+  if (lds > 160 * 1024) return NRQ_LAUNCH_TOO_WIDE;
+  if (grid == 0) return 0;
+  hipLaunchKernelGGL((wstream_matvec<FMT, NW, NS, NORM>), dim3(grid), dim3(64 * NW), lds, (hipStream_t)stream, A, bpr,
+                     rpw, nstages);
   return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
 }
 
@@ -438,12 +532,57 @@ static int ws_rows_per_wave(int bpr, int cap) {
 template <int FMT>
 static int launch_ws(const MatvecLaunch& L) {
   const int rpw = ws_rows_per_wave<FMT>(L.bpr, L.tile_rows);
+  WsArgs A{};
+  A.w[0] = (const uint8_t*)L.w;
+  A.y[0] = L.y;
+  A.rows[0] = L.rows;
+  A.nmat = 1;
+  A.x = (const uint8_t*)L.x;
   // NW = 4 waves share one activation copy; NS = 2 (double buffering) keeps a
   // tile in flight per wave while the other is computed, within the LDS of a CU.
-  int rc = launch_ws_t<FMT, 4, 2>(L, rpw);
-  if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2>(L, rpw);
-  if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2>(L, 1);
+  int rc = launch_ws_t<FMT, 4, 2, false>(A, L.bpr, rpw, L.stream);
+  if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, false>(A, L.bpr, rpw, L.stream);
+  if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, false>(A, L.bpr, 1, L.stream);
   return rc;
+}
+
+static int ws_num_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    n = (hipGetDevice(&dev) == hipSuccess &&
+         hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            ? v
+            : 256;
+  }
+  return n;
+}
+
+int launch_norm_matvec_q8_0(const NormMatvecLaunch& L) {
+  if (L.nmat < 1 || L.nmat > 3 || L.n <= 0 || L.n % 256 || L.n > kFusedNormMax) return NRQ_LAUNCH_TOO_WIDE;
+  const int bpr = L.n / 32;
+  // Every workgroup runs the norm's sequential sum once, and its LDS allows one
+  // workgroup per CU, so the launch is sized to one workgroup per CU: rows per
+  // wave grow (in steps that keep the tiles full) until the grid fits.
+  const int rpw0 = ws_rows_per_wave<kQ8_0>(bpr, 0);
+  long total = 0;
+  for (int i = 0; i < L.nmat; i++) total += L.rows[i];
+  const long slots = 4L * ws_num_cus();
+  int rpw = rpw0;
+  while (rpw + rpw0 <= 64 && (total + rpw - 1) / rpw + 3L * L.nmat > slots) rpw += rpw0;
+  WsArgs A{};
+  for (int i = 0; i < L.nmat; i++) {
+    A.w[i] = (const uint8_t*)L.w[i];
+    A.y[i] = L.y[i];
+    A.rows[i] = L.rows[i];
+  }
+  A.nmat = L.nmat;
+  A.nx = L.x;
+  A.nadd = L.add;
+  A.nx_out = L.x_out;
+  A.nw = L.norm_w;
+  A.eps = L.eps;
+  return launch_ws_t<kQ8_0, 4, 2, true>(A, bpr, rpw, L.stream);
 }
 
 int launch_wstream_scalar(int dtype, const MatvecLaunch& L) {
