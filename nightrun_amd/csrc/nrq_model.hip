@@ -214,9 +214,18 @@ enum { CTL_TOKEN = 0, CTL_POS = 1, CTL_STEP = 2, CTL_WORDS = 4 };
 // ---- kernels ------------------------------------------------------------------------
 
 // QMat::dequant_row for Q8_0 (infer.rs:37-42, q8.rs:47-55): x[i] = f32(q) * d
+// Workgroup 0 also writes (cos, sin) of pos * freqs[i] for the step: rope::apply
+// takes sincosf(pos * freq_i) for every head and layer alike (rope.rs:49-65).
 __global__ void embed_q8_0_kernel(const uint8_t* __restrict__ E, const int* __restrict__ ctl, int dim,
-                                  float* __restrict__ x) {
+                                  float* __restrict__ x, const float* __restrict__ freqs, int half,
+                                  float* __restrict__ rope_cs) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (blockIdx.x == 0 && (int)threadIdx.x < half) {
+    float sn, cs;
+    dev_sincosf((float)ctl[CTL_POS] * freqs[threadIdx.x], &sn, &cs);
+    rope_cs[2 * threadIdx.x] = cs;
+    rope_cs[2 * threadIdx.x + 1] = sn;
+  }
   if (i >= dim) return;
   const size_t tok = (size_t)(uint32_t)ctl[CTL_TOKEN];
   const uint8_t* blk = E + (tok * (dim / 32) + i / 32) * kQ8_0Bytes;
@@ -279,19 +288,15 @@ constexpr int kAttNT = 1024;
 constexpr int kAttMaxCtx = 8192;
 constexpr int kAttProd = 8704;  // floats per product stage (head_dim x (chunk + 4) <= 8704)
 
-// Positions per product chunk: a multiple of 64 with head_dim x (chunk + 4) <= kAttProd.
-__host__ __device__ inline int att_chunk(int hd) {
-  const int c = (8192 / hd) & ~63;
-  return c < 64 ? 64 : c;
-}
-
 // One workgroup per query head: the attention block of infer.rs:540-572.
-//  1. The key rows of the first kAttNT positions are requested first (every
-//     row but the current one is already in the cache), then rope::apply
-//     (rope.rs:49-65) on the head's q and on its KV head's k at the current
-//     position, and the KV append as f16 (infer.rs:547-551) by the first query
-//     head of each KV group. The fresh key/value are used from LDS, so the
-//     other heads of the group never read the row being written.
+//  1. Loads first (every key/value row but the current one is already in the
+//     cache): the key rows of this thread's positions (two rounds of kAttNT
+//     positions when they fit in registers) and, in the producer waves, the
+//     value rows of the first three chunks. Then rope::apply (rope.rs:49-65)
+//     on the head's q and its KV head's k with the step's (cos, sin) table, and
+//     the KV append as f16 (infer.rs:547-551) by the first query head of each
+//     KV group. The fresh key/value are used from LDS, so the other heads of
+//     the group never read the row being written.
 //  2. scores: dot_f16(k_t, q) * scale (kernels.rs:146-160, dimension order).
 //  3. softmax (vec.rs:30-42): max, exp, the exp-sum in position order (one
 //     lane), inv, a_t = e_t * inv.
@@ -303,15 +308,25 @@ __host__ __device__ inline int att_chunk(int hd) {
 //  5. out (f32) and, when out_q8 != null, its Q8_0 blocks for the output
 //     projection.
 // LDS: att[ctx] | prod[2][kAttProd] | q[hd] | kcur[hd] | vcur[hd] | red[32]
+template <int HD>
 __global__ __launch_bounds__(kAttNT) void attention_kernel(
     const float* __restrict__ q_in, const float* __restrict__ k_in, const float* __restrict__ v_in,
-    const float* __restrict__ freqs, const int* __restrict__ ctl, int n_heads, int n_kv_heads, int hd, int ctx,
-    int layer, float scale, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, float* __restrict__ out,
+    const float* __restrict__ rope_cs, const int* __restrict__ ctl, int n_heads, int n_kv_heads, int ctx, int layer,
+    float scale, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, float* __restrict__ out,
     uint8_t* __restrict__ out_q8) {
+  constexpr int hd = HD, half = HD / 2, g8 = HD / 8;
+  constexpr int C = (8192 / HD) & ~63 ? (8192 / HD) & ~63 : 64;  // positions per product chunk
+  constexpr int CP = C + 4;
+  static_assert(HD * CP <= kAttProd, "product chunk exceeds its LDS stage");
+  constexpr int cw = (HD + 63) / 64;  // chain waves
+  constexpr int nprod = kAttNT - 64 * cw;
+  constexpr int npc = C * g8;  // 16-byte value pieces per chunk
+  static_assert(npc <= 2 * nprod, "two pieces per producer thread");
+  constexpr bool kTwoRounds = HD <= 64;  // second round of key rows held in registers
   extern __shared__ __align__(16) float sm[];
   const int h = blockIdx.x, tid = threadIdx.x;
   const int pos = ctl[CTL_POS], n = pos + 1;
-  const int gqa = n_heads / n_kv_heads, g = h / gqa, kvd = n_kv_heads * hd, half = hd / 2, g8 = hd / 8;
+  const int gqa = n_heads / n_kv_heads, g = h / gqa, kvd = n_kv_heads * hd;
   const bool writer = (h % gqa) == 0;
   float* att = sm;
   float* prod = sm + ((ctx + 3) & ~3);
@@ -321,19 +336,39 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   float* red = vcur + hd;
   const size_t row = ((size_t)layer * ctx + pos) * kvd + (size_t)g * hd;
   const size_t base = (size_t)layer * ctx * kvd + (size_t)g * hd;
-  uint4 kr[16];  // key row of position tid (16-byte pieces, g8 <= 16 used)
-  auto load_key = [&](int t) {
+  const int ptid = tid - 64 * cw;
+  const bool producer = ptid >= 0;
+  const int nchunks = (n + C - 1) / C;
+
+  uint4 kr[g8], kr2[kTwoRounds ? g8 : 1];
+  auto load_key = [&](int t, uint4* r) {
     if (t < n && t != pos) {
       const uint4* src = (const uint4*)(kc + base + (size_t)t * kvd);
 #pragma unroll
-      for (int j = 0; j < 16; j++)
-        if (j < g8) kr[j] = src[j];
+      for (int j = 0; j < g8; j++) r[j] = src[j];
     }
   };
-  load_key(tid);
+  // value piece idx of a chunk: position idx % C (consecutive lanes, consecutive
+  // positions), dimensions 8 (idx / C) .. + 8
+  auto vload = [&](int c, uint4 r[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int idx = ptid + nprod * j;
+      const int tl = idx % C, i0 = 8 * (idx / C);
+      const int t = c * C + tl;
+      if (idx < npc && t < n && t != pos) r[j] = *(const uint4*)(vc + base + (size_t)t * kvd + i0);
+    }
+  };
+  uint4 s0[2], s1[2], s2[2];  // value rows of chunks k with k % 3 == 0, 1, 2
+  load_key(tid, kr);
+  if constexpr (kTwoRounds) load_key(tid + kAttNT, kr2);
+  if (producer) {
+    vload(0, s0);
+    vload(1, s1);
+    vload(2, s2);
+  }
   for (int i = tid; i < half; i += kAttNT) {
-    float sn, cs;
-    dev_sincosf((float)pos * freqs[i], &sn, &cs);
+    const float cs = rope_cs[2 * i], sn = rope_cs[2 * i + 1];
     const float qa = q_in[(size_t)h * hd + 2 * i], qb = q_in[(size_t)h * hd + 2 * i + 1];
     qs[2 * i] = qa * cs - qb * sn;
     qs[2 * i + 1] = qa * sn + qb * cs;
@@ -354,26 +389,34 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   __syncthreads();
   // Scores: thread tid takes positions tid, tid + kAttNT, ...
   float mx = -INFINITY;
-  for (int t = tid; t < n; t += kAttNT) {
-    if (t != tid) load_key(t);
+  auto score = [&](int t, const uint4* r) {
     float s = 0.0f;
     if (t == pos) {
       for (int i = 0; i < hd; i++) s = s + kcur[i] * qs[i];
     } else {
 #pragma unroll
-      for (int p8 = 0; p8 < 16; p8++)
-        if (p8 < g8) {
-          const uint32_t kw[4] = {kr[p8].x, kr[p8].y, kr[p8].z, kr[p8].w};
+      for (int p8 = 0; p8 < g8; p8++) {
+        const uint32_t kw[4] = {r[p8].x, r[p8].y, r[p8].z, r[p8].w};
 #pragma unroll
-          for (int j = 0; j < 4; j++) {
-            s = s + f16_bits_to_f32(kw[j] & 0xffffu) * qs[8 * p8 + 2 * j];
-            s = s + f16_bits_to_f32(kw[j] >> 16) * qs[8 * p8 + 2 * j + 1];
-          }
+        for (int j = 0; j < 4; j++) {
+          s = s + f16_bits_to_f32(kw[j] & 0xffffu) * qs[8 * p8 + 2 * j];
+          s = s + f16_bits_to_f32(kw[j] >> 16) * qs[8 * p8 + 2 * j + 1];
         }
+      }
     }
     const float a = s * scale;
     att[t] = a;
     mx = fmaxf(mx, a);
+  };
+  if (tid < n) score(tid, kr);
+  int t1 = tid + kAttNT;
+  if constexpr (kTwoRounds) {
+    if (t1 < n) score(t1, kr2);
+    t1 += kAttNT;
+  }
+  for (; t1 < n; t1 += kAttNT) {
+    load_key(t1, kr);
+    score(t1, kr);
   }
   // the max is order-independent, and the sign of a zero maximum cannot change
   // any exp(v - max)
@@ -389,23 +432,6 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   __syncthreads();
   const float inv = red[16];
   for (int t = tid; t < n; t += kAttNT) att[t] = att[t] * inv;
-  // value products: chain waves hold lanes tid < hd, producers the waves after them
-  const int C = att_chunk(hd), CP = C + 4;
-  const int cw = (hd + 63) / 64;
-  const int nprod = kAttNT - 64 * cw, ptid = tid - 64 * cw;
-  const bool producer = ptid >= 0;
-  const int npc = C * g8;  // 16-byte value pieces per chunk (<= 2 * nprod)
-  const int nchunks = (n + C - 1) / C;
-  // piece idx of a chunk: position idx % C (consecutive lanes, consecutive positions), dims 8 (idx / C) ..
-  auto vload = [&](int c, uint4 r[2]) {
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int idx = ptid + nprod * j;
-      const int tl = idx % C, i0 = 8 * (idx / C);
-      const int t = c * C + tl;
-      if (idx < npc && t < n && t != pos) r[j] = *(const uint4*)(vc + base + (size_t)t * kvd + i0);
-    }
-  };
   auto vprod = [&](int c, const uint4 r[2]) {
     float* pb = prod + (c & 1) * kAttProd;
 #pragma unroll
@@ -431,12 +457,6 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
       for (int q = 0; q < 8; q++) pb[(i0 + q) * CP + tl] = a * vv[q];
     }
   };
-  uint4 s0[2], s1[2], s2[2];  // value rows of chunks k with k % 3 == 0, 1, 2
-  if (producer) {
-    vload(0, s0);
-    vload(1, s1);
-    vload(2, s2);
-  }
   __syncthreads();  // att[] normalized
   if (producer) {
     vprod(0, s0);
@@ -608,6 +628,7 @@ struct nrq_model {
   const float* out_norm = nullptr;
   std::vector<Layer> L;
   float* freqs = nullptr;
+  float* rope_cs = nullptr;  // (cos, sin) of the step's position, head_dim floats
   uint16_t *kc = nullptr, *vc = nullptr;
   float *x = nullptr, *x2 = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
   float *gate = nullptr, *up = nullptr, *xb2 = nullptr, *logits = nullptr;
@@ -710,7 +731,7 @@ int enqueue_step(nrq_model* m) {
   const auto& c = m->cfg;
   const int d = c.dim, kvd = m->kv_dim, att = m->att_dim, ffn = c.ffn_dim;
   hipLaunchKernelGGL(nrq::embed_q8_0_kernel, dim3((d + 255) / 256), dim3(256), 0, m->stream,
-                     (const uint8_t*)m->embed.w, m->ctl, d, m->x);
+                     (const uint8_t*)m->embed.w, m->ctl, d, m->x, m->freqs, c.head_dim / 2, m->rope_cs);
   if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: embed launch failed");
   const float scale = 1.0f / sqrtf((float)c.head_dim);
   const float* pending = nullptr;  // residual not yet added into *xr
@@ -732,9 +753,13 @@ int enqueue_step(nrq_model* m) {
     }
     {
       const bool q8 = Ly.m[3].dt == NRQ_Q8_0;
-      hipLaunchKernelGGL(nrq::attention_kernel, dim3(c.n_heads), dim3(nrq::kAttNT), m->att_lds, m->stream, m->q, m->k,
-                         m->v, m->freqs, m->ctl, c.n_heads, c.n_kv_heads, c.head_dim, c.ctx, l, scale, m->kc, m->vc,
-                         m->attn, q8 ? m->xq : nullptr);
+      auto* kern = c.head_dim == 32   ? nrq::attention_kernel<32>
+                   : c.head_dim == 64 ? nrq::attention_kernel<64>
+                   : c.head_dim == 96 ? nrq::attention_kernel<96>
+                                      : nrq::attention_kernel<128>;
+      hipLaunchKernelGGL(kern, dim3(c.n_heads), dim3(nrq::kAttNT), m->att_lds, m->stream, m->q, m->k, m->v,
+                         m->rope_cs, m->ctl, c.n_heads, c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->attn,
+                         q8 ? m->xq : nullptr);
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: attention launch failed");
       if (!q8 && (rc = quantize_for(m, Ly.m[3].dt, m->attn, att, m->xq))) return rc;
     }
@@ -815,7 +840,8 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
     void** p;
     size_t bytes;
   } allocs[] = {
-      {(void**)&m->freqs, (size_t)c.head_dim / 2 * 4}, {(void**)&m->kc, kvn * 2}, {(void**)&m->vc, kvn * 2},
+      {(void**)&m->freqs, (size_t)c.head_dim / 2 * 4}, {(void**)&m->rope_cs, (size_t)c.head_dim * 4},
+      {(void**)&m->kc, kvn * 2}, {(void**)&m->vc, kvn * 2},
       {(void**)&m->x, (size_t)c.dim * 4}, {(void**)&m->x2, (size_t)c.dim * 4}, {(void**)&m->xb, (size_t)m->maxd * 4},
       {(void**)&m->q, (size_t)m->att_dim * 4}, {(void**)&m->k, (size_t)m->kv_dim * 4},
       {(void**)&m->v, (size_t)m->kv_dim * 4}, {(void**)&m->attn, (size_t)m->att_dim * 4},
@@ -987,7 +1013,7 @@ int nrq_model_destroy(nrq_model* m) {
   if (m->stream) hipStreamSynchronize(m->stream);
   if (m->exec) hipGraphExecDestroy(m->exec);
   if (m->graph) hipGraphDestroy(m->graph);
-  void* bufs[] = {m->freqs, m->kc, m->vc, m->x, m->x2, m->xb, m->q, m->k, m->v, m->attn, m->gate, m->up, m->xb2,
+  void* bufs[] = {m->freqs, m->rope_cs, m->kc, m->vc, m->x, m->x2, m->xb, m->q, m->k, m->v, m->attn, m->gate, m->up, m->xb2,
                   m->logits, m->xq, m->xq2, m->ctl, m->out_tokens};
   for (void* p : bufs)
     if (p) hipFree(p);
