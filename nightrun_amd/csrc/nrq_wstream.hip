@@ -26,6 +26,10 @@ namespace nrq {
 
 namespace {
 
+__device__ __forceinline__ void ws_dma4(const void* g, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" : : "s"(m0), "v"(g) : "memory");
+}
+
 __device__ __forceinline__ void ws_dma16(const void* g, uint32_t m0) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(g) : "memory");
 }
@@ -56,7 +60,8 @@ __device__ __forceinline__ uint32_t ws_lds_addr(const void* p) {
 //   XS   activation dwords per block in LDS
 // Activation LDS layouts (dwords):
 //   Q8_0 : [qs 8][d][pad 3]                                    stride 12
-//   Q4_K : [qs 64][bsum pair sums as i16x2: 4][d][pad 15]      stride 84
+//   Q4_K : [qs 64][bsums 8][d][pad 11]                        stride 84
+//          (placed by dword DMA straight from the Q8_K blocks, no repack)
 //   Q6_K : [qs 64][-32 * group sums: 16][d][pad 3]             stride 84
 // Strides 12 and 84 put the blocks read by one instruction on distinct
 // 4-bank groups (84 = 20 mod 64).
@@ -95,18 +100,7 @@ __device__ void ws_repack(const uint32_t* raw, uint32_t xskew, int bpr, uint32_t
     }
     for (int i = tid; i < bpr * 16; i += nt) {
       const int b = i >> 4, g = i & 15;
-      if constexpr (FMT == kQ4K) {
-        if (g < 4) {
-          // sub-blocks 2g, 2g+1: bsums[4g] + bsums[4g+1] | (bsums[4g+2] + bsums[4g+3]) << 16.
-          // Each pair sum is a sum of 32 int8 values, so it fits an i16.
-          const uint32_t v0 = rw[b * 73 + 65 + 2 * g], v1 = rw[b * 73 + 66 + 2 * g];
-          const int s0 = (int)(int16_t)(v0 & 0xffffu) + (int)(int16_t)(v0 >> 16);
-          const int s1 = (int)(int16_t)(v1 & 0xffffu) + (int)(int16_t)(v1 >> 16);
-          xl[b * XS + 64 + g] = ((uint32_t)s0 & 0xffffu) | ((uint32_t)s1 << 16);
-        } else if (g == 4) {
-          xl[b * XS + 68] = rw[b * 73];
-        }
-      } else {
+      if constexpr (FMT == kQ6K) {
         int s = 0;  // -32 * (sum of the group's 16 quants): the (q - 32) term of the scalar dot
 #pragma unroll
         for (int k = 0; k < 4; k++) s = sdot4(rw[b * 73 + 1 + 4 * g + k], 0xe0e0e0e0u, s);
@@ -182,12 +176,17 @@ __device__ __forceinline__ float ws_q4k(const uint8_t* lds_w, uint32_t o, const 
   sum_q = sum_q + (float)__mul24((int)((scB >> 16) & 0xffu), sub[6]);
   sum_q = sum_q + (float)__mul24((int)(scB >> 24), sub[7]);
   // sum_m: m_j zero-extended into i16 pairs, dotted with the i16 pair sums.
-  const u32x4 bs = *(const u32x4*)(xb + 64);
-  int sum_m = sdot2(__builtin_amdgcn_perm(0u, mnA, 0x0c010c00u), bs.x, 0);
-  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnA, 0x0c030c02u), bs.y, sum_m);
-  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnB, 0x0c010c00u), bs.z, sum_m);
-  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnB, 0x0c030c02u), bs.w, sum_m);
-  const float xd = __uint_as_float(xb[68]);
+  // m_j in both i16 halves against the activation's bsums[2j] | bsums[2j+1] << 16
+  const u32x4 b0 = *(const u32x4*)(xb + 64), b1 = *(const u32x4*)(xb + 68);
+  int sum_m = sdot2(__builtin_amdgcn_perm(0u, mnA, 0x0c000c00u), b0.x, 0);
+  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnA, 0x0c010c01u), b0.y, sum_m);
+  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnA, 0x0c020c02u), b0.z, sum_m);
+  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnA, 0x0c030c03u), b0.w, sum_m);
+  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnB, 0x0c000c00u), b1.x, sum_m);
+  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnB, 0x0c010c01u), b1.y, sum_m);
+  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnB, 0x0c020c02u), b1.z, sum_m);
+  sum_m = sdot2(__builtin_amdgcn_perm(0u, mnB, 0x0c030c03u), b1.w, sum_m);
+  const float xd = __uint_as_float(xb[72]);
   const float d_all = f16_bits_to_f32(h.x & 0xffffu) * xd;
   const float dmin_all = f16_bits_to_f32(h.x >> 16) * xd;
   const float a = d_all * sum_q;
@@ -282,9 +281,14 @@ template <int FMT>
 struct WSGeom {
   size_t xl, xraw, stage, u, per_wave, total;
   __host__ __device__ WSGeom(int bpr, int rpw, int ns, int nw) {
-    xl = ((size_t)bpr * WS<FMT>::XS * 4 + 15) & ~(size_t)15;
-    // the DMA writes whole KiB per wave instruction
-    xraw = ((size_t)bpr * WS<FMT>::XB + 15 + 15 + 1023) & ~(size_t)1023;
+    if (FMT == kQ4K) {  // dword DMAs of 64 lanes write whole 256-byte runs
+      xl = ((size_t)bpr * WS<FMT>::XS + 63) / 64 * 256;
+      xraw = 0;
+    } else {
+      xl = ((size_t)bpr * WS<FMT>::XS * 4 + 15) & ~(size_t)15;
+      // the DMA writes whole KiB per wave instruction
+      xraw = ((size_t)bpr * WS<FMT>::XB + 15 + 15 + 1023) & ~(size_t)1023;
+    }
     stage = (size_t)WS<FMT>::NI * 1024;
     u = ((size_t)rpw * bpr * 4 + 15) & ~(size_t)15;
     per_wave = (size_t)ns * stage + u;
@@ -358,6 +362,23 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
       const uint32_t dst = ws_lds_addr(nxs + (size_t)a * n);
       for (int k = wave; k < nk; k += NW) ws_dma16_g(src[a] + 256 * k + 4 * lane, dst + (uint32_t)k * 1024u);
     }
+  } else if constexpr (FMT == kQ4K) {
+    // LDS dword p of the padded layout = dword j = p % 84 of block b = p / 84:
+    // qs and bsums (j < 72) are Q8_K dwords 1 + j, d (j = 72) is dword 0;
+    // padding and the run past the last block load dword 0 of a block.
+    const uint32_t* xw = (const uint32_t*)A.x;
+    const int nins = (bpr * WS<FMT>::XS + 63) / 64;
+    const uint32_t xbase = ws_lds_addr(xl);
+    for (int k = wave; k < nins; k += NW) {
+      const int p = 64 * k + lane;
+      int b = p / WS<FMT>::XS;
+      int j = p - b * WS<FMT>::XS;
+      if (b >= bpr) {
+        b = bpr - 1;
+        j = 72;
+      }
+      ws_dma4(xw + (size_t)b * 73 + (j < 72 ? 1 + j : 0), xbase + (uint32_t)k * 256u);
+    }
   } else {
     const uintptr_t xa = (uintptr_t)A.x;
     const uintptr_t xa0 = xa & ~(uintptr_t)15;
@@ -418,10 +439,11 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
         ((uint8_t*)xb)[lane32] = (uint8_t)(int8_t)q;
         if (lane32 == 0) xb[8] = __float_as_uint(f16_bits_to_f32(d_bits));
       }
-  } else {
+    ws_lds_barrier();
+  } else if constexpr (FMT != kQ4K) {
     ws_repack<FMT>((const uint32_t*)xraw, (uint32_t)((uintptr_t)A.x & 15), bpr, xl, tid, NT);
+    ws_lds_barrier();
   }
-  ws_lds_barrier();
 
   // Lane l's k-th block of tile t is flat block fbeg + t*TBK + l + 64k; track its (row, block).
   int rr[F::BPL], bb[F::BPL];
