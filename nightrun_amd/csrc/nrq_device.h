@@ -195,4 +195,64 @@ __device__ inline float chain_from(const float* __restrict__ a, int n, float s) 
 }
 __device__ inline float chain_sum(const float* __restrict__ a, int n) { return chain_from(a, n, 0.0f); }
 
+// musl scalbnf
+__device__ __forceinline__ float dev_scalbnf(float x, int n) {
+  float y = x;
+  if (n > 127) {
+    y *= __uint_as_float(0x7f000000u);
+    n -= 127;
+    if (n > 127) {
+      y *= __uint_as_float(0x7f000000u);
+      n -= 127;
+      if (n > 127) n = 127;
+    }
+  } else if (n < -126) {
+    y *= __uint_as_float(0x00800000u) * __uint_as_float(0x4b800000u);
+    n += 126 - 24;
+    if (n < -126) {
+      y *= __uint_as_float(0x00800000u) * __uint_as_float(0x4b800000u);
+      n += 126 - 24;
+      if (n < -126) n = -126;
+    }
+  }
+  return y * __uint_as_float((uint32_t)(0x7f + n) << 23);
+}
+
+// musl expf (FreeBSD e_expf.c algorithm): x = k ln2 + r, exp(r) from the
+// two-term Remez form, scaled by 2^k.
+__device__ inline float dev_expf(float x) {
+  const float ln2hi = 6.9314575195e-01f, ln2lo = 1.4286067653e-06f, invln2 = 1.4426950216e+00f;
+  const float P1 = 1.6666625440e-1f, P2 = -2.7667332906e-3f;
+  uint32_t hx = __float_as_uint(x);
+  const int sign = (int)(hx >> 31);
+  hx &= 0x7fffffffu;
+  if (hx >= 0x42aeac50u) {
+    if (hx > 0x7f800000u) return x;
+    if (hx >= 0x42b17218u && !sign) return x * __uint_as_float(0x7f000000u);
+    if (sign && hx >= 0x42cff1b5u) return 0.0f;
+  }
+  int k;
+  float hi, lo;
+  if (hx > 0x3eb17218u) {
+    if (hx > 0x3f851592u)
+      k = (int)(invln2 * x + (sign ? -0.5f : 0.5f));
+    else
+      k = 1 - sign - sign;
+    const float kf = (float)k;
+    hi = x - kf * ln2hi;
+    lo = kf * ln2lo;
+    x = hi - lo;
+  } else if (hx > 0x39000000u) {
+    k = 0;
+    hi = x;
+    lo = 0.0f;
+  } else {
+    return 1.0f + x;
+  }
+  const float xx = x * x;
+  const float c = x - xx * (P1 + xx * P2);
+  const float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
+  return k == 0 ? y : dev_scalbnf(y, k);
+}
+
 }  // namespace nrq

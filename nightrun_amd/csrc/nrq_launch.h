@@ -67,6 +67,9 @@ struct NormMatvecLaunch {
   const void* w[3];
   float* y[3];
   int rows[3];
+  // optional, for a gate|up pair: the Q8_0 blocks of swiglu(gate, up) are
+  // written here (y is then not written); rows a multiple of 32
+  uint8_t* swiglu_q8;
   void* stream;
 };
 int launch_norm_matvec_q8_0(const NormMatvecLaunch& L);

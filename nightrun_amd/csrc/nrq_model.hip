@@ -35,66 +35,6 @@ namespace nrq {
 
 namespace {
 
-// musl scalbnf
-__device__ __forceinline__ float dev_scalbnf(float x, int n) {
-  float y = x;
-  if (n > 127) {
-    y *= __uint_as_float(0x7f000000u);
-    n -= 127;
-    if (n > 127) {
-      y *= __uint_as_float(0x7f000000u);
-      n -= 127;
-      if (n > 127) n = 127;
-    }
-  } else if (n < -126) {
-    y *= __uint_as_float(0x00800000u) * __uint_as_float(0x4b800000u);
-    n += 126 - 24;
-    if (n < -126) {
-      y *= __uint_as_float(0x00800000u) * __uint_as_float(0x4b800000u);
-      n += 126 - 24;
-      if (n < -126) n = -126;
-    }
-  }
-  return y * __uint_as_float((uint32_t)(0x7f + n) << 23);
-}
-
-// musl expf (FreeBSD e_expf.c algorithm): x = k ln2 + r, exp(r) from the
-// two-term Remez form, scaled by 2^k.
-__device__ float dev_expf(float x) {
-  const float ln2hi = 6.9314575195e-01f, ln2lo = 1.4286067653e-06f, invln2 = 1.4426950216e+00f;
-  const float P1 = 1.6666625440e-1f, P2 = -2.7667332906e-3f;
-  uint32_t hx = __float_as_uint(x);
-  const int sign = (int)(hx >> 31);
-  hx &= 0x7fffffffu;
-  if (hx >= 0x42aeac50u) {
-    if (hx > 0x7f800000u) return x;
-    if (hx >= 0x42b17218u && !sign) return x * __uint_as_float(0x7f000000u);
-    if (sign && hx >= 0x42cff1b5u) return 0.0f;
-  }
-  int k;
-  float hi, lo;
-  if (hx > 0x3eb17218u) {
-    if (hx > 0x3f851592u)
-      k = (int)(invln2 * x + (sign ? -0.5f : 0.5f));
-    else
-      k = 1 - sign - sign;
-    const float kf = (float)k;
-    hi = x - kf * ln2hi;
-    lo = kf * ln2lo;
-    x = hi - lo;
-  } else if (hx > 0x39000000u) {
-    k = 0;
-    hi = x;
-    lo = 0.0f;
-  } else {
-    return 1.0f + x;
-  }
-  const float xx = x * x;
-  const float c = x - xx * (P1 + xx * P2);
-  const float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
-  return k == 0 ? y : dev_scalbnf(y, k);
-}
-
 // __sindf / __cosdf: double polynomials on [-pi/4, pi/4]
 __device__ __forceinline__ float dev_sindf(double x) {
   const double S1 = -0x15555554cbac77.0p-55, S2 = 0x111110896efbb2.0p-59;
@@ -702,7 +642,7 @@ int matvec_group(nrq_model* m, const Mat* const* ws, float* const* ys, const int
 // Q8_0: the residual is read from *xr and, with a pending add, the sum goes to
 // *xo and the two buffers swap. Returns 1 when the shapes do not allow it.
 int fused_norm_group(nrq_model* m, float** xr, float** xo, const float* add, const float* normw,
-                     const Mat* const* ws, float* const* ys, const int* rows, int n) {
+                     const Mat* const* ws, float* const* ys, const int* rows, int n, uint8_t* swiglu_q8 = nullptr) {
   for (int i = 0; i < n; i++)
     if (ws[i]->dt != NRQ_Q8_0) return 1;
   nrq::NormMatvecLaunch L{};
@@ -718,6 +658,7 @@ int fused_norm_group(nrq_model* m, float** xr, float** xo, const float* add, con
     L.y[i] = ys[i];
     L.rows[i] = rows[i];
   }
+  L.swiglu_q8 = swiglu_q8;
   L.stream = m->stream;
   const int rc = nrq::launch_norm_matvec_q8_0(L);
   if (rc == nrq::NRQ_LAUNCH_TOO_WIDE) return 1;
@@ -740,6 +681,7 @@ int enqueue_step(nrq_model* m) {
   int rc;
   for (int l = 0; l < c.n_layers; l++) {
     const Layer& Ly = m->L[l];
+    bool swiglu_done = false;
     {
       const Mat* ws[3] = {&Ly.m[0], &Ly.m[1], &Ly.m[2]};
       float* ys[3] = {m->q, m->k, m->v};
@@ -768,14 +710,19 @@ int enqueue_step(nrq_model* m) {
       const Mat* ws[2] = {&Ly.m[4], &Ly.m[5]};
       float* ys[2] = {m->gate, m->up};
       const int rows[2] = {ffn, ffn};
-      rc = fused_norm_group(m, &xr, &xo, m->xb2, Ly.ffn_norm, ws, ys, rows, 2);
+      // with a Q8_0 down projection the same launch also applies swiglu and
+      // quantizes its input
+      const bool sw = Ly.m[6].dt == NRQ_Q8_0;
+      rc = fused_norm_group(m, &xr, &xo, m->xb2, Ly.ffn_norm, ws, ys, rows, 2, sw ? m->xq : nullptr);
+      if (rc == 1 && sw) rc = fused_norm_group(m, &xr, &xo, m->xb2, Ly.ffn_norm, ws, ys, rows, 2);
+      else if (rc == 0 && sw) swiglu_done = true;
       if (rc == 1) {
         if ((rc = norm_quant(m, xr, m->xb2, Ly.ffn_norm, Ly.m[4].dt))) return rc;
         rc = matvec_group(m, ws, ys, rows, 2, d);
       }
       if (rc) return rc;
     }
-    {
+    if (!swiglu_done) {
       const bool q8 = Ly.m[6].dt == NRQ_Q8_0;
       hipLaunchKernelGGL(nrq::swiglu_kernel, dim3((ffn + 255) / 256), dim3(256), 0, m->stream, m->gate, m->up, ffn,
                          q8 ? m->xq : nullptr);

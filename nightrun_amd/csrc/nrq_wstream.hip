@@ -275,6 +275,10 @@ struct WsArgs {
   float* nx_out;
   const float* nw;
   float eps;
+  // gate|up pair (nmat == 2, equal rows, multiple of 32): workgroup w computes
+  // rows 32w .. 32w+31 of both (waves 0-1 gate, 2-3 up) and writes the Q8_0
+  // blocks of swiglu(gate, up) (vec.rs:45-52, q8.rs:27-44) instead of y
+  uint8_t* swiglu_q8;
 };
 
 template <int FMT>
@@ -316,10 +320,14 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  // workgroups [wg_end[i-1], wg_end[i]) take matrix i
+  // workgroups [wg_end[i-1], wg_end[i]) take matrix i (the swiglu pair: waves 0-1 and 2-3)
   int mi = 0;
-  while (mi + 1 < A.nmat && (int)blockIdx.x >= A.wg_end[mi]) mi++;
-  const int lwg = (int)blockIdx.x - (mi ? A.wg_end[mi - 1] : 0);
+  if (A.swiglu_q8) {
+    mi = wave >> 1;
+  } else {
+    while (mi + 1 < A.nmat && (int)blockIdx.x >= A.wg_end[mi]) mi++;
+  }
+  const int lwg = A.swiglu_q8 ? 0 : (int)blockIdx.x - (mi ? A.wg_end[mi - 1] : 0);
   const uint8_t* __restrict__ W = A.w[mi];
   float* __restrict__ Y = A.y[mi];
   const int rows = A.rows[mi];
@@ -330,7 +338,7 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
   float* u = (float*)(stages + (size_t)nstages * STAGE);
   const uint32_t stage0 = ws_lds_addr(stages);
 
-  const int row0 = (lwg * NW + wave) * rpw;
+  const int row0 = A.swiglu_q8 ? (int)blockIdx.x * 2 * rpw + (wave & 1) * rpw : (lwg * NW + wave) * rpw;
   const int nr = max(0, min(rpw, rows - row0));
   const int nb = nr * bpr;
   const size_t fbeg = (size_t)max(row0, 0) * bpr;  // first flat block of this wave
@@ -496,10 +504,30 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
   ws_wait_lgkm0();
   asm volatile("" ::: "memory");
   // the reference's `sumf += contribution` chain, block order
+  float s = 0.0f;
   if (lane < nr) {
-    float s = 0.0f;
     for (int b = 0; b < bpr; b++) s = s + u[b * rpw + lane];
-    Y[row0 + lane] = s;
+    if (!A.swiglu_q8) Y[row0 + lane] = s;
+  }
+  if (A.swiglu_q8) {
+    // gate rows land in gu[0 .. 2 rpw), up rows in gu[2 rpw .. 4 rpw) (rpw = 16)
+    float* gu = (float*)xl;  // the activation is no longer read
+    ws_lds_barrier();
+    if (lane < rpw) gu[(wave >> 1) * 2 * rpw + (wave & 1) * rpw + lane] = s;
+    ws_lds_barrier();
+    if (tid < 2 * rpw) {
+      const float gv = gu[tid], uv = gu[2 * rpw + tid];
+      const float silu = gv / (1.0f + dev_expf(-gv));
+      const float v = silu * uv;
+      uint32_t d_bits;
+      const int q = q8_0_lane(v, &d_bits);
+      uint8_t* blk = A.swiglu_q8 + (size_t)blockIdx.x * kQ8_0Bytes;
+      blk[2 + tid] = (uint8_t)(int8_t)q;
+      if (tid == 0) {
+        blk[0] = (uint8_t)(d_bits & 0xff);
+        blk[1] = (uint8_t)(d_bits >> 8);
+      }
+    }
   }
 }
 
@@ -508,14 +536,17 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
 template <int FMT, int NW, int NS, bool NORM>
 static int launch_ws_t(WsArgs A, int bpr, int rpw, void* stream) {
   constexpr int TBK = 64 * WS<FMT>::BPL;
-  int maxrows = 0, grid = 0;
-  for (int i = 0; i < A.nmat; i++) {
-    const long waves = (A.rows[i] + rpw - 1) / rpw;
-    grid += (int)((waves + NW - 1) / NW);
-    A.wg_end[i] = grid;
-    maxrows = A.rows[i] > maxrows ? A.rows[i] : maxrows;
+  int grid = 0;
+  if (A.swiglu_q8) {
+    grid = A.rows[0] / (2 * rpw);
+    A.wg_end[0] = A.wg_end[1] = grid;
+  } else {
+    for (int i = 0; i < A.nmat; i++) {
+      const long waves = (A.rows[i] + rpw - 1) / rpw;
+      grid += (int)((waves + NW - 1) / NW);
+      A.wg_end[i] = grid;
+    }
   }
-  (void)maxrows;
   const long tiles_per_wave = ((long)rpw * bpr + TBK - 1) / TBK;
   const int nstages = (int)(tiles_per_wave < NS ? tiles_per_wave : NS);
   const WSGeom<FMT> G(bpr, rpw, nstages, NW);
@@ -592,6 +623,10 @@ int launch_norm_matvec_q8_0(const NormMatvecLaunch& L) {
   const long slots = 4L * ws_num_cus();
   int rpw = rpw0;
   while (rpw + rpw0 <= 64 && (total + rpw - 1) / rpw + 3L * L.nmat > slots) rpw += rpw0;
+  if (L.swiglu_q8) {  // 16 rows per wave: a workgroup owns 32 rows of gate and of up
+    if (L.nmat != 2 || L.rows[0] != L.rows[1] || L.rows[0] % 32) return NRQ_LAUNCH_TOO_WIDE;
+    rpw = 16;
+  }
   WsArgs A{};
   for (int i = 0; i < L.nmat; i++) {
     A.w[i] = (const uint8_t*)L.w[i];
@@ -604,6 +639,7 @@ int launch_norm_matvec_q8_0(const NormMatvecLaunch& L) {
   A.nx_out = L.x_out;
   A.nw = L.norm_w;
   A.eps = L.eps;
+  A.swiglu_q8 = L.swiglu_q8;
   return launch_ws_t<kQ8_0, 4, 2, true>(A, bpr, rpw, L.stream);
 }
 
