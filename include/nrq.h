@@ -163,7 +163,7 @@ typedef struct {
 /* InferCtx::new (infer.rs:352-492): device KV cache, scratch, rope table. */
 int nrq_model_create(const nrq_model_config *cfg, nrq_model **out);
 /* Binds one tensor already in HBM (matrices Q8_0/Q4_K/Q6_K in their block
- * layout, 16-byte aligned; norms NRQ_F32). The output head is tied to the
+ * layout; norms NRQ_F32; every tensor 16-byte aligned). The output head is tied to the
  * embedding until an NRQ_TENSOR_OUTPUT is set (infer.rs:415-419). The
  * embedding must be Q8_0. */
 int nrq_model_set_tensor(nrq_model *m, int kind, int layer, int dtype, const void *dev_ptr);

@@ -129,9 +129,14 @@ __device__ __forceinline__ int rust_f32_to_i32(float f) {
 // a 32-lane group: amax over the group, d = f16(amax / 127), round half away
 // from zero, clamp to [-127, 127]. Returns this lane's quant and the f16 bits of d.
 __device__ __forceinline__ int q8_0_lane(float v, uint32_t* d_bits_out) {
+  // max over quads (DPP quad_perm), then over each 16-lane row (DPP row_ror
+  // 4 and 8), then across the two rows of the group: max is exact in any order
   float amax = fabsf(v);
-#pragma unroll
-  for (int m = 16; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+  amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0xB1, 0xF, 0xF, false)));
+  amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0x4E, 0xF, 0xF, false)));
+  amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0x124, 0xF, 0xF, false)));
+  amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0x128, 0xF, 0xF, false)));
+  amax = fmaxf(amax, __shfl_xor(amax, 16, 32));
   amax = fmaxf(0.0f, amax);
   const uint32_t d_bits = f32_to_f16_bits(amax / 127.0f);
   const float d = f16_bits_to_f32(d_bits);
@@ -142,6 +147,52 @@ __device__ __forceinline__ int q8_0_lane(float v, uint32_t* d_bits_out) {
   q = q < -127 ? -127 : (q > 127 ? 127 : q);
   *d_bits_out = d_bits;
   return q;
+}
+
+// q8::quantize (q8.rs:27-44) of one 32-value block held as eight consecutive
+// values in each lane of an aligned lane quad (lane & 3 = eighth of the block).
+// The block amax is exact in any order, so a quad DPP max reduction gives the
+// reference's value. Returns the eight quants packed little-endian in two
+// dwords and the f16 bits of d.
+__device__ __forceinline__ float dpp_quad_xor1(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+}
+__device__ __forceinline__ float dpp_quad_xor2(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+}
+// Max over the 64 lanes of a wave (every lane active), in every lane: DPP
+// within quads and 16-lane rows, then two cross-row exchanges. fmaxf is
+// exact and ignores NaN in any order.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_quad_xor1(v));
+  v = fmaxf(v, dpp_quad_xor2(v));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ void q8_0_quad8(const float o[8], uint32_t* lo, uint32_t* hi, uint32_t* d_bits_out) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(o[e]));
+  amax = fmaxf(amax, dpp_quad_xor1(amax));
+  amax = fmaxf(amax, dpp_quad_xor2(amax));
+  const uint32_t d_bits = f32_to_f16_bits(amax / 127.0f);
+  const float d = f16_bits_to_f32(d_bits);
+  const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float xi = o[e] * inv;
+    const float r = xi >= 0.0f ? xi + 0.5f : xi - 0.5f;
+    int q = rust_f32_to_i32(r);
+    q = q < -127 ? -127 : (q > 127 ? 127 : q);
+    w[e >> 2] |= ((uint32_t)q & 0xffu) << (8 * (e & 3));
+  }
+  *lo = w[0];
+  *hi = w[1];
+  *d_bits_out = d_bits;
 }
 
 // Sequential f32 sum s + a[0] + a[1] + ... + a[n-1], in index order, by
@@ -194,6 +245,68 @@ __device__ inline float chain_from(const float* __restrict__ a, int n, float s) 
   return s;
 }
 __device__ inline float chain_sum(const float* __restrict__ a, int n) { return chain_from(a, n, 0.0f); }
+
+// The same sequential sum, s + a[0] + ... + a[n-1] in index order, run by a
+// whole wave (all 64 lanes active, a in LDS, 4-byte aligned); the result is
+// valid in lane 0. Lanes 0-15 load 16 consecutive values into one VGPR and
+// lane 0 adds them in order, reading lane k through a DPP row shift
+// (row_shl:k). Eight such VGPRs keep 128 values in flight ahead of the adds.
+// The first n & ~127 values take this path, the rest a plain loop.
+#define NRQ_DPP_ADD(b, k) "v_add_f32_dpp %0, %" #b ", %0 row_shl:" #k " row_mask:0xf bank_mask:0xf\n"
+#define NRQ_DPP_ADD16(b)                                                                                 \
+  "v_add_f32_e32 %0, %" #b ", %0\n" NRQ_DPP_ADD(b, 1) NRQ_DPP_ADD(b, 2) NRQ_DPP_ADD(b, 3) NRQ_DPP_ADD(b, 4) \
+      NRQ_DPP_ADD(b, 5) NRQ_DPP_ADD(b, 6) NRQ_DPP_ADD(b, 7) NRQ_DPP_ADD(b, 8) NRQ_DPP_ADD(b, 9)              \
+          NRQ_DPP_ADD(b, 10) NRQ_DPP_ADD(b, 11) NRQ_DPP_ADD(b, 12) NRQ_DPP_ADD(b, 13) NRQ_DPP_ADD(b, 14)     \
+              NRQ_DPP_ADD(b, 15)
+#define NRQ_DPP_LD(b, off) "ds_read_b32 %" #b ", %10 offset:" #off "\n"
+__device__ inline float wave_chain_from(const float* __restrict__ a, int n, float s) {
+  const int n128 = n & ~127;
+  if (n128 > 0) {
+    uint32_t addr = (uint32_t)(uintptr_t)a + 4u * (uint32_t)(threadIdx.x & 15);
+    int iters = __builtin_amdgcn_readfirstlane(n128 >> 7);
+    float b0, b1, b2, b3, b4, b5, b6, b7;
+    // Iteration i adds values 128i .. 128i+127 (VGPR b holds 128i + 16b + lane)
+    // and, unless it is the last, refills each VGPR for iteration i + 1 right
+    // after adding it; LDS reads return in order, so lgkmcnt(7) means the
+    // oldest of the eight outstanding reads has landed.
+    asm volatile(
+        NRQ_DPP_LD(1, 0) NRQ_DPP_LD(2, 64) NRQ_DPP_LD(3, 128) NRQ_DPP_LD(4, 192) NRQ_DPP_LD(5, 256)
+            NRQ_DPP_LD(6, 320) NRQ_DPP_LD(7, 384) NRQ_DPP_LD(8, 448)
+        "s_nop 4\n"
+        "1:\n"
+        "s_sub_u32 %9, %9, 1\n"
+        "s_cmp_eq_u32 %9, 0\n"
+        "s_cbranch_scc1 2f\n"
+        "s_waitcnt lgkmcnt(7)\n" NRQ_DPP_ADD16(1) NRQ_DPP_LD(1, 512)
+        "s_waitcnt lgkmcnt(7)\n" NRQ_DPP_ADD16(2) NRQ_DPP_LD(2, 576)
+        "s_waitcnt lgkmcnt(7)\n" NRQ_DPP_ADD16(3) NRQ_DPP_LD(3, 640)
+        "s_waitcnt lgkmcnt(7)\n" NRQ_DPP_ADD16(4) NRQ_DPP_LD(4, 704)
+        "s_waitcnt lgkmcnt(7)\n" NRQ_DPP_ADD16(5) NRQ_DPP_LD(5, 768)
+        "s_waitcnt lgkmcnt(7)\n" NRQ_DPP_ADD16(6) NRQ_DPP_LD(6, 832)
+        "s_waitcnt lgkmcnt(7)\n" NRQ_DPP_ADD16(7) NRQ_DPP_LD(7, 896)
+        "s_waitcnt lgkmcnt(7)\n" NRQ_DPP_ADD16(8) NRQ_DPP_LD(8, 960)
+        "v_add_u32_e32 %10, 0x200, %10\n"
+        "s_branch 1b\n"
+        "2:\n"
+        "s_waitcnt lgkmcnt(7)\n" NRQ_DPP_ADD16(1)
+        "s_waitcnt lgkmcnt(6)\n" NRQ_DPP_ADD16(2)
+        "s_waitcnt lgkmcnt(5)\n" NRQ_DPP_ADD16(3)
+        "s_waitcnt lgkmcnt(4)\n" NRQ_DPP_ADD16(4)
+        "s_waitcnt lgkmcnt(3)\n" NRQ_DPP_ADD16(5)
+        "s_waitcnt lgkmcnt(2)\n" NRQ_DPP_ADD16(6)
+        "s_waitcnt lgkmcnt(1)\n" NRQ_DPP_ADD16(7)
+        "s_waitcnt lgkmcnt(0)\n" NRQ_DPP_ADD16(8)
+        : "+v"(s), "=&v"(b0), "=&v"(b1), "=&v"(b2), "=&v"(b3), "=&v"(b4), "=&v"(b5), "=&v"(b6), "=&v"(b7),
+          "+s"(iters), "+v"(addr)
+        :
+        : "memory", "scc");
+  }
+  for (int i = n128; i < n; i++) s = s + a[i];
+  return s;
+}
+#undef NRQ_DPP_LD
+#undef NRQ_DPP_ADD16
+#undef NRQ_DPP_ADD
 
 // musl scalbnf
 __device__ __forceinline__ float dev_scalbnf(float x, int n) {

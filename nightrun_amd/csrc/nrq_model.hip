@@ -181,47 +181,80 @@ constexpr int kNormPT = kNormMax / kNormNT;  // values per thread
 // rmsnorm (vec.rs:4-14): ss += v*v in element order, scale = 1/sqrtf(ss/n + eps),
 // out = x * scale * w. Writes out (f32) and, when xq != null, its Q8_0 blocks
 // (q8.rs:27-44). One workgroup; n <= kNormMax, a multiple of 256. Thread t
-// owns elements t + 256k, loaded once, all loads issued before the first use.
+// owns the 8-value runs t + 256k (four consecutive runs, an aligned lane quad,
+// make one Q8_0 block), loaded once, all loads issued before the first use;
+// wave 0 runs the sequential sum of squares.
 __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, const float* __restrict__ add,
                                                        const float* __restrict__ w, int n, float eps,
                                                        float* __restrict__ out, uint8_t* __restrict__ xq) {
   __shared__ __align__(16) float sq[kNormMax];
   __shared__ float s_scale;
   const int tid = threadIdx.x;
-  const int cnt = n / kNormNT;
-  float v[kNormPT], a[kNormPT], wv[kNormPT];
+  const int nrun = n >> 3;
+  constexpr int RK = kNormPT / 8;  // runs per thread
+  float4 v[2 * RK], a[2 * RK], wv[2 * RK];
 #pragma unroll
-  for (int k = 0; k < kNormPT; k++)
-    if (k < cnt) {
-      v[k] = x[tid + kNormNT * k];
-      wv[k] = w[tid + kNormNT * k];
-      a[k] = add ? add[tid + kNormNT * k] : 0.0f;
-    }
-#pragma unroll
-  for (int k = 0; k < kNormPT; k++)
-    if (k < cnt) {
+  for (int k = 0; k < RK; k++) {
+    const int j = tid + kNormNT * k;
+    if (j < nrun) {
+      v[2 * k] = ((const float4*)x)[2 * j];
+      v[2 * k + 1] = ((const float4*)x)[2 * j + 1];
+      wv[2 * k] = ((const float4*)w)[2 * j];
+      wv[2 * k + 1] = ((const float4*)w)[2 * j + 1];
       if (add) {
-        v[k] = v[k] + 1.0f * a[k];
-        x[tid + kNormNT * k] = v[k];
+        a[2 * k] = ((const float4*)add)[2 * j];
+        a[2 * k + 1] = ((const float4*)add)[2 * j + 1];
       }
-      sq[tid + kNormNT * k] = v[k] * v[k];
     }
+  }
+#pragma unroll
+  for (int k = 0; k < RK; k++) {
+    const int j = tid + kNormNT * k;
+    if (j < nrun) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        float4& p = v[2 * k + h];
+        if (add) {
+          const float4 q = a[2 * k + h];
+          p.x = p.x + 1.0f * q.x;
+          p.y = p.y + 1.0f * q.y;
+          p.z = p.z + 1.0f * q.z;
+          p.w = p.w + 1.0f * q.w;
+          ((float4*)x)[2 * j + h] = p;
+        }
+        ((float4*)sq)[2 * j + h] = make_float4(p.x * p.x, p.y * p.y, p.z * p.z, p.w * p.w);
+      }
+    }
+  }
   __syncthreads();
-  if (tid == 0) {
-    const float ss = chain_sum(sq, n);
-    s_scale = 1.0f / sqrtf(ss / (float)n + eps);
+  if (tid < 64) {
+    const float ss = wave_chain_from(sq, n, 0.0f);
+    if (tid == 0) s_scale = 1.0f / sqrtf(ss / (float)n + eps);
   }
   __syncthreads();
   const float scale = s_scale;
-  const int lane32 = tid & 31;
 #pragma unroll
-  for (int k = 0; k < kNormPT; k++)
-    if (k < cnt) {
-      const int i = tid + kNormNT * k;
-      const float o = v[k] * scale * wv[k];
-      out[i] = o;
-      if (xq) quant_q8_0_lane(o, lane32, xq + (size_t)(i >> 5) * kQ8_0Bytes);
+  for (int k = 0; k < RK; k++) {
+    const int j = tid + kNormNT * k;
+    if (j < nrun) {
+      const float4 p0 = v[2 * k], p1 = v[2 * k + 1], w0 = wv[2 * k], w1 = wv[2 * k + 1];
+      float o[8] = {p0.x * scale * w0.x, p0.y * scale * w0.y, p0.z * scale * w0.z, p0.w * scale * w0.w,
+                    p1.x * scale * w1.x, p1.y * scale * w1.y, p1.z * scale * w1.z, p1.w * scale * w1.w};
+      ((float4*)out)[2 * j] = make_float4(o[0], o[1], o[2], o[3]);
+      ((float4*)out)[2 * j + 1] = make_float4(o[4], o[5], o[6], o[7]);
+      if (xq) {
+        uint32_t lo, hi, d_bits;
+        q8_0_quad8(o, &lo, &hi, &d_bits);
+        uint8_t* blk = xq + (size_t)(j >> 2) * kQ8_0Bytes;
+        uint16_t* qs = (uint16_t*)(blk + 2 + 8 * (j & 3));  // 2-byte aligned
+        qs[0] = (uint16_t)lo;
+        qs[1] = (uint16_t)(lo >> 16);
+        qs[2] = (uint16_t)hi;
+        qs[3] = (uint16_t)(hi >> 16);
+        if ((j & 3) == 0) *(uint16_t*)blk = (uint16_t)d_bits;
+      }
     }
+  }
 }
 
 constexpr int kAttNT = 1024;
@@ -360,15 +393,17 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   }
   // the max is order-independent, and the sign of a zero maximum cannot change
   // any exp(v - max)
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  mx = wave_max(mx);
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
   mx = red[0];
   for (int w = 1; w < kAttNT / 64; w++) mx = fmaxf(mx, red[w]);
   for (int t = tid; t < n; t += kAttNT) att[t] = dev_expf(att[t] - mx);
   __syncthreads();
-  if (tid == 0) red[16] = 1.0f / chain_sum(att, n);
+  if (tid < 64) {
+    const float tot = wave_chain_from(att, n, 0.0f);
+    if (tid == 0) red[16] = 1.0f / tot;
+  }
   __syncthreads();
   const float inv = red[16];
   for (int t = tid; t < n; t += kAttNT) att[t] = att[t] * inv;
@@ -818,6 +853,7 @@ int nrq_model_set_tensor(nrq_model* m, int kind, int layer, int dtype, const voi
   const bool is_norm = kind == NRQ_TENSOR_ATTN_NORM || kind == NRQ_TENSOR_FFN_NORM || kind == NRQ_TENSOR_OUTPUT_NORM;
   if (is_norm) {
     if (dtype != NRQ_F32) return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: norms are f32");
+    if (((uintptr_t)dev_ptr & 15) != 0) return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: norm not 16-byte aligned");
   } else {
     if (dtype != NRQ_Q8_0 && dtype != NRQ_Q4_K && dtype != NRQ_Q6_K)
       return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: unknown matrix dtype");

@@ -281,6 +281,12 @@ struct WsArgs {
   uint8_t* swiglu_q8;
 };
 
+// Block contributions of a wave's rows wait in LDS for the per-row sum. Long
+// rows (48+ blocks) are stored row-major with a padded stride, so each lane
+// sums its own row with 16-byte pipelined reads; short rows block-major.
+__host__ __device__ inline bool ws_u_rowmajor(int bpr) { return bpr >= 48; }
+__host__ __device__ inline int ws_u_stride(int bpr) { return ((bpr + 3) & ~3) + 4; }
+
 template <int FMT>
 struct WSGeom {
   size_t xl, xraw, stage, u, per_wave, total;
@@ -294,7 +300,7 @@ struct WSGeom {
       xraw = ((size_t)bpr * WS<FMT>::XB + 15 + 15 + 1023) & ~(size_t)1023;
     }
     stage = (size_t)WS<FMT>::NI * 1024;
-    u = ((size_t)rpw * bpr * 4 + 15) & ~(size_t)15;
+    u = (((size_t)rpw * (ws_u_rowmajor(bpr) ? ws_u_stride(bpr) : bpr)) * 4 + 15) & ~(size_t)15;
     per_wave = (size_t)ns * stage + u;
     total = xl + xraw + (size_t)nw * per_wave;
   }
@@ -413,40 +419,59 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
     const float* as = nxs + n;
     const float* wsn = nxs + 2 * (size_t)n;
     float* sq = nxs + 3 * (size_t)n;
-    const int cnt = n / NT;
+    // Thread t owns the 8-value runs j = t + NT*k; four consecutive runs (an
+    // aligned lane quad) make one Q8_0 block.
+    const int nrun = n >> 3;
+    const float4* xs4 = (const float4*)xs;
+    const float4* as4 = (const float4*)as;
+    const float4* ws4 = (const float4*)wsn;
     float v[kFusedNormPT];
 #pragma unroll
-    for (int k = 0; k < kFusedNormPT; k++)
-      if (k < cnt) {
-        const int i = tid + NT * k;
-        float a = xs[i];
+    for (int k = 0; k < kFusedNormPT / 8; k++) {
+      const int j = tid + NT * k;
+      if (j < nrun) {
+        const float4 p0 = xs4[2 * j], p1 = xs4[2 * j + 1];
+        float a[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
         if (A.nadd) {
-          a = a + 1.0f * as[i];
-          if (blockIdx.x == 0) A.nx_out[i] = a;
+          const float4 q0 = as4[2 * j], q1 = as4[2 * j + 1];
+          const float b[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+          for (int e = 0; e < 8; e++) a[e] = a[e] + 1.0f * b[e];
+          if (blockIdx.x == 0) {
+            ((float4*)A.nx_out)[2 * j] = make_float4(a[0], a[1], a[2], a[3]);
+            ((float4*)A.nx_out)[2 * j + 1] = make_float4(a[4], a[5], a[6], a[7]);
+          }
         }
-        v[k] = a;
-        sq[i] = a * a;
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[8 * k + e] = a[e];
+        ((float4*)sq)[2 * j] = make_float4(a[0] * a[0], a[1] * a[1], a[2] * a[2], a[3] * a[3]);
+        ((float4*)sq)[2 * j + 1] = make_float4(a[4] * a[4], a[5] * a[5], a[6] * a[6], a[7] * a[7]);
       }
+    }
     ws_lds_barrier();
     float* scale_slot = sq + n;  // one float past the squares
-    if (tid == 0) {
-      const float ss = chain_sum(sq, n);
-      scale_slot[0] = 1.0f / sqrtf(ss / (float)n + A.eps);
+    if (wave == 0) {
+      const float ss = wave_chain_from(sq, n, 0.0f);
+      if (lane == 0) scale_slot[0] = 1.0f / sqrtf(ss / (float)n + A.eps);
     }
     ws_lds_barrier();
     const float scale = scale_slot[0];
-    const int lane32 = tid & 31;
 #pragma unroll
-    for (int k = 0; k < kFusedNormPT; k++)
-      if (k < cnt) {
-        const int i = tid + NT * k;
-        const float o = v[k] * scale * wsn[i];
-        uint32_t d_bits;
-        const int q = q8_0_lane(o, &d_bits);
-        uint32_t* xb = xl + (i >> 5) * WS<kQ8_0>::XS;
-        ((uint8_t*)xb)[lane32] = (uint8_t)(int8_t)q;
-        if (lane32 == 0) xb[8] = __float_as_uint(f16_bits_to_f32(d_bits));
+    for (int k = 0; k < kFusedNormPT / 8; k++) {
+      const int j = tid + NT * k;
+      if (j < nrun) {
+        const float4 w0 = ws4[2 * j], w1 = ws4[2 * j + 1];
+        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = v[8 * k + e] * scale * w[e];
+        uint32_t lo, hi, d_bits;
+        q8_0_quad8(o, &lo, &hi, &d_bits);
+        uint32_t* xb = xl + (j >> 2) * WS<kQ8_0>::XS;
+        ((uint2*)xb)[j & 3] = make_uint2(lo, hi);
+        if ((j & 3) == 0) xb[8] = __float_as_uint(f16_bits_to_f32(d_bits));
       }
+    }
     ws_lds_barrier();
   } else if constexpr (FMT != kQ4K) {
     ws_repack<FMT>((const uint32_t*)xraw, (uint32_t)((uintptr_t)A.x & 15), bpr, xl, tid, NT);
@@ -462,6 +487,8 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
     bb[k] = f - rr[k] * bpr;
   }
   const int step_r = TBK / bpr, step_b = TBK - step_r * bpr;
+  const bool urm = ws_u_rowmajor(bpr);
+  const int ust = ws_u_stride(bpr);
 
   for (int t = 0; t < ntiles; t++) {
     const int after = min(nstages - 1, ntiles - 1 - t);  // tiles issued after t
@@ -486,7 +513,7 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
         if constexpr (FMT == kQ8_0) c = ws_q80((const uint32_t*)cur, o, xb);
         else if constexpr (FMT == kQ4K) c = ws_q4k(cur, o, xb);
         else c = ws_q6k((const uint32_t*)cur, o, xb);
-        u[__umul24((uint32_t)bb[k], (uint32_t)rpw) + rr[k]] = c;
+        u[urm ? __umul24((uint32_t)rr[k], (uint32_t)ust) + bb[k] : __umul24((uint32_t)bb[k], (uint32_t)rpw) + rr[k]] = c;
       }
       rr[k] += step_r;
       bb[k] += step_b;
@@ -506,7 +533,11 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
   // the reference's `sumf += contribution` chain, block order
   float s = 0.0f;
   if (lane < nr) {
-    for (int b = 0; b < bpr; b++) s = s + u[b * rpw + lane];
+    if (urm) {
+      s = chain_from(u + lane * ust, bpr, 0.0f);
+    } else {
+      for (int b = 0; b < bpr; b++) s = s + u[b * rpw + lane];
+    }
     if (!A.swiglu_q8) Y[row0 + lane] = s;
   }
   if (A.swiglu_q8) {
