@@ -299,16 +299,19 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   extern __shared__ __align__(16) float sm[];
   const int h = blockIdx.x, tid = threadIdx.x;
   const int pos = ctl[CTL_POS], n = pos + 1;
-  const int gqa = n_heads / n_kv_heads, g = h / gqa, kvd = n_kv_heads * hd;
+  const int gqa = n_heads / n_kv_heads, g = h / gqa;
   const bool writer = (h % gqa) == 0;
   float* att = sm;
-  float* prod = sm + ((ctx + 3) & ~3);
+  float* prod = sm + ((ctx + 127) & ~127);
   float* qs = prod + 2 * kAttProd;
   float* kcur = qs + hd;
   float* vcur = kcur + hd;
   float* red = vcur + hd;
-  const size_t row = ((size_t)layer * ctx + pos) * kvd + (size_t)g * hd;
-  const size_t base = (size_t)layer * ctx * kvd + (size_t)g * hd;
+  // KV cache, per layer and KV head, piece-major: [hd / 8][ctx][8 dims] f16, so
+  // that lanes taking consecutive positions read consecutive 16-byte pieces
+  const size_t base = ((size_t)layer * n_kv_heads + g) * hd * ctx;
+  const size_t ctx8 = (size_t)ctx * 8;
+  auto kvi = [&](int t, int d) { return base + (size_t)(d >> 3) * ctx8 + (size_t)t * 8 + (d & 7); };
   const int ptid = tid - 64 * cw;
   const bool producer = ptid >= 0;
   const int nchunks = (n + C - 1) / C;
@@ -316,9 +319,9 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   uint4 kr[g8], kr2[kTwoRounds ? g8 : 1];
   auto load_key = [&](int t, uint4* r) {
     if (t < n && t != pos) {
-      const uint4* src = (const uint4*)(kc + base + (size_t)t * kvd);
+      const uint4* src = (const uint4*)(kc + base + (size_t)t * 8);
 #pragma unroll
-      for (int j = 0; j < g8; j++) r[j] = src[j];
+      for (int j = 0; j < g8; j++) r[j] = src[(size_t)j * ctx];
     }
   };
   // value piece idx of a chunk: position idx % C (consecutive lanes, consecutive
@@ -329,7 +332,7 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
       const int idx = ptid + nprod * j;
       const int tl = idx % C, i0 = 8 * (idx / C);
       const int t = c * C + tl;
-      if (idx < npc && t < n && t != pos) r[j] = *(const uint4*)(vc + base + (size_t)t * kvd + i0);
+      if (idx < npc && t < n && t != pos) r[j] = *(const uint4*)(vc + kvi(t, i0));
     }
   };
   uint4 s0[2], s1[2], s2[2];  // value rows of chunks k with k % 3 == 0, 1, 2
@@ -350,14 +353,14 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
     kcur[2 * i] = f16_bits_to_f32(k0);
     kcur[2 * i + 1] = f16_bits_to_f32(k1);
     if (writer) {
-      kc[row + 2 * i] = (uint16_t)k0;
-      kc[row + 2 * i + 1] = (uint16_t)k1;
+      kc[kvi(pos, 2 * i)] = (uint16_t)k0;
+      kc[kvi(pos, 2 * i + 1)] = (uint16_t)k1;
     }
   }
   for (int i = tid; i < hd; i += kAttNT) {
     const uint32_t vb = f32_to_f16_bits(v_in[(size_t)g * hd + i]);
     vcur[i] = f16_bits_to_f32(vb);
-    if (writer) vc[row + i] = (uint16_t)vb;
+    if (writer) vc[kvi(pos, i)] = (uint16_t)vb;
   }
   __syncthreads();
   // Scores: thread tid takes positions tid, tid + kAttNT, ...
@@ -398,10 +401,13 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   __syncthreads();
   mx = red[0];
   for (int w = 1; w < kAttNT / 64; w++) mx = fmaxf(mx, red[w]);
-  for (int t = tid; t < n; t += kAttNT) att[t] = dev_expf(att[t] - mx);
+  // exps, then zeros up to a multiple of 128: adding +0 leaves the
+  // (non-negative) sum unchanged, and the whole sum takes the DPP path
+  const int n128 = (n + 127) & ~127;
+  for (int t = tid; t < n128; t += kAttNT) att[t] = t < n ? dev_expf(att[t] - mx) : 0.0f;
   __syncthreads();
   if (tid < 64) {
-    const float tot = wave_chain_from(att, n, 0.0f);
+    const float tot = wave_chain_from(att, n128, 0.0f);
     if (tid == 0) red[16] = 1.0f / tot;
   }
   __syncthreads();
@@ -809,7 +815,7 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
   m->att_dim = c.n_heads * c.head_dim;
   m->maxd = std::max(std::max(c.dim, m->att_dim), c.ffn_dim);
   m->L.resize(c.n_layers);
-  m->att_lds = ((size_t)((c.ctx + 3) & ~3) + 2 * nrq::kAttProd + 3 * (size_t)c.head_dim + 32) * 4;
+  m->att_lds = ((size_t)((c.ctx + 127) & ~127) + 2 * nrq::kAttProd + 3 * (size_t)c.head_dim + 32) * 4;
   auto bail = [&](hipError_t e, const char* what) {
     nrq::set_last_error((std::string(what) + ": " + hipGetErrorString(e)).c_str());
     nrq_model_destroy(m);
@@ -977,8 +983,23 @@ int nrq_model_kv_cache(nrq_model* m, void* k_host, void* v_host, size_t bytes) {
   const size_t kvb = (size_t)m->cfg.n_layers * m->cfg.ctx * m->kv_dim * 2;
   if (bytes != kvb) return mfail(NRQ_ERR_SHAPE, "nrq_model_kv_cache: size mismatch");
   MHIP(hipStreamSynchronize(m->stream));
-  if (k_host) MHIP(hipMemcpy(k_host, m->kc, kvb, hipMemcpyDeviceToHost));
-  if (v_host) MHIP(hipMemcpy(v_host, m->vc, kvb, hipMemcpyDeviceToHost));
+  // the device cache is piece-major per (layer, KV head): [hd / 8][ctx][8]
+  const int L = m->cfg.n_layers, ctx = m->cfg.ctx, nkv = m->cfg.n_kv_heads, hd = m->cfg.head_dim;
+  std::vector<uint16_t> raw(kvb / 2);
+  void* outs[2] = {k_host, v_host};
+  const uint16_t* devs[2] = {m->kc, m->vc};
+  for (int a = 0; a < 2; a++) {
+    if (!outs[a]) continue;
+    MHIP(hipMemcpy(raw.data(), devs[a], kvb, hipMemcpyDeviceToHost));
+    uint16_t* o = (uint16_t*)outs[a];
+    for (int l = 0; l < L; l++)
+      for (int g = 0; g < nkv; g++) {
+        const uint16_t* src = raw.data() + ((size_t)l * nkv + g) * hd * ctx;
+        for (int j = 0; j < hd / 8; j++)
+          for (int t = 0; t < ctx; t++)
+            memcpy(o + ((size_t)l * ctx + t) * m->kv_dim + (size_t)g * hd + 8 * j, src + ((size_t)j * ctx + t) * 8, 16);
+      }
+  }
   return NRQ_OK;
 }
 
