@@ -285,12 +285,17 @@ struct WsArgs {
 // rows (48+ blocks) are stored row-major with a padded stride, so each lane
 // sums its own row with 16-byte pipelined reads; short rows block-major.
 __host__ __device__ inline bool ws_u_rowmajor(int bpr) { return bpr >= 48; }
+
+// Kernel variants, chosen at launch so that each instantiation carries only
+// its own code: the fused rmsnorm prologue, the swiglu pair epilogue, and the
+// row-major contribution layout.
+enum { kWsNorm = 1, kWsSwiglu = 2, kWsRowMajorU = 4 };
 __host__ __device__ inline int ws_u_stride(int bpr) { return ((bpr + 3) & ~3) + 4; }
 
 template <int FMT>
 struct WSGeom {
   size_t xl, xraw, stage, u, per_wave, total;
-  __host__ __device__ WSGeom(int bpr, int rpw, int ns, int nw) {
+  __host__ __device__ WSGeom(int bpr, int rpw, int ns, int nw, bool urm) {
     if (FMT == kQ4K) {  // dword DMAs of 64 lanes write whole 256-byte runs
       xl = ((size_t)bpr * WS<FMT>::XS + 63) / 64 * 256;
       xraw = 0;
@@ -300,7 +305,7 @@ struct WSGeom {
       xraw = ((size_t)bpr * WS<FMT>::XB + 15 + 15 + 1023) & ~(size_t)1023;
     }
     stage = (size_t)WS<FMT>::NI * 1024;
-    u = (((size_t)rpw * (ws_u_rowmajor(bpr) ? ws_u_stride(bpr) : bpr)) * 4 + 15) & ~(size_t)15;
+    u = (((size_t)rpw * (urm ? ws_u_stride(bpr) : bpr)) * 4 + 15) & ~(size_t)15;
     per_wave = (size_t)ns * stage + u;
     total = xl + xraw + (size_t)nw * per_wave;
   }
@@ -317,34 +322,36 @@ __device__ __forceinline__ void ws_dma16_g(const void* g, uint32_t m0) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(g) : "memory");
 }
 
-template <int FMT, int NW, int NS, bool NORM>
+template <int FMT, int NW, int NS, int MODE>
 __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int rpw, int nstages) {
+  constexpr bool NORM = (MODE & kWsNorm) != 0, SWI = (MODE & kWsSwiglu) != 0, URM = (MODE & kWsRowMajorU) != 0;
   using F = WS<FMT>;
   constexpr int NI = F::NI, BS = F::BS, TBK = 64 * F::BPL, STAGE = NI * 1024, NT = 64 * NW;
   static_assert(NS >= 1 && NS <= 4, "the vmcnt waits cover up to 4 stages");
   static_assert(!NORM || (FMT == kQ8_0 && NW == 4), "the fused norm feeds Q8_0 weights, 256 lanes");
+  static_assert(!SWI || NORM, "the swiglu pair is a fused-norm variant");
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   // workgroups [wg_end[i-1], wg_end[i]) take matrix i (the swiglu pair: waves 0-1 and 2-3)
   int mi = 0;
-  if (A.swiglu_q8) {
+  if constexpr (SWI) {
     mi = wave >> 1;
   } else {
     while (mi + 1 < A.nmat && (int)blockIdx.x >= A.wg_end[mi]) mi++;
   }
-  const int lwg = A.swiglu_q8 ? 0 : (int)blockIdx.x - (mi ? A.wg_end[mi - 1] : 0);
+  const int lwg = SWI ? 0 : (int)blockIdx.x - (mi ? A.wg_end[mi - 1] : 0);
   const uint8_t* __restrict__ W = A.w[mi];
   float* __restrict__ Y = A.y[mi];
   const int rows = A.rows[mi];
-  const WSGeom<FMT> G(bpr, rpw, nstages, NW);
+  const WSGeom<FMT> G(bpr, rpw, nstages, NW, URM);
   uint32_t* xl = (uint32_t*)smem;
   uint8_t* xraw = smem + G.xl;
   uint8_t* stages = xraw + G.xraw + (size_t)wave * G.per_wave;
   float* u = (float*)(stages + (size_t)nstages * STAGE);
   const uint32_t stage0 = ws_lds_addr(stages);
 
-  const int row0 = A.swiglu_q8 ? (int)blockIdx.x * 2 * rpw + (wave & 1) * rpw : (lwg * NW + wave) * rpw;
+  const int row0 = SWI ? (int)blockIdx.x * 2 * rpw + (wave & 1) * rpw : (lwg * NW + wave) * rpw;
   const int nr = max(0, min(rpw, rows - row0));
   const int nb = nr * bpr;
   const size_t fbeg = (size_t)max(row0, 0) * bpr;  // first flat block of this wave
@@ -487,7 +494,6 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
     bb[k] = f - rr[k] * bpr;
   }
   const int step_r = TBK / bpr, step_b = TBK - step_r * bpr;
-  const bool urm = ws_u_rowmajor(bpr);
   const int ust = ws_u_stride(bpr);
 
   for (int t = 0; t < ntiles; t++) {
@@ -513,7 +519,8 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
         if constexpr (FMT == kQ8_0) c = ws_q80((const uint32_t*)cur, o, xb);
         else if constexpr (FMT == kQ4K) c = ws_q4k(cur, o, xb);
         else c = ws_q6k((const uint32_t*)cur, o, xb);
-        u[urm ? __umul24((uint32_t)rr[k], (uint32_t)ust) + bb[k] : __umul24((uint32_t)bb[k], (uint32_t)rpw) + rr[k]] = c;
+        if constexpr (URM) u[__umul24((uint32_t)rr[k], (uint32_t)ust) + bb[k]] = c;
+        else u[__umul24((uint32_t)bb[k], (uint32_t)rpw) + rr[k]] = c;
       }
       rr[k] += step_r;
       bb[k] += step_b;
@@ -533,14 +540,14 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
   // the reference's `sumf += contribution` chain, block order
   float s = 0.0f;
   if (lane < nr) {
-    if (urm) {
+    if constexpr (URM) {
       s = chain_from(u + lane * ust, bpr, 0.0f);
     } else {
       for (int b = 0; b < bpr; b++) s = s + u[b * rpw + lane];
     }
-    if (!A.swiglu_q8) Y[row0 + lane] = s;
+    if constexpr (!SWI) Y[row0 + lane] = s;
   }
-  if (A.swiglu_q8) {
+  if constexpr (SWI) {
     // gate rows land in gu[0 .. 2 rpw), up rows in gu[2 rpw .. 4 rpw) (rpw = 16)
     float* gu = (float*)xl;  // the activation is no longer read
     ws_lds_barrier();
@@ -564,11 +571,12 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
 
 // ---- launch ----------------------------------------------------------------------------------
 
-template <int FMT, int NW, int NS, bool NORM>
+template <int FMT, int NW, int NS, int MODE>
 static int launch_ws_t(WsArgs A, int bpr, int rpw, void* stream) {
+  constexpr bool NORM = (MODE & kWsNorm) != 0, SWI = (MODE & kWsSwiglu) != 0, URM = (MODE & kWsRowMajorU) != 0;
   constexpr int TBK = 64 * WS<FMT>::BPL;
   int grid = 0;
-  if (A.swiglu_q8) {
+  if constexpr (SWI) {
     grid = A.rows[0] / (2 * rpw);
     A.wg_end[0] = A.wg_end[1] = grid;
   } else {
@@ -580,12 +588,12 @@ static int launch_ws_t(WsArgs A, int bpr, int rpw, void* stream) {
   }
   const long tiles_per_wave = ((long)rpw * bpr + TBK - 1) / TBK;
   const int nstages = (int)(tiles_per_wave < NS ? tiles_per_wave : NS);
-  const WSGeom<FMT> G(bpr, rpw, nstages, NW);
+  const WSGeom<FMT> G(bpr, rpw, nstages, NW, URM);
   // fused norm: x, add, weight, squares (n floats each) and the scale
   const size_t lds = G.total + (NORM ? (size_t)4 * bpr * 32 * 4 + 16 : 0);
   if (lds > 160 * 1024) return NRQ_LAUNCH_TOO_WIDE;
   if (grid == 0) return 0;
-  hipLaunchKernelGGL((wstream_matvec<FMT, NW, NS, NORM>), dim3(grid), dim3(64 * NW), lds, (hipStream_t)stream, A, bpr,
+  hipLaunchKernelGGL((wstream_matvec<FMT, NW, NS, MODE>), dim3(grid), dim3(64 * NW), lds, (hipStream_t)stream, A, bpr,
                      rpw, nstages);
   return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
 }
@@ -624,9 +632,16 @@ static int launch_ws(const MatvecLaunch& L) {
   A.x = (const uint8_t*)L.x;
   // NW = 4 waves share one activation copy; NS = 2 (double buffering) keeps a
   // tile in flight per wave while the other is computed, within the LDS of a CU.
-  int rc = launch_ws_t<FMT, 4, 2, false>(A, L.bpr, rpw, L.stream);
-  if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, false>(A, L.bpr, rpw, L.stream);
-  if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, false>(A, L.bpr, 1, L.stream);
+  int rc;
+  if (ws_u_rowmajor(L.bpr)) {
+    rc = launch_ws_t<FMT, 4, 2, kWsRowMajorU>(A, L.bpr, rpw, L.stream);
+    if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, kWsRowMajorU>(A, L.bpr, rpw, L.stream);
+    if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, kWsRowMajorU>(A, L.bpr, 1, L.stream);
+  } else {
+    rc = launch_ws_t<FMT, 4, 2, 0>(A, L.bpr, rpw, L.stream);
+    if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, 0>(A, L.bpr, rpw, L.stream);
+    if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, 0>(A, L.bpr, 1, L.stream);
+  }
   return rc;
 }
 
@@ -671,7 +686,12 @@ int launch_norm_matvec_q8_0(const NormMatvecLaunch& L) {
   A.nw = L.norm_w;
   A.eps = L.eps;
   A.swiglu_q8 = L.swiglu_q8;
-  return launch_ws_t<kQ8_0, 4, 2, true>(A, bpr, rpw, L.stream);
+  const bool urm = ws_u_rowmajor(bpr);
+  if (L.swiglu_q8)
+    return urm ? launch_ws_t<kQ8_0, 4, 2, kWsNorm | kWsSwiglu | kWsRowMajorU>(A, bpr, rpw, L.stream)
+               : launch_ws_t<kQ8_0, 4, 2, kWsNorm | kWsSwiglu>(A, bpr, rpw, L.stream);
+  return urm ? launch_ws_t<kQ8_0, 4, 2, kWsNorm | kWsRowMajorU>(A, bpr, rpw, L.stream)
+             : launch_ws_t<kQ8_0, 4, 2, kWsNorm>(A, bpr, rpw, L.stream);
 }
 
 int launch_wstream_scalar(int dtype, const MatvecLaunch& L) {
