@@ -34,8 +34,8 @@ struct MatmulLaunch {
   int bpr;
   int batch;
   void* stream;
-  int variant = 0;  // scalar order: 0 int8-MFMA kernel (LDS-staged for Q4_K/Q6_K), 1 one decode
-                    // launch per token, 2 int8-MFMA kernel with direct loads
+  int variant = 0;  // scalar order: 0 int8-MFMA kernels (32 x 32 tiles for Q4_K/Q6_K), 1 one
+                    // decode launch per token, 2 the 16 x 16 int8-MFMA kernel for every format
 };
 
 struct QuantLaunch {
@@ -76,6 +76,10 @@ int launch_norm_matvec_q8_0(const NormMatvecLaunch& L);
 int launch_matmul(int dtype, int order, const MatmulLaunch& L);
 // Scalar-order batched matmul on int8 MFMA (nrq_mmq.hip).
 int launch_mmq(int dtype, const MatmulLaunch& L);
+// Q4_K/Q6_K prefill on 32-row x 32-token wave tiles (nrq_mmt.hip); mmt_fits:
+// the kernel handles the format.
+bool mmt_fits(int dtype, const MatmulLaunch& L);
+int launch_mmt(int dtype, const MatmulLaunch& L);
 int launch_quantize_q8_0(const QuantLaunch& L);
 // y[0..n) = +0.0 (a kernel, not hipMemsetAsync, so it is safe under graph capture)
 int launch_fill_zero(float* y, long long n, void* stream);

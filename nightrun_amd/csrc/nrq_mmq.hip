@@ -1,4 +1,6 @@
-// Batched prefill matmul on int8 MFMA, scalar f32 order:
+// Batched prefill matmul on int8 MFMA, scalar f32 order, 16 x 16 tiles: the
+// kernel for Q8_0 weights, and an alternate for Q4_K / Q6_K (whose default is
+// the 32 x 32 tile kernel of nrq_mmt.hip):
 //   y[t][r] = dot(W[r, :], xs[t])   for t < batch (the reference's MAX_BATCH is 64)
 // bit-identical to per-token matvec, as the reference's matmul_q8 /
 // kquant_matmul! guarantee (crates/nr-tensor/src/kernels.rs:84-143,
@@ -263,369 +265,6 @@ __global__ __launch_bounds__(256) void mmq_kernel(const uint8_t* __restrict__ W,
   if (ce_row < rows && ce_tok < batch) Y[(size_t)ce_tok * rows + ce_row] = chain;
 }
 
-// ---- LDS-staged kernel: Q4_K / Q6_K weights against Q8_K activations ---------------------
-//
-// A wave owns a 16-token x 16-row element tile and a contiguous range of the
-// row's blocks (split s of S). Per block it moves, with LDS DMA
-// (global_load_lds, no VGPRs), the 16 tokens' Q8_K blocks and the 16 rows'
-// weight blocks into one of two wave-private stages, so the next block is in
-// flight while this one is computed; a wave waits only on its own loads.
-//
-// Per block, each integer sub-dot is one v_mfma_i32_16x16x32_i8 output:
-//   Q4_K: sub-block j (32 quants) is one MFMA; sum_m is four v_dot2 of the
-//         rows' mins against the tokens' bsum pair sums.
-//   Q6_K: group G (16 quants) fills k-groups 0-1 with raw 6-bit quants; k-groups
-//         2-3 carry the same activation bytes against -32, so the MFMA returns
-//         sum((q - 32) * q8) exactly (kquant.rs:232-242).
-// Then the reference's f32 steps run per element in its order. The block
-// contributions of a split stay in registers; after all splits, the
-// reference's `sumf +=` chain runs split by split in block order, each split
-// continuing from the previous split's partial sum (handed over in LDS).
-//
-// Workgroup: 4 waves = T token tiles x S splits (T * S = 4), one 16-row tile.
-// Stage layout (dwords). Every DMA moves 16 bytes per lane from a 16-byte
-// aligned address; a Q8_K token block (292 B, 4-byte aligned) lands in a
-// 19-piece window and starts s4 dwords in; a Q6_K block (210 B, 2-byte
-// aligned) lands in a 14-piece window and starts `skew` bytes in.
-constexpr int kMqAct = 0;       // [16 tokens][76]: 5 DMAs of 64 pieces (+64 pieces of clamped lanes)
-constexpr int kMqScal = 1280;   // [5][16]: tokens' bsum pair sums P0..P3, then d
-constexpr int kMqWt = 1360;     // Q4_K [16 rows][36], 3 DMAs | Q6_K [16 rows][56], 4 DMAs
-constexpr int kMqActInst = 5;
-constexpr int kMqMaxPer = 16;   // blocks per split held in registers when S > 1
-
-template <int FMT>
-struct MQ;
-template <>
-struct MQ<kQ4K> {
-  static constexpr int WI = 3, WROW = 36, STAGE = kMqWt + 3 * 256;
-  static constexpr int NI = kMqActInst + WI;
-};
-template <>
-struct MQ<kQ6K> {
-  static constexpr int WI = 4, WROW = 56, STAGE = kMqWt + 4 * 256;
-  static constexpr int NI = kMqActInst + WI;
-};
-
-__device__ __forceinline__ void mq_dma16(const uint8_t* sbase, uint32_t voff, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" : : "s"(m0), "v"(voff), "s"(sbase) : "memory");
-}
-__device__ __forceinline__ void mq_dma16v(const void* g, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(g) : "memory");
-}
-template <int N>
-__device__ __forceinline__ void mq_wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-__device__ __forceinline__ void mq_wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0x7f | (0 << 8) | (3 << 14)); }
-__device__ __forceinline__ uint32_t mq_lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
-}
-
-// Contribution of the staged block to this lane's 4 elements (tokens 4g + i, row n).
-// `A` is token n's Q8_K block in LDS.
-__device__ __forceinline__ void mq_block_q4k(const uint32_t* st, const uint32_t* A, int n, int g, float c[4]) {
-  {  // token n's bsum pair sums for sub-blocks 2g, 2g+1, and its d
-    const uint32_t v0 = A[65 + 2 * g], v1 = A[66 + 2 * g];
-    const int s0 = (int)(int16_t)(v0 & 0xffffu) + (int)(int16_t)(v0 >> 16);
-    const int s1 = (int)(int16_t)(v1 & 0xffffu) + (int)(int16_t)(v1 >> 16);
-    uint32_t* scal = (uint32_t*)st + kMqScal;
-    scal[g * 16 + n] = ((uint32_t)s0 & 0xffffu) | ((uint32_t)s1 << 16);
-    if (g == 0) scal[64 + n] = A[0];
-  }
-  const uint32_t* Wr = st + kMqWt + n * 36;
-  const u32x4 h = *(const u32x4*)Wr;
-  // kquant.rs:83-92, four scales or mins per word
-  const uint32_t scA = h.y & 0x3f3f3f3fu, mnA = h.z & 0x3f3f3f3fu;
-  const uint32_t scB = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
-  const uint32_t mnB = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
-  i32x4 sub[8];
-#pragma unroll
-  for (int cc = 0; cc < 4; cc++) {
-    const uint2 q = *(const uint2*)(Wr + 4 + 8 * cc + 2 * g);
-    const uint32_t lo0 = q.x & 0x0f0f0f0fu, lo1 = q.y & 0x0f0f0f0fu;
-    const uint32_t hi0 = (q.x >> 4) & 0x0f0f0f0fu, hi1 = (q.y >> 4) & 0x0f0f0f0fu;
-    const int a = 1 + 16 * cc + 2 * g;  // sub-block 2cc: q8 bytes 64cc + 8g ..
-    sub[2 * cc] = mfma16(A[a], A[a + 1], lo0, lo1);
-    sub[2 * cc + 1] = mfma16(A[a + 8], A[a + 9], hi0, hi1);
-  }
-  // kquant.rs:207: sum_q += f32(sc) * f32(sub) in j order (the product is exact)
-  float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const float sc = (float)(((j < 4 ? scA : scB) >> (8 * (j & 3))) & 0xffu);
-#pragma unroll
-    for (int i = 0; i < 4; i++) sq[i] = fmaf(sc, (float)sub[j][i], sq[i]);
-  }
-  const uint32_t* scal = st + kMqScal;
-  const u32x4 P0 = *(const u32x4*)(scal + 4 * g), P1 = *(const u32x4*)(scal + 16 + 4 * g);
-  const u32x4 P2 = *(const u32x4*)(scal + 32 + 4 * g), P3 = *(const u32x4*)(scal + 48 + 4 * g);
-  const u32x4 XD = *(const u32x4*)(scal + 64 + 4 * g);
-  const uint32_t M0 = __builtin_amdgcn_perm(0u, mnA, 0x0c010c00u), M1 = __builtin_amdgcn_perm(0u, mnA, 0x0c030c02u);
-  const uint32_t M2 = __builtin_amdgcn_perm(0u, mnB, 0x0c010c00u), M3 = __builtin_amdgcn_perm(0u, mnB, 0x0c030c02u);
-  const float dw = f16_bits_to_f32(h.x & 0xffffu), dmw = f16_bits_to_f32(h.x >> 16);
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    // kquant.rs:209-215
-    int sum_m = sdot2(M0, P0[i], 0);
-    sum_m = sdot2(M1, P1[i], sum_m);
-    sum_m = sdot2(M2, P2[i], sum_m);
-    sum_m = sdot2(M3, P3[i], sum_m);
-    const float xd = __uint_as_float(XD[i]);
-    const float d_all = dw * xd, dmin_all = dmw * xd;
-    const float a = d_all * sq[i];
-    const float m = dmin_all * (float)sum_m;
-    c[i] = a - m;
-  }
-}
-
-// `Wr` is row n's window, the block starting `sh` (0 or 2) bytes into Wr[0].
-__device__ __forceinline__ void mq_block_q6k(const uint32_t* st, const uint32_t* A, const uint32_t* Wr, uint32_t sh,
-                                             int n, int g, float c[4]) {
-  if (g == 0) ((uint32_t*)st)[kMqScal + 64 + n] = A[0];  // token n's d
-  const int gh = g & 1;
-  const bool zh = g >= 2;  // k-groups 2-3: the -32 half
-  uint32_t S[4];
-#pragma unroll
-  for (int t = 0; t < 4; t++) S[t] = __builtin_amdgcn_alignbyte(Wr[49 + t], Wr[48 + t], sh);  // scales[16]
-  const uint32_t dbits = sh ? (Wr[52] >> 16) : (Wr[52] & 0xffffu);
-  float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int hh = 0; hh < 2; hh++) {
-    uint32_t q6[2][4][2];  // [u][plane][dword]: quants l = 16u + 8gh + 0..7 of the half's planes
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-      const int la = 16 * hh + 4 * u + 2 * gh, lb = la + 8, qb = 32 + 8 * hh + 4 * u + 2 * gh;
-      const uint32_t a0 = __builtin_amdgcn_alignbyte(Wr[la + 1], Wr[la], sh);
-      const uint32_t a1 = __builtin_amdgcn_alignbyte(Wr[la + 2], Wr[la + 1], sh);
-      const uint32_t b0 = __builtin_amdgcn_alignbyte(Wr[lb + 1], Wr[lb], sh);
-      const uint32_t b1 = __builtin_amdgcn_alignbyte(Wr[lb + 2], Wr[lb + 1], sh);
-      const uint32_t h0 = __builtin_amdgcn_alignbyte(Wr[qb + 1], Wr[qb], sh);
-      const uint32_t h1 = __builtin_amdgcn_alignbyte(Wr[qb + 2], Wr[qb + 1], sh);
-      uint32_t p0[4], p1[4];
-      q6k_planes(a0, b0, h0, p0);
-      q6k_planes(a1, b1, h1, p1);
-#pragma unroll
-      for (int pn = 0; pn < 4; pn++) {
-        q6[u][pn][0] = zh ? 0xe0e0e0e0u : p0[pn];
-        q6[u][pn][1] = zh ? 0xe0e0e0e0u : p1[pn];
-      }
-    }
-#pragma unroll
-    for (int pn = 0; pn < 4; pn++) {
-#pragma unroll
-      for (int u = 0; u < 2; u++) {
-        const int G = 8 * hh + 2 * pn + u;  // kquant.rs:232-246 group order
-        const int a = 1 + 32 * hh + 8 * pn + 4 * u + 2 * gh;  // q8 bytes 128hh + 32pn + 16u + 8gh ..
-        const i32x4 gs = mfma16(A[a], A[a + 1], q6[u][pn][0], q6[u][pn][1]);
-        const float sc = (float)(int)(int8_t)((S[G >> 2] >> (8 * (G & 3))) & 0xffu);
-        // kquant.rs:244: sum += f32(sc) * f32(gs); |sc * gs| <= 128 * 65536, exact
-#pragma unroll
-        for (int i = 0; i < 4; i++) sum[i] = fmaf(sc, (float)gs[i], sum[i]);
-      }
-    }
-  }
-  const u32x4 XD = *(const u32x4*)(st + kMqScal + 64 + 4 * g);
-  const float dw = f16_bits_to_f32(dbits);
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float d_all = dw * __uint_as_float(XD[i]);
-    c[i] = d_all * sum[i];  // kquant.rs:246-247
-  }
-}
-
-template <int FMT, int S>
-__global__ __launch_bounds__(256) void mmq_lds_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ X,
-                                                      float* __restrict__ Y, int rows, int bpr, int batch, int ntg,
-                                                      int nrt) {
-  constexpr int T = 4 / S;
-  constexpr int NI = MQ<FMT>::NI, WI = MQ<FMT>::WI, STAGE = MQ<FMT>::STAGE;
-  constexpr int NPER = S == 1 ? 1 : kMqMaxPer;
-  extern __shared__ __align__(16) uint32_t lds[];
-  // XCD-aware numbering: the token groups of one row tile share an XCD (and its L2)
-  const int wg = blockIdx.x;
-  const int xcd = wg & 7, slot = wg >> 3;
-  const int tg = slot % ntg;
-  const int rt = (slot / ntg) * 8 + xcd;
-  if (rt >= nrt) return;  // padding workgroup (uniform, before any barrier)
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int tw = wave % T, sp = wave / T;
-  const int n = lane & 15, g = lane >> 4;
-  const int t0 = (tg * T + tw) * 16, r0 = rt * 16;
-  uint32_t* stages = lds + wave * 2 * STAGE;
-  const int per = (bpr + S - 1) / S;
-  const int b_lo = sp * per;
-  const int nmine = max(0, min(per, bpr - b_lo));
-  const uintptr_t xu = (uintptr_t)X;
-
-  // Per-lane DMA sources, fixed over blocks (clamped rows / tokens load valid memory, store nothing):
-  // piece p of the activation = 16-byte piece p % 19 of token p / 19's window.
-  uint32_t aoff[kMqActInst], aq[kMqActInst];
-#pragma unroll
-  for (int k = 0; k < kMqActInst; k++) {
-    const int p = min(64 * k + lane, 16 * 19 - 1);
-    const int tt = p / 19;
-    aq[k] = 16u * (uint32_t)(p - tt * 19);
-    aoff[k] = (uint32_t)min(t0 + tt, batch - 1) * (uint32_t)bpr * (uint32_t)kQ8KBytes;
-  }
-  uint32_t woff[WI];  // Q4_K: byte offset of the piece at block 0; Q6_K: the row's first block index
-  uint32_t wq[WI];
-#pragma unroll
-  for (int k = 0; k < WI; k++) {
-    if constexpr (FMT == kQ4K) {
-      const int pc = min(64 * k + lane, 16 * 9 - 1);
-      const int rr = pc / 9;
-      woff[k] = (uint32_t)min(r0 + rr, rows - 1) * (uint32_t)bpr * (uint32_t)kQ4KBytes + 16u * (uint32_t)(pc - rr * 9);
-      wq[k] = 0;
-    } else {
-      const int pc = min(64 * k + lane, 16 * 14 - 1);
-      const int rr = pc / 14;
-      woff[k] = (uint32_t)min(r0 + rr, rows - 1) * (uint32_t)bpr;
-      wq[k] = 16u * (uint32_t)(pc - rr * 14);
-    }
-  }
-  const uint32_t tok_n = (uint32_t)min(t0 + n, batch - 1) * (uint32_t)bpr * (uint32_t)kQ8KBytes;
-  const uint32_t mrow = (uint32_t)min(r0 + n, rows - 1) * (uint32_t)bpr;  // this lane's row, in blocks
-
-  auto issue = [&](int b, int stg) {
-    const uint32_t sb = mq_lds_addr(stages + stg * STAGE);
-    const uint32_t xb = (uint32_t)b * (uint32_t)kQ8KBytes;
-#pragma unroll
-    for (int k = 0; k < kMqActInst; k++) {
-      const uintptr_t src = ((xu + aoff[k] + xb) & ~(uintptr_t)15) + aq[k];
-      mq_dma16v((const void*)src, sb + (uint32_t)(kMqAct + 256 * k) * 4u);
-    }
-    if constexpr (FMT == kQ4K) {
-      const uint8_t* wb = W + (size_t)b * kQ4KBytes;
-#pragma unroll
-      for (int k = 0; k < WI; k++) mq_dma16(wb, woff[k], sb + (uint32_t)(kMqWt + 256 * k) * 4u);
-    } else {
-#pragma unroll
-      for (int k = 0; k < WI; k++) {
-        const uint32_t start = (woff[k] + (uint32_t)b) * (uint32_t)kQ6KBytes;
-        mq_dma16(W, (start & ~15u) + wq[k], sb + (uint32_t)(kMqWt + 256 * k) * 4u);
-      }
-    }
-  };
-
-  float cb[NPER][4];
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (nmine > 0) issue(b_lo, 0);
-  if (nmine > 1) issue(b_lo + 1, 1);
-  auto step = [&](int k) {
-    if (k + 1 < nmine) mq_wait_vm<NI>();
-    else mq_wait_vm<0>();
-    asm volatile("" ::: "memory");
-    const uint32_t b = (uint32_t)(b_lo + k);
-    const uint32_t* st = stages + (k & 1) * STAGE;
-    const uint32_t* A = st + kMqAct + n * 76 + (((xu + tok_n + b * (uint32_t)kQ8KBytes) & 15) >> 2);
-    float c[4];
-    if constexpr (FMT == kQ4K) {
-      mq_block_q4k(st, A, n, g, c);
-    } else {
-      const uint32_t skew = ((mrow + b) * (uint32_t)kQ6KBytes) & 15u;
-      mq_block_q6k(st, A, st + kMqWt + n * 56 + (skew >> 2), skew & 3u, n, g, c);
-    }
-    if constexpr (S == 1) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) acc[i] = acc[i] + c[i];  // the `sumf +=` chain, block order
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < NPER; kk++)
-        if (kk == k) {
-#pragma unroll
-          for (int i = 0; i < 4; i++) cb[kk][i] = c[i];
-        }
-    }
-    if (k + 2 < nmine) {
-      mq_wait_lgkm0();  // this stage's LDS reads are done before the DMA refills it
-      asm volatile("" ::: "memory");
-      issue(b_lo + k + 2, k & 1);
-    }
-  };
-  if constexpr (S == 1) {
-    for (int k = 0; k < nmine; k++) step(k);
-  } else {
-#pragma unroll
-    for (int k = 0; k < NPER; k++)
-      if (k < nmine) step(k);
-    // chain across splits, in block order: split s continues from split s - 1
-    float* hand = (float*)(lds + 4 * 2 * STAGE) + tw * 256;
-    for (int s = 0; s < S; s++) {
-      if (sp == s) {
-        if (s > 0) {
-#pragma unroll
-          for (int i = 0; i < 4; i++) acc[i] = hand[i * 64 + lane];
-        }
-#pragma unroll
-        for (int kk = 0; kk < NPER; kk++)
-          if (kk < nmine) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[i] = acc[i] + cb[kk][i];
-          }
-        if (s + 1 < S) {
-#pragma unroll
-          for (int i = 0; i < 4; i++) hand[i * 64 + lane] = acc[i];
-        }
-      }
-      __syncthreads();
-    }
-  }
-  if (sp == S - 1) {
-    const int row = r0 + n;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int tok = t0 + 4 * g + i;
-      if (row < rows && tok < batch) Y[(size_t)tok * rows + row] = acc[i];
-    }
-  }
-}
-
-// Token tiles per workgroup: the most that still gives >= 512 workgroups (two
-// per CU), so short matrices split the blocks instead; a split holds at most
-// kMqMaxPer blocks in registers.
-template <int FMT>
-static int launch_mmq_lds(const MatmulLaunch& L) {
-  const int nrt = (L.rows + 15) / 16, ntt = (L.batch + 15) / 16;
-  const long rt_pad = (long)((nrt + 7) / 8) * 8;
-  int T = 0;
-  const int cand[3] = {4, 2, 1};
-  for (int c = 0; c < 3; c++) {
-    const int t = cand[c], sp = 4 / t;
-    if (t > 1 && t > ntt) continue;                             // more token tiles than tokens
-    if (sp > 1 && (L.bpr + sp - 1) / sp > kMqMaxPer) continue;  // splits too long for registers
-    T = t;
-    if (rt_pad * ((ntt + t - 1) / t) >= 512) break;
-  }
-  if (T == 0) T = 4;  // few tokens and long rows: no split, idle token tiles
-  const int S = 4 / T;
-  const int ntg = (ntt + T - 1) / T;
-  const long nwg = rt_pad * ntg;
-  if (nwg > 0x7fffffffL) return NRQ_LAUNCH_BAD_ARG;
-  const size_t lds = (size_t)4 * 2 * MQ<FMT>::STAGE * 4 + (S > 1 ? (size_t)T * 256 * 4 : 0);
-  hipStream_t st = (hipStream_t)L.stream;
-  const uint8_t* w = (const uint8_t*)L.w;
-  const uint8_t* x = (const uint8_t*)L.xs;
-  if (S == 1)
-    hipLaunchKernelGGL((mmq_lds_kernel<FMT, 1>), dim3((unsigned)nwg), dim3(256), lds, st, w, x, L.y, L.rows, L.bpr,
-                       L.batch, ntg, nrt);
-  else if (S == 2)
-    hipLaunchKernelGGL((mmq_lds_kernel<FMT, 2>), dim3((unsigned)nwg), dim3(256), lds, st, w, x, L.y, L.rows, L.bpr,
-                       L.batch, ntg, nrt);
-  else
-    hipLaunchKernelGGL((mmq_lds_kernel<FMT, 4>), dim3((unsigned)nwg), dim3(256), lds, st, w, x, L.y, L.rows, L.bpr,
-                       L.batch, ntg, nrt);
-  return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
-}
-
-// The LDS-staged kernel forms 32-bit byte offsets into W and X.
-static bool mmq_lds_fits(int dtype, const MatmulLaunch& L) {
-  const unsigned long long wb = (unsigned long long)L.rows * L.bpr * (dtype == kQ4K ? kQ4KBytes : kQ6KBytes);
-  const unsigned long long xb = (unsigned long long)L.batch * L.bpr * kQ8KBytes;
-  return wb + 256 < (1ull << 32) && xb + 256 < (1ull << 32);
-}
-
 int launch_mmq(int dtype, const MatmulLaunch& L) {
   if (L.rows <= 0 || L.bpr <= 0 || L.batch <= 0) return 0;
   const int nrt = (L.rows + 15) / 16, ntt = (L.batch + 15) / 16;
@@ -635,8 +274,7 @@ int launch_mmq(int dtype, const MatmulLaunch& L) {
   hipStream_t st = (hipStream_t)L.stream;
   const uint8_t* w = (const uint8_t*)L.w;
   const uint8_t* x = (const uint8_t*)L.xs;
-  if (L.variant == 0 && (dtype == kQ4K || dtype == kQ6K) && mmq_lds_fits(dtype, L))
-    return dtype == kQ4K ? launch_mmq_lds<kQ4K>(L) : launch_mmq_lds<kQ6K>(L);
+  if (L.variant == 0 && mmt_fits(dtype, L)) return launch_mmt(dtype, L);
   if (dtype == kQ8_0)
     hipLaunchKernelGGL(mmq_kernel<kQ8_0>, grid, dim3(256), 0, st, w, x, L.y, L.rows, L.bpr, L.batch, ntt, nrt);
   else if (dtype == kQ4K)

@@ -1,0 +1,447 @@
+// Batched prefill matmul for K-quant weights (Q4_K, Q6_K) against Q8_K
+// activations on int8 MFMA, in the reference's scalar f32 order:
+//   dot_q4k_scalar (crates/nr-tensor/src/kquant.rs:192-218)
+//   dot_q6k_scalar (crates/nr-tensor/src/kquant.rs:220-250)
+// so y[t][r] equals the per-token matvec bit for bit, as kquant_matmul!
+// guarantees (kquant.rs:566-639).
+//
+// Tiles. A wave owns 32 weight rows x 32 tokens (v_mfma_i32_32x32x16_i8: lane l
+// holds row l % 32 and 16 tokens, so a row's scales stay in one lane and one
+// unpacked weight operand serves 16 outputs per lane). A workgroup is KS waves
+// over the same tile, splitting its blocks: in round k, wave s takes block
+// KS*k + s. With KS = 1 the reference's `sumf +=` chain runs in registers; with
+// KS > 1 each wave writes its round's contributions to LDS and, after the next
+// round's barrier, the wave that owns an element adds the KS contributions in
+// block order.
+//
+// Loads. Each lane reads what its MFMA operands need straight into registers,
+// one block ahead of use: its token's 16 activation bytes of each Q4_K
+// sub-block (one 16-byte load per sub-block) or 8 bytes of each Q6_K group,
+// and its row's weight bytes for the same K positions. Inside a Q4_K
+// sub-block, MFMA step h of lane half kg covers elements 32j + 16kg + 8h .. +8,
+// so both operands are contiguous (the sub-block's integer dot is exact in any
+// order). The token values the f32 steps need per output element (bsum pair
+// sums, d) pass through a small per-wave LDS table, from the lane that loaded
+// the token to the lanes that hold its outputs.
+//
+// f32 steps. Q4_K's sum_q += f32(sc_j) * f32(sub_j): each product is an
+// integer below 63 * 61440 < 2^22, so the first four partial sums are exact
+// integers below 2^24 and are formed on the 24-bit integer multiplier; the
+// remaining four steps are f32 (fmaf with an exact product rounds like the
+// reference's multiply-then-add). sum_m is four v_dot2 of the row's mins
+// against the token's bsum pair sums. Q6_K: sum += f32(sc) * f32(gs) in group
+// order, gs = sum((q - 32) * q8) from one MFMA step per 16-quant group.
+#include "nrq_device.h"
+#include "nrq_launch.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+
+namespace nrq {
+
+namespace {
+
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x3a __attribute__((ext_vector_type(3), aligned(4)));
+typedef uint32_t u32x2a __attribute__((ext_vector_type(2), aligned(4)));
+
+__device__ __forceinline__ i32x16 md_mfma(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, i32x16 c) {
+  const long a = (long)(((uint64_t)a1 << 32) | a0);
+  const long b = (long)(((uint64_t)b1 << 32) | b0);
+  return __builtin_amdgcn_mfma_i32_32x32x16_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void md_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x7f | (0 << 8) | (3 << 14));  // this wave's LDS accesses are done
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// `v`, ordered after all 16 values of `dep` are computed. MFMA steps have no
+// side effects, so the compiler would otherwise issue a block's steps far
+// ahead of the f32 chains that consume them and hold every result (16
+// registers each); tying each step's operand to the chains of two steps back
+// keeps two results live.
+__device__ __forceinline__ uint32_t md_after(uint32_t v, const float dep[16]) {
+  asm volatile("" : "+v"(v) : "v"(dep[0]), "v"(dep[1]), "v"(dep[2]), "v"(dep[3]), "v"(dep[4]), "v"(dep[5]),
+               "v"(dep[6]), "v"(dep[7]), "v"(dep[8]), "v"(dep[9]), "v"(dep[10]), "v"(dep[11]), "v"(dep[12]),
+               "v"(dep[13]), "v"(dep[14]), "v"(dep[15]));
+  return v;
+}
+
+// (q - 32) as int8 for four 6-bit quants whose bit 5 is already inverted
+// (q ^ 32, so bit 5 set means negative): (v + 0x60) ^ 0x60 copies bit 5 into
+// bits 6-7, with no carry between bytes.
+__device__ __forceinline__ uint32_t md_q6_signed(uint32_t v) { return (v + 0x60606060u) ^ 0x60606060u; }
+
+// Per-wave table of the tile's 32 token values: Q4_K bsum pair sums P0..P3, then d.
+constexpr int kMdScalDw = 160;
+
+// Registers one block needs, loaded one block ahead of use.
+template <int FMT>
+struct MdLoad;
+template <>
+struct MdLoad<kQ4K> {
+  u32x4a a[8];  // activation: sub-block j, bytes 32j + 16kg .. +16
+  u32x4a bs;    // bsum dwords 65 + 4kg .. +4 (pair sums c = 2kg, 2kg + 1)
+  uint32_t d;   // activation d (f32 bits)
+  u32x4 h;      // weight header: d | dmin, scales[12]
+  u32x4 q[4];   // qs bytes 32cc + 16kg .. +16
+};
+template <>
+struct MdLoad<kQ6K> {
+  u32x2a a[16];  // activation: group G, bytes 16G + 8kg .. +8
+  uint32_t d;
+  u32x3a w[12];  // aligned 12-byte windows [hh][u][ql low planes, ql high planes, qh]
+  u32x4a s;      // aligned window over scales[16] ...
+  uint32_t s4;   // ... and d
+};
+
+template <int FMT>
+__device__ __forceinline__ void md_load(MdLoad<FMT>& L, const uint8_t* __restrict__ xb, const uint8_t* __restrict__ wb,
+                                        int kg);
+
+template <>
+__device__ __forceinline__ void md_load<kQ4K>(MdLoad<kQ4K>& L, const uint8_t* __restrict__ xb,
+                                              const uint8_t* __restrict__ wb, int kg) {
+#pragma unroll
+  for (int j = 0; j < 8; j++) L.a[j] = *(const u32x4a*)(xb + 4 + 32 * j + 16 * kg);
+  L.bs = *(const u32x4a*)(xb + 260 + 16 * kg);
+  L.d = *(const uint32_t*)xb;
+  L.h = *(const u32x4*)wb;
+#pragma unroll
+  for (int cc = 0; cc < 4; cc++) L.q[cc] = *(const u32x4*)(wb + 16 + 32 * cc + 16 * kg);
+}
+
+// Q6_K loads by half: half 0 = groups 0-7 and their weights, plus d and the
+// scales (read at the block's start); half 1 = groups 8-15.
+__device__ __forceinline__ void md_load_q6k_half(MdLoad<kQ6K>& L, const uint8_t* __restrict__ xb,
+                                                 const uint8_t* __restrict__ wb, int kg, int hh) {
+#pragma unroll
+  for (int G = 8 * hh; G < 8 * hh + 8; G++) L.a[G] = *(const u32x2a*)(xb + 4 + 16 * G + 8 * kg);
+  const uint8_t* w4 = wb - ((uintptr_t)wb & 3u);  // the block is 2-byte aligned
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int l0 = 16 * u + 8 * kg;
+    L.w[6 * hh + 3 * u + 0] = *(const u32x3a*)(w4 + 64 * hh + l0);        // ql[64hh + l]: planes 0, 2
+    L.w[6 * hh + 3 * u + 1] = *(const u32x3a*)(w4 + 64 * hh + 32 + l0);   // ql[64hh + 32 + l]: planes 1, 3
+    L.w[6 * hh + 3 * u + 2] = *(const u32x3a*)(w4 + 128 + 32 * hh + l0);  // qh[32hh + l]
+  }
+  if (hh == 0) {
+    L.d = *(const uint32_t*)xb;
+    L.s = *(const u32x4a*)(w4 + 192);
+    L.s4 = *(const uint32_t*)(w4 + 208);
+  }
+}
+
+template <>
+__device__ __forceinline__ void md_load<kQ6K>(MdLoad<kQ6K>& L, const uint8_t* __restrict__ xb,
+                                              const uint8_t* __restrict__ wb, int kg) {
+  md_load_q6k_half(L, xb, wb, kg, 0);
+  md_load_q6k_half(L, xb, wb, kg, 1);
+}
+
+// Q4_K block: contributions c[e] of this lane's 16 outputs (row l % 32,
+// tile tokens 8(e/4) + 4kg + e%4). `ta` is this lane's operand token.
+// prefetch() runs once L is no longer read (it loads the next block into L).
+template <typename PF>
+__device__ __forceinline__ void md_q4k(MdLoad<kQ4K>& L, uint32_t* scal, int ta, int kg, float c[16], PF prefetch) {
+  {  // token ta: bsum pair sums p_{2c} | p_{2c+1} << 16 for c = 2kg, 2kg + 1, and d
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const uint32_t v0 = L.bs[2 * k], v1 = L.bs[2 * k + 1];
+      const int s0 = (int)(int16_t)(v0 & 0xffffu) + (int)(int16_t)(v0 >> 16);
+      const int s1 = (int)(int16_t)(v1 & 0xffffu) + (int)(int16_t)(v1 >> 16);
+      scal[(2 * kg + k) * 32 + ta] = ((uint32_t)s0 & 0xffffu) | ((uint32_t)s1 << 16);
+    }
+    if (kg == 0) scal[128 + ta] = L.d;
+  }
+  const u32x4 h = L.h;
+  // kquant.rs:83-92, four scales or mins per word
+  const uint32_t scA = h.y & 0x3f3f3f3fu, mnA = h.z & 0x3f3f3f3fu;
+  const uint32_t scB = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+  const uint32_t mnB = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+  // mins m_{2c} | m_{2c+1} << 16, against the pair sums p_{2c} | p_{2c+1} << 16
+  const uint32_t M0 = __builtin_amdgcn_perm(0u, mnA, 0x0c010c00u), M1 = __builtin_amdgcn_perm(0u, mnA, 0x0c030c02u);
+  const uint32_t M2 = __builtin_amdgcn_perm(0u, mnB, 0x0c010c00u), M3 = __builtin_amdgcn_perm(0u, mnB, 0x0c030c02u);
+  const float dw = f16_bits_to_f32(h.x & 0xffffu), dmw = f16_bits_to_f32(h.x >> 16);
+  int S[16];
+  float sq[16];
+  auto sub_of = [&](int j, const float dep[16]) {
+    const u32x4 q = L.q[j >> 1];
+    const uint32_t sh = (j & 1) ? 4u : 0u;
+    const uint32_t b0 = (q.x >> sh) & 0x0f0f0f0fu, b1 = (q.y >> sh) & 0x0f0f0f0fu;
+    const uint32_t b2 = (q.z >> sh) & 0x0f0f0f0fu, b3 = (q.w >> sh) & 0x0f0f0f0fu;
+    const i32x16 z = {};
+    return md_mfma(L.a[j][2], L.a[j][3], b2, b3, md_mfma(md_after(L.a[j][0], dep), L.a[j][1], b0, b1, z));
+  };
+  float dep[16];
+#pragma unroll
+  for (int e = 0; e < 16; e++) dep[e] = 0.0f;
+  i32x16 nsub = sub_of(0, dep);
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const i32x16 sub = nsub;
+    // the next sub-block's steps wait for this lane's chains after sub-block j - 1
+    if (j >= 1) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) dep[e] = j <= 4 ? __int_as_float(S[e]) : sq[e];
+    }
+    if (j + 1 < 8) nsub = sub_of(j + 1, dep);
+    if (j < 4) {
+      // kquant.rs:207, j = 0..3: exact integer partial sums (|sum| <= 4 * 63 * 61440 < 2^24)
+      const int sc = (int)((scA >> (8 * j)) & 0xffu);
+#pragma unroll
+      for (int e = 0; e < 16; e++) S[e] = j == 0 ? __mul24(sc, sub[e]) : S[e] + __mul24(sc, sub[e]);
+      if (j == 3) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) sq[e] = (float)S[e];
+      }
+    } else {
+      const float sc = (float)((scB >> (8 * (j - 4))) & 0xffu);
+#pragma unroll
+      for (int e = 0; e < 16; e++) sq[e] = fmaf(sc, (float)sub[e], sq[e]);  // j = 4..7, f32
+    }
+  }
+  prefetch();  // the block's operands are consumed: the next block's loads may reuse L
+#pragma unroll
+  for (int qq = 0; qq < 4; qq++) {
+    const int t4 = 8 * qq + 4 * kg;  // tile tokens t4 .. t4 + 3
+    const u32x4 P0 = *(const u32x4*)(scal + t4), P1 = *(const u32x4*)(scal + 32 + t4);
+    const u32x4 P2 = *(const u32x4*)(scal + 64 + t4), P3 = *(const u32x4*)(scal + 96 + t4);
+    const u32x4 XD = *(const u32x4*)(scal + 128 + t4);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int e = 4 * qq + i;
+      // kquant.rs:209-213
+      int sm = sdot2(M0, P0[i], 0);
+      sm = sdot2(M1, P1[i], sm);
+      sm = sdot2(M2, P2[i], sm);
+      sm = sdot2(M3, P3[i], sm);
+      const float xd = __uint_as_float(XD[i]);
+      const float d_all = dw * xd, dmin_all = dmw * xd;
+      const float av = d_all * sq[e];
+      const float mv = dmin_all * (float)sm;
+      c[e] = av - mv;  // kquant.rs:215
+    }
+  }
+}
+
+// Q6_K block, `sh` = its start's byte offset (0 or 2) past the aligned windows.
+// prefetch(half) runs once that half of L is no longer read.
+template <typename PF>
+__device__ __forceinline__ void md_q6k(MdLoad<kQ6K>& L, uint32_t sh, uint32_t* scal, int ta, int kg, float c[16],
+                                       PF prefetch) {
+  if (kg == 0) scal[128 + ta] = L.d;
+  uint32_t S[4];  // scales[16], realigned
+  {
+    const uint32_t sw[5] = {L.s.x, L.s.y, L.s.z, L.s.w, L.s4};
+#pragma unroll
+    for (int t = 0; t < 4; t++) S[t] = __builtin_amdgcn_alignbyte(sw[t + 1], sw[t], sh);
+  }
+  const uint32_t dbits = sh ? (L.s4 >> 16) : (L.s4 & 0xffffu);
+  const float dw = f16_bits_to_f32(dbits);
+  float sum[16];
+#pragma unroll
+  for (int e = 0; e < 16; e++) sum[e] = 0.0f;
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++) {
+    // this half's ql and qh dwords for quants l = 16u + 8kg + 0..7, realigned;
+    // qh ^ 0xaa inverts bit 5 of every quant (see md_q6_signed)
+    uint32_t QA[2][2], QB[2][2], QH[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const u32x3a wa = L.w[6 * hh + 3 * u], wb = L.w[6 * hh + 3 * u + 1], wq = L.w[6 * hh + 3 * u + 2];
+      QA[u][0] = __builtin_amdgcn_alignbyte(wa.y, wa.x, sh);
+      QA[u][1] = __builtin_amdgcn_alignbyte(wa.z, wa.y, sh);
+      QB[u][0] = __builtin_amdgcn_alignbyte(wb.y, wb.x, sh);
+      QB[u][1] = __builtin_amdgcn_alignbyte(wb.z, wb.y, sh);
+      QH[u][0] = __builtin_amdgcn_alignbyte(wq.y, wq.x, sh) ^ 0xaaaaaaaau;
+      QH[u][1] = __builtin_amdgcn_alignbyte(wq.z, wq.y, sh) ^ 0xaaaaaaaau;
+    }
+    // group G = 8hh + 2pn + u: (q - 32) of plane pn (kquant.rs:233-237), formed when its step issues
+    auto step = [&](int g8, const float dep[16]) {
+      const int pn = g8 >> 1, u = g8 & 1, G = 8 * hh + g8;
+      uint32_t bq[2];
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const uint32_t ql = (pn & 1) ? QB[u][k] : QA[u][k];
+        const uint32_t lo = (pn >> 1) ? ((ql >> 4) & 0x0f0f0f0fu) : (ql & 0x0f0f0f0fu);
+        const uint32_t hi = (pn == 0 ? (QH[u][k] << 4) : pn == 1 ? (QH[u][k] << 2) : pn == 2 ? QH[u][k] : (QH[u][k] >> 2)) &
+                            0x30303030u;
+        bq[k] = md_q6_signed(md_after(lo | hi, dep));
+      }
+      const i32x16 z = {};
+      return md_mfma(L.a[G][0], L.a[G][1], bq[0], bq[1], z);
+    };
+    i32x16 ngs = step(0, sum);
+#pragma unroll
+    for (int g8 = 0; g8 < 8; g8++) {
+      const int G = 8 * hh + g8;  // kquant.rs:238-246: groups in order (g8 = 2pn + u)
+      const i32x16 gs = ngs;
+      if (g8 + 1 < 8) ngs = step(g8 + 1, sum);  // waits for this lane's chains after group G - 1
+      const float sc = (float)(int)(int8_t)((S[G >> 2] >> (8 * (G & 3))) & 0xffu);
+      // kquant.rs:244: sum += f32(sc) * f32(gs); |sc * gs| <= 128 * 65536, exact
+#pragma unroll
+      for (int e = 0; e < 16; e++) sum[e] = fmaf(sc, (float)gs[e], sum[e]);
+    }
+    prefetch(hh);
+  }
+#pragma unroll
+  for (int qq = 0; qq < 4; qq++) {
+    const u32x4 XD = *(const u32x4*)(scal + 128 + 8 * qq + 4 * kg);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float d_all = dw * __uint_as_float(XD[i]);
+      c[4 * qq + i] = d_all * sum[4 * qq + i];  // kquant.rs:246-247
+    }
+  }
+}
+
+}  // namespace
+
+template <int FMT, int KS>
+__global__ __launch_bounds__(64 * KS) void mmd_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ X,
+                                                      float* __restrict__ Y, int rows, int bpr, int batch, int ntt,
+                                                      int nrt) {
+  constexpr int OWN = 16 / KS;  // chain elements per lane when KS > 1
+  constexpr size_t BS = FMT == kQ4K ? kQ4KBytes : kQ6KBytes;
+  extern __shared__ __align__(16) uint32_t lds[];
+  // XCD-aware numbering: the token tiles of one row tile share an XCD and its L2.
+  const int wg = blockIdx.x;
+  const int xcd = wg & 7, slot = wg >> 3;
+  const int tt = slot % ntt;
+  const int rt = (slot / ntt) * 8 + xcd;
+  if (rt >= nrt) return;  // padding workgroup (uniform, before any barrier)
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ta = lane & 31, kg = lane >> 5;
+  const int r0 = rt * 32, t0 = tt * 32;
+  // rows and tokens past the end load valid memory (the last row / token) and store nothing
+  const uint8_t* xrow = X + (size_t)min(t0 + ta, batch - 1) * bpr * kQ8KBytes;
+  const uint8_t* wrow = W + (size_t)min(r0 + ta, rows - 1) * bpr * BS;
+  uint32_t* scal = lds + ks * kMdScalDw;
+  float* xch = (float*)(lds + KS * kMdScalDw);  // KS > 1: [2][KS][1024], producer-lane-major
+  const int nrounds = (bpr + KS - 1) / KS;
+
+  float acc[KS == 1 ? 16 : OWN];
+#pragma unroll
+  for (int e = 0; e < (KS == 1 ? 16 : OWN); e++) acc[e] = 0.0f;
+  auto chain_add = [&](int r) {
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+      if (KS * r + s < bpr) {
+        const float* src = xch + ((r & 1) * KS + s) * 1024 + ks * (1024 / KS) + lane * OWN;
+#pragma unroll
+        for (int u = 0; u < OWN; u++) acc[u] = acc[u] + src[u];  // block order
+      }
+    }
+  };
+  // Loads are unconditional (past the last block they repeat it: valid memory,
+  // never used), so the registers hold one block's values, never a choice of two.
+  MdLoad<FMT> L;
+  {
+    const int b0 = min(ks, bpr - 1);
+    md_load<FMT>(L, xrow + (size_t)b0 * kQ8KBytes, wrow + (size_t)b0 * BS, kg);
+  }
+  for (int k = 0; k < nrounds; k++) {
+    const int b = KS * k + ks;
+    const int bn = min(b + KS, bpr - 1);
+    if constexpr (KS > 1) {
+      md_barrier();
+      if (k > 0) chain_add(k - 1);
+    }
+    if (b < bpr) {
+      float c[16];
+      const uint8_t* xn = xrow + (size_t)bn * kQ8KBytes;
+      const uint8_t* wn = wrow + (size_t)bn * BS;
+      if constexpr (FMT == kQ4K) {
+        md_q4k(L, scal, ta, kg, c, [&]() { md_load<kQ4K>(L, xn, wn, kg); });
+      } else {
+        md_q6k(L, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), scal, ta, kg, c,
+               [&](int hh) { md_load_q6k_half(L, xn, wn, kg, hh); });
+      }
+      if constexpr (KS == 1) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[e] = acc[e] + c[e];  // block order
+      } else {
+        float* dst = xch + ((k & 1) * KS + ks) * 1024 + lane * 16;
+#pragma unroll
+        for (int e = 0; e < 16; e += 4) *(float4*)(dst + e) = make_float4(c[e], c[e + 1], c[e + 2], c[e + 3]);
+      }
+    }
+  }
+  if constexpr (KS == 1) {
+    const int row = r0 + ta;
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const int tok = t0 + 8 * (e >> 2) + 4 * kg + (e & 3);
+      if (row < rows && tok < batch) Y[(size_t)tok * rows + row] = acc[e];
+    }
+  } else {
+    md_barrier();
+    chain_add(nrounds - 1);
+#pragma unroll
+    for (int u = 0; u < OWN; u++) {
+      const int f = ks * (1024 / KS) + lane * OWN + u;  // producer lane f / 16, its element f % 16
+      const int pl = f >> 4, e = f & 15;
+      const int row = r0 + (pl & 31), tok = t0 + 8 * (e >> 2) + 4 * (pl >> 5) + (e & 3);
+      if (row < rows && tok < batch) Y[(size_t)tok * rows + row] = acc[u];
+    }
+  }
+}
+
+// ---- launch ----------------------------------------------------------------------------------
+
+namespace {
+
+template <int FMT, int KS>
+int md_launch_t(const MatmulLaunch& L) {
+  const int nrt = (L.rows + 31) / 32, ntt = (L.batch + 31) / 32;
+  const long rt_pad = (long)((nrt + 7) / 8) * 8;
+  const long nwg = rt_pad * ntt;
+  if (nwg > 0x7fffffffL) return NRQ_LAUNCH_BAD_ARG;
+  const size_t lds = (size_t)KS * kMdScalDw * 4 + (KS > 1 ? (size_t)2 * KS * 1024 * 4 : 0);
+  hipLaunchKernelGGL((mmd_kernel<FMT, KS>), dim3((unsigned)nwg), dim3(64 * KS), lds, (hipStream_t)L.stream,
+                     (const uint8_t*)L.w, (const uint8_t*)L.xs, L.y, L.rows, L.bpr, L.batch, ntt, nrt);
+  return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
+}
+
+template <int FMT>
+int md_launch(const MatmulLaunch& L, int ks) {
+  if (ks >= 8) return md_launch_t<FMT, 8>(L);
+  if (ks == 4) return md_launch_t<FMT, 4>(L);
+  if (ks == 2) return md_launch_t<FMT, 2>(L);
+  return md_launch_t<FMT, 1>(L);
+}
+
+// Block splits per tile: the fewest that give about one wave per SIMD
+// (4 per CU), at most one block per split per round.
+int md_choose(const MatmulLaunch& L) {
+  const char* env = getenv("NRQ_MMT_SPLITS");  // tuning override: 1, 2, 4 or 8
+  if (env && env[0]) {
+    const int ks = atoi(env);
+    if (ks == 1 || ks == 2 || ks == 4 || ks == 8) return ks;
+  }
+  const long tiles = (long)((L.rows + 31) / 32) * ((L.batch + 31) / 32);
+  int ks = 1;
+  while (ks < 8 && ks < L.bpr && tiles * ks < 4L * 256) ks *= 2;
+  return ks;
+}
+
+}  // namespace
+
+bool mmt_fits(int dtype, const MatmulLaunch& L) {
+  (void)L;
+  return dtype == kQ4K || dtype == kQ6K;
+}
+
+int launch_mmt(int dtype, const MatmulLaunch& L) {
+  if (L.rows <= 0 || L.bpr <= 0 || L.batch <= 0) return 0;
+  const int ks = md_choose(L);
+  return dtype == kQ4K ? md_launch<kQ4K>(L, ks) : md_launch<kQ6K>(L, ks);
+}
+
+}  // namespace nrq
