@@ -630,15 +630,18 @@ static int launch_ws(const MatvecLaunch& L) {
   A.rows[0] = L.rows;
   A.nmat = 1;
   A.x = (const uint8_t*)L.x;
-  // NW = 4 waves share one activation copy; NS = 2 (double buffering) keeps a
-  // tile in flight per wave while the other is computed, within the LDS of a CU.
+  // NW waves share one activation copy; NS = 2 (double buffering) keeps a tile
+  // in flight per wave while the other is computed, within the LDS of a CU.
   int rc;
   if (ws_u_rowmajor(L.bpr)) {
     rc = launch_ws_t<FMT, 4, 2, kWsRowMajorU>(A, L.bpr, rpw, L.stream);
     if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, kWsRowMajorU>(A, L.bpr, rpw, L.stream);
     if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, kWsRowMajorU>(A, L.bpr, 1, L.stream);
   } else {
-    rc = launch_ws_t<FMT, 4, 2, 0>(A, L.bpr, rpw, L.stream);
+    // Q4_K: eight waves share one activation copy (about 3% faster than four on
+    // the 8192 x 3072 matvec, measured in one process; other formats gain nothing)
+    rc = FMT == kQ4K ? launch_ws_t<FMT, 8, 2, 0>(A, L.bpr, rpw, L.stream) : NRQ_LAUNCH_TOO_WIDE;
+    if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 4, 2, 0>(A, L.bpr, rpw, L.stream);
     if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, 0>(A, L.bpr, rpw, L.stream);
     if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, 0>(A, L.bpr, 1, L.stream);
   }

@@ -422,3 +422,23 @@ def test_matmul_adversarial_and_saturated(gpu, oracle, dtype):
         ws = np.repeat(q4 if dtype == 2 else q6, rows * 4, axis=0)
         assert_bitwise(gpu_matmul(dtype, 0, ws, xs, rows, cols, batch),
                        oracle.matmul(dtype, 0, ws, xs, rows, cols, batch))
+
+
+@pytest.mark.parametrize("dtype", [2, 3])
+def test_matmul_every_split_count(gpu, oracle, dtype, monkeypatch):
+    """The K-quant prefill kernel splits a 32 x 32 tile's blocks over 1, 2, 4 or
+    8 waves (chosen by shape; NRQ_MMT_SPLITS forces one). Every split count
+    gives the oracle's bits: odd block counts (the last round partly empty), a
+    partial token tile, batches past 64 and fewer than 32 tokens."""
+    qk = oracle.QK[dtype]
+    cases = []
+    for rows, bpr, batch in ((96, 8, 64), (40, 37, 33), (50, 3, 130), (20, 11, 5)):
+        cols = bpr * qk
+        w = oracle.gen_weights(dtype, 800 + bpr, rows, cols)
+        xs = oracle.quantize_act(dtype, oracle.Rng(801 + bpr).normal(batch * cols))
+        cases.append((rows, cols, batch, w, xs, oracle.matmul(dtype, 0, w, xs, rows, cols, batch, threads=THREADS)))
+    for ks in ("1", "2", "4", "8"):
+        monkeypatch.setenv("NRQ_MMT_SPLITS", ks)
+        for rows, cols, batch, w, xs, want in cases:
+            assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, batch), want,
+                           f"splits {ks} rows {rows} cols {cols} batch {batch}")
