@@ -15,7 +15,8 @@
 // block order.
 //
 // Loads. Each lane reads what its MFMA operands need straight into registers,
-// one block ahead of use: its token's 16 activation bytes of each Q4_K
+// one block ahead of use (from a second register buffer, or into the current
+// one once its operands are consumed): its token's 16 activation bytes of each Q4_K
 // sub-block (one 16-byte load per sub-block) or 8 bytes of each Q6_K group,
 // and its row's weight bytes for the same K positions. Inside a Q4_K
 // sub-block, MFMA step h of lane half kg covers elements 32j + 16kg + 8h .. +8,
@@ -302,7 +303,7 @@ __device__ __forceinline__ void md_q6k(MdLoad<kQ6K>& L, uint32_t sh, uint32_t* s
 
 }  // namespace
 
-template <int FMT, int KS>
+template <int FMT, int KS, bool DB>
 __global__ __launch_bounds__(64 * KS) void mmd_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ X,
                                                       float* __restrict__ Y, int rows, int bpr, int batch, int ntt,
                                                       int nrt) {
@@ -341,35 +342,73 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(const uint8_t* __restrict_
   };
   // Loads are unconditional (past the last block they repeat it: valid memory,
   // never used), so the registers hold one block's values, never a choice of two.
-  MdLoad<FMT> L;
-  {
-    const int b0 = min(ks, bpr - 1);
-    md_load<FMT>(L, xrow + (size_t)b0 * kQ8KBytes, wrow + (size_t)b0 * BS, kg);
-  }
-  for (int k = 0; k < nrounds; k++) {
-    const int b = KS * k + ks;
-    const int bn = min(b + KS, bpr - 1);
-    if constexpr (KS > 1) {
-      md_barrier();
-      if (k > 0) chain_add(k - 1);
+  auto finish = [&](int k, const float c[16]) {
+    if constexpr (KS == 1) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[e] = acc[e] + c[e];  // block order
+    } else {
+      float* dst = xch + ((k & 1) * KS + ks) * 1024 + lane * 16;
+#pragma unroll
+      for (int e = 0; e < 16; e += 4) *(float4*)(dst + e) = make_float4(c[e], c[e + 1], c[e + 2], c[e + 3]);
     }
-    if (b < bpr) {
-      float c[16];
-      const uint8_t* xn = xrow + (size_t)bn * kQ8KBytes;
-      const uint8_t* wn = wrow + (size_t)bn * BS;
-      if constexpr (FMT == kQ4K) {
-        md_q4k(L, scal, ta, kg, c, [&]() { md_load<kQ4K>(L, xn, wn, kg); });
-      } else {
-        md_q6k(L, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), scal, ta, kg, c,
-               [&](int hh) { md_load_q6k_half(L, xn, wn, kg, hh); });
+  };
+  if constexpr (DB) {
+    // two register buffers: a block's loads are issued a whole block ahead
+    MdLoad<FMT> La, Lb;
+    {
+      const int b0 = min(ks, bpr - 1);
+      md_load<FMT>(La, xrow + (size_t)b0 * kQ8KBytes, wrow + (size_t)b0 * BS, kg);
+    }
+    auto body = [&](int k, MdLoad<FMT>& cur, MdLoad<FMT>& nxt) {
+      const int b = KS * k + ks;
+      const int bn = min(b + KS, bpr - 1);
+      md_load<FMT>(nxt, xrow + (size_t)bn * kQ8KBytes, wrow + (size_t)bn * BS, kg);
+      if constexpr (KS > 1) {
+        md_barrier();
+        if (k > 0) chain_add(k - 1);
       }
-      if constexpr (KS == 1) {
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[e] = acc[e] + c[e];  // block order
-      } else {
-        float* dst = xch + ((k & 1) * KS + ks) * 1024 + lane * 16;
-#pragma unroll
-        for (int e = 0; e < 16; e += 4) *(float4*)(dst + e) = make_float4(c[e], c[e + 1], c[e + 2], c[e + 3]);
+      if (b < bpr) {
+        float c[16];
+        if constexpr (FMT == kQ4K) {
+          md_q4k(cur, scal, ta, kg, c, [&]() {});
+        } else {
+          md_q6k(cur, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), scal, ta, kg, c, [&](int) {});
+        }
+        finish(k, c);
+      }
+    };
+    int k = 0;
+    for (; k + 1 < nrounds; k += 2) {
+      body(k, La, Lb);
+      body(k + 1, Lb, La);
+    }
+    if (k < nrounds) body(k, La, Lb);
+  } else {
+    // one register buffer: the next block's loads are issued as soon as the
+    // current block's operands are consumed
+    MdLoad<FMT> L;
+    {
+      const int b0 = min(ks, bpr - 1);
+      md_load<FMT>(L, xrow + (size_t)b0 * kQ8KBytes, wrow + (size_t)b0 * BS, kg);
+    }
+    for (int k = 0; k < nrounds; k++) {
+      const int b = KS * k + ks;
+      const int bn = min(b + KS, bpr - 1);
+      if constexpr (KS > 1) {
+        md_barrier();
+        if (k > 0) chain_add(k - 1);
+      }
+      if (b < bpr) {
+        float c[16];
+        const uint8_t* xn = xrow + (size_t)bn * kQ8KBytes;
+        const uint8_t* wn = wrow + (size_t)bn * BS;
+        if constexpr (FMT == kQ4K) {
+          md_q4k(L, scal, ta, kg, c, [&]() { md_load<kQ4K>(L, xn, wn, kg); });
+        } else {
+          md_q6k(L, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), scal, ta, kg, c,
+                 [&](int hh) { md_load_q6k_half(L, xn, wn, kg, hh); });
+        }
+        finish(k, c);
       }
     }
   }
@@ -397,28 +436,34 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(const uint8_t* __restrict_
 
 namespace {
 
-template <int FMT, int KS>
+template <int FMT, int KS, bool DB>
 int md_launch_t(const MatmulLaunch& L) {
   const int nrt = (L.rows + 31) / 32, ntt = (L.batch + 31) / 32;
   const long rt_pad = (long)((nrt + 7) / 8) * 8;
   const long nwg = rt_pad * ntt;
   if (nwg > 0x7fffffffL) return NRQ_LAUNCH_BAD_ARG;
   const size_t lds = (size_t)KS * kMdScalDw * 4 + (KS > 1 ? (size_t)2 * KS * 1024 * 4 : 0);
-  hipLaunchKernelGGL((mmd_kernel<FMT, KS>), dim3((unsigned)nwg), dim3(64 * KS), lds, (hipStream_t)L.stream,
+  hipLaunchKernelGGL((mmd_kernel<FMT, KS, DB>), dim3((unsigned)nwg), dim3(64 * KS), lds, (hipStream_t)L.stream,
                      (const uint8_t*)L.w, (const uint8_t*)L.xs, L.y, L.rows, L.bpr, L.batch, ntt, nrt);
   return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
 }
 
-template <int FMT>
-int md_launch(const MatmulLaunch& L, int ks) {
-  if (ks >= 8) return md_launch_t<FMT, 8>(L);
-  if (ks == 4) return md_launch_t<FMT, 4>(L);
-  if (ks == 2) return md_launch_t<FMT, 2>(L);
-  return md_launch_t<FMT, 1>(L);
+template <int FMT, bool DB>
+int md_launch_ks(const MatmulLaunch& L, int ks) {
+  if (ks >= 8) return md_launch_t<FMT, 8, DB>(L);
+  if (ks == 4) return md_launch_t<FMT, 4, DB>(L);
+  if (ks == 2) return md_launch_t<FMT, 2, DB>(L);
+  return md_launch_t<FMT, 1, DB>(L);
 }
 
-// Block splits per tile: the fewest that give about one wave per SIMD
-// (4 per CU), at most one block per split per round.
+template <int FMT>
+int md_launch(const MatmulLaunch& L, int ks, bool db) {
+  return db ? md_launch_ks<FMT, true>(L, ks) : md_launch_ks<FMT, false>(L, ks);
+}
+
+// Block splits per tile: the fewest that give about one wave per SIMD (4 per
+// CU), and at most 4 for rows of 16 blocks or fewer (more splits leave each
+// wave one or two blocks). Measured on the Qwen3-4B layer shapes at M = 64.
 int md_choose(const MatmulLaunch& L) {
   const char* env = getenv("NRQ_MMT_SPLITS");  // tuning override: 1, 2, 4 or 8
   if (env && env[0]) {
@@ -426,9 +471,18 @@ int md_choose(const MatmulLaunch& L) {
     if (ks == 1 || ks == 2 || ks == 4 || ks == 8) return ks;
   }
   const long tiles = (long)((L.rows + 31) / 32) * ((L.batch + 31) / 32);
+  const int cap = L.bpr <= 16 ? 4 : 8;
   int ks = 1;
-  while (ks < 8 && ks < L.bpr && tiles * ks < 4L * 256) ks *= 2;
+  while (ks < cap && ks < L.bpr && tiles * ks < 4L * 256) ks *= 2;
   return ks;
+}
+
+// Two register buffers (a block's loads issued a whole block ahead) pay off
+// where waves are fewest per SIMD: one split, or eight splits of long Q6_K rows.
+bool md_double_buffer(int dtype, int ks) {
+  const char* env = getenv("NRQ_MMT_DB");  // tuning override: 0 or 1
+  if (env && env[0]) return env[0] == '1';
+  return ks == 1 || (dtype == kQ6K && ks == 8);
 }
 
 }  // namespace
@@ -441,7 +495,8 @@ bool mmt_fits(int dtype, const MatmulLaunch& L) {
 int launch_mmt(int dtype, const MatmulLaunch& L) {
   if (L.rows <= 0 || L.bpr <= 0 || L.batch <= 0) return 0;
   const int ks = md_choose(L);
-  return dtype == kQ4K ? md_launch<kQ4K>(L, ks) : md_launch<kQ6K>(L, ks);
+  const bool db = md_double_buffer(dtype, ks);
+  return dtype == kQ4K ? md_launch<kQ4K>(L, ks, db) : md_launch<kQ6K>(L, ks, db);
 }
 
 }  // namespace nrq

@@ -427,8 +427,9 @@ def test_matmul_adversarial_and_saturated(gpu, oracle, dtype):
 @pytest.mark.parametrize("dtype", [2, 3])
 def test_matmul_every_split_count(gpu, oracle, dtype, monkeypatch):
     """The K-quant prefill kernel splits a 32 x 32 tile's blocks over 1, 2, 4 or
-    8 waves (chosen by shape; NRQ_MMT_SPLITS forces one). Every split count
-    gives the oracle's bits: odd block counts (the last round partly empty), a
+    8 waves and holds one or two blocks of loads in registers (chosen by shape;
+    NRQ_MMT_SPLITS and NRQ_MMT_DB force them). Every combination gives the
+    oracle's bits: odd block counts (the last round partly empty), a
     partial token tile, batches past 64 and fewer than 32 tokens."""
     qk = oracle.QK[dtype]
     cases = []
@@ -437,8 +438,10 @@ def test_matmul_every_split_count(gpu, oracle, dtype, monkeypatch):
         w = oracle.gen_weights(dtype, 800 + bpr, rows, cols)
         xs = oracle.quantize_act(dtype, oracle.Rng(801 + bpr).normal(batch * cols))
         cases.append((rows, cols, batch, w, xs, oracle.matmul(dtype, 0, w, xs, rows, cols, batch, threads=THREADS)))
-    for ks in ("1", "2", "4", "8"):
-        monkeypatch.setenv("NRQ_MMT_SPLITS", ks)
-        for rows, cols, batch, w, xs, want in cases:
-            assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, batch), want,
-                           f"splits {ks} rows {rows} cols {cols} batch {batch}")
+    for db in ("0", "1"):
+        monkeypatch.setenv("NRQ_MMT_DB", db)
+        for ks in ("1", "2", "4", "8"):
+            monkeypatch.setenv("NRQ_MMT_SPLITS", ks)
+            for rows, cols, batch, w, xs, want in cases:
+                assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, batch), want,
+                               f"splits {ks} double buffer {db} rows {rows} cols {cols} batch {batch}")
