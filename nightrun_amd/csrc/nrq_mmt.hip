@@ -29,8 +29,9 @@
 // integer below 63 * 61440 < 2^22, so the first four partial sums are exact
 // integers below 2^24 and are formed on the 24-bit integer multiplier; the
 // remaining four steps are f32 (fmaf with an exact product rounds like the
-// reference's multiply-then-add). sum_m is four v_dot2 of the row's mins
-// against the token's bsum pair sums. Q6_K: sum += f32(sc) * f32(gs) in group
+// reference's multiply-then-add). sum_m = sum of m_{k/2} * bsums[k] is two
+// more MFMA steps (the bsums split exactly into low 7 bits and a signed high
+// part). Q6_K: sum += f32(sc) * f32(gs) in group
 // order, gs = sum((q - 32) * q8) from one MFMA step per 16-quant group.
 #include "nrq_device.h"
 #include "nrq_launch.h"
@@ -77,7 +78,7 @@ __device__ __forceinline__ uint32_t md_after(uint32_t v, const float dep[16]) {
 // bits 6-7, with no carry between bytes.
 __device__ __forceinline__ uint32_t md_q6_signed(uint32_t v) { return (v + 0x60606060u) ^ 0x60606060u; }
 
-// Per-wave table of the tile's 32 token values: Q4_K bsum pair sums P0..P3, then d.
+// Per-wave table of the tile's 32 token values (dword 128 + t: d of token t).
 constexpr int kMdScalDw = 160;
 
 // Registers one block needs, loaded one block ahead of use.
@@ -86,7 +87,7 @@ struct MdLoad;
 template <>
 struct MdLoad<kQ4K> {
   u32x4a a[8];  // activation: sub-block j, bytes 32j + 16kg .. +16
-  u32x4a bs;    // bsum dwords 65 + 4kg .. +4 (pair sums c = 2kg, 2kg + 1)
+  u32x4a bs;    // bsums 8kg .. 8kg+7 (dwords 65 + 4kg .. +4)
   uint32_t d;   // activation d (f32 bits)
   u32x4 h;      // weight header: d | dmin, scales[12]
   u32x4 q[4];   // qs bytes 32cc + 16kg .. +16
@@ -149,24 +150,19 @@ __device__ __forceinline__ void md_load<kQ6K>(MdLoad<kQ6K>& L, const uint8_t* __
 // prefetch() runs once L is no longer read (it loads the next block into L).
 template <typename PF>
 __device__ __forceinline__ void md_q4k(MdLoad<kQ4K>& L, uint32_t* scal, int ta, int kg, float c[16], PF prefetch) {
-  {  // token ta: bsum pair sums p_{2c} | p_{2c+1} << 16 for c = 2kg, 2kg + 1, and d
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const uint32_t v0 = L.bs[2 * k], v1 = L.bs[2 * k + 1];
-      const int s0 = (int)(int16_t)(v0 & 0xffffu) + (int)(int16_t)(v0 >> 16);
-      const int s1 = (int)(int16_t)(v1 & 0xffffu) + (int)(int16_t)(v1 >> 16);
-      scal[(2 * kg + k) * 32 + ta] = ((uint32_t)s0 & 0xffffu) | ((uint32_t)s1 << 16);
-    }
-    if (kg == 0) scal[128 + ta] = L.d;
-  }
+  if (kg == 0) scal[128 + ta] = L.d;  // token ta's d
   const u32x4 h = L.h;
   // kquant.rs:83-92, four scales or mins per word
   const uint32_t scA = h.y & 0x3f3f3f3fu, mnA = h.z & 0x3f3f3f3fu;
   const uint32_t scB = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
   const uint32_t mnB = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
-  // mins m_{2c} | m_{2c+1} << 16, against the pair sums p_{2c} | p_{2c+1} << 16
-  const uint32_t M0 = __builtin_amdgcn_perm(0u, mnA, 0x0c010c00u), M1 = __builtin_amdgcn_perm(0u, mnA, 0x0c030c02u);
-  const uint32_t M2 = __builtin_amdgcn_perm(0u, mnB, 0x0c010c00u), M3 = __builtin_amdgcn_perm(0u, mnB, 0x0c030c02u);
+  // kquant.rs:209-213: sum_m = sum_k m_{k/2} * bsums[k] over the 16 bsums, as two
+  // MFMA steps (K = 16): lane half kg holds bsums 8kg .. 8kg+7 of token ta,
+  // split exactly as bsum = 128 * hi + lo (lo = low 7 bits, hi in [-16, 15]),
+  // against m_{4kg}, m_{4kg}, m_{4kg+1}, ... of row l % 32.
+  // (the two steps issue after the sub-block loop, whose results they would otherwise sit beside)
+  const uint32_t sb0 = L.bs[0], sb1 = L.bs[1], sb2 = L.bs[2], sb3 = L.bs[3];
+  const uint32_t mn = kg ? mnB : mnA;
   const float dw = f16_bits_to_f32(h.x & 0xffffu), dmw = f16_bits_to_f32(h.x >> 16);
   int S[16];
   float sq[16];
@@ -206,21 +202,26 @@ __device__ __forceinline__ void md_q4k(MdLoad<kQ4K>& L, uint32_t* scal, int ta, 
       for (int e = 0; e < 16; e++) sq[e] = fmaf(sc, (float)sub[e], sq[e]);  // j = 4..7, f32
     }
   }
+  i32x16 smlo, smhi;
+  {
+    const uint32_t lo0 = md_after(__builtin_amdgcn_perm(sb1, sb0, 0x06040200u) & 0x7f7f7f7fu, sq);
+    const uint32_t lo1 = __builtin_amdgcn_perm(sb3, sb2, 0x06040200u) & 0x7f7f7f7fu;
+    const uint32_t hi0 = __builtin_amdgcn_perm((sb1 >> 7) & 0x00ff00ffu, (sb0 >> 7) & 0x00ff00ffu, 0x06040200u);
+    const uint32_t hi1 = __builtin_amdgcn_perm((sb3 >> 7) & 0x00ff00ffu, (sb2 >> 7) & 0x00ff00ffu, 0x06040200u);
+    const uint32_t m0 = __builtin_amdgcn_perm(mn, mn, 0x01010000u), m1 = __builtin_amdgcn_perm(mn, mn, 0x03030202u);
+    const i32x16 z = {};
+    smlo = md_mfma(lo0, lo1, m0, m1, z);
+    smhi = md_mfma(md_after(hi0, sq), hi1, m0, m1, z);
+  }
   prefetch();  // the block's operands are consumed: the next block's loads may reuse L
 #pragma unroll
   for (int qq = 0; qq < 4; qq++) {
     const int t4 = 8 * qq + 4 * kg;  // tile tokens t4 .. t4 + 3
-    const u32x4 P0 = *(const u32x4*)(scal + t4), P1 = *(const u32x4*)(scal + 32 + t4);
-    const u32x4 P2 = *(const u32x4*)(scal + 64 + t4), P3 = *(const u32x4*)(scal + 96 + t4);
     const u32x4 XD = *(const u32x4*)(scal + 128 + t4);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int e = 4 * qq + i;
-      // kquant.rs:209-213
-      int sm = sdot2(M0, P0[i], 0);
-      sm = sdot2(M1, P1[i], sm);
-      sm = sdot2(M2, P2[i], sm);
-      sm = sdot2(M3, P3[i], sm);
+      const int sm = (int)(((uint32_t)smhi[e] << 7) + (uint32_t)smlo[e]);  // exact: |sum_m| < 2^22
       const float xd = __uint_as_float(XD[i]);
       const float d_all = dw * xd, dmin_all = dmw * xd;
       const float av = d_all * sq[e];
