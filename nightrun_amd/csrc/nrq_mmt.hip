@@ -462,7 +462,9 @@ int md_launch(const MatmulLaunch& L, int ks, bool db) {
   return db ? md_launch_ks<FMT, true>(L, ks) : md_launch_ks<FMT, false>(L, ks);
 }
 
-// Block splits per tile: the fewest that give about one wave per SIMD (4 per
+// Block splits per tile: none when the tiles alone give two waves per CU
+// (a whole row of blocks per wave, double-buffered, beat two splits by 3-6%
+// on 9728 x 2560); else the fewest that give about one wave per SIMD (4 per
 // CU), and at most 4 for rows of 16 blocks or fewer (more splits leave each
 // wave one or two blocks). Measured on the Qwen3-4B layer shapes at M = 64.
 int md_choose(const MatmulLaunch& L) {
@@ -472,6 +474,7 @@ int md_choose(const MatmulLaunch& L) {
     if (ks == 1 || ks == 2 || ks == 4 || ks == 8) return ks;
   }
   const long tiles = (long)((L.rows + 31) / 32) * ((L.batch + 31) / 32);
+  if (tiles >= 2L * 256) return 1;
   const int cap = L.bpr <= 16 ? 4 : 8;
   int ks = 1;
   while (ks < cap && ks < L.bpr && tiles * ks < 4L * 256) ks *= 2;
