@@ -17,7 +17,9 @@ Beside it, in the same JSON line:
   prefill        one Qwen3-4B layer's seven matmuls at M = 64 tokens (int8 MFMA)
   decode         greedy tokens/s of a Llama-3.2-1B-shape Q8_0 model (random
                  init) with the KV cache filled to 1024 positions, each step one
-                 HIP graph replay (nrq_model_generate)
+                 HIP graph replay (nrq_model_generate); the model is loaded from
+                 an in-memory .nrm file (load time beside it) and its data
+                 section's CRC-32 is timed on the device (verify_crc)
   cpu_baseline   the CPU oracle's AVX2 restatement of the matvec, and its
                  scalar-order restatement of the full decode step, timed on a
                  bounded sample on the host cores
@@ -229,18 +231,103 @@ def model_bytes_per_token(cfg, kv_pos):
     return cfg["n_layers"] * per_layer + head + kv_bytes
 
 
+def nrm_blob(cfg, w):
+    """The weights `w` as a .nrm v3 file in memory (crates/nr-model/src/format.rs:1-10:
+    192-byte header | tokenizer blob | 32-byte table entries | data, every tensor
+    64-byte aligned, meta and data CRCs), head tied to the embedding."""
+    import struct
+
+    from nightrun_amd import nrm
+
+    d, hd = cfg["dim"], cfg["head_dim"]
+    att, kv, ffn = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd, cfg["ffn_dim"]
+    shapes = {"wq": (11, att, d), "wk": (12, kv, d), "wv": (13, kv, d), "wo": (14, d, att), "w_gate": (16, ffn, d),
+              "w_up": (17, ffn, d), "w_down": (18, d, ffn)}
+    ts = [(1, 0, w["embed_dtype"], cfg["vocab"], d, w["embed"]), (2, 0, 0, 1, d, w["out_norm"])]
+    for l, lw in enumerate(w["layers"]):
+        ts += [(10, l, 0, 1, d, lw["attn_norm"]), (15, l, 0, 1, d, lw["ffn_norm"])]
+        ts += [(k, l, lw["dtypes"][n], r, c, lw[n]) for n, (k, r, c) in shapes.items()]
+    tok = b"\0" * 64
+    table_off = 192 + len(tok)
+    data_off = -(-(table_off + 32 * len(ts)) // 64) * 64
+    offs, pos = [], 0
+    for t in ts:
+        offs.append(pos)
+        pos = -(-(pos + t[5].nbytes) // 64) * 64
+    data_size = offs[-1] + ts[-1][5].nbytes
+    b = np.zeros(data_off + data_size, np.uint8)
+    hdr = bytearray(192)
+    hdr[0:4] = b"NRUN"
+    struct.pack_into("<II8I", hdr, 4, 3, 1, d, cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"], hd, ffn,
+                     cfg["vocab"], 131072)
+    struct.pack_into("<6fI4f", hdr, 44, cfg["rope_theta"], cfg["norm_eps"], 0.0, 0.0, 0.0, 0.0, 1, 1.0, 0.0, 1.0, 1.0)
+    hdr[88:96] = b"llama-1b"
+    struct.pack_into("<QQQIIQQ", hdr, 136, 192, len(tok), table_off, len(ts), 0, data_off, data_size)
+    table = bytearray(32 * len(ts))
+    for i, (t, off) in enumerate(zip(ts, offs)):
+        struct.pack_into("<HHHHQQII", table, 32 * i, t[0], t[1], t[2], 0, off, t[5].nbytes, t[3], t[4])
+        b[data_off + off:data_off + off + t[5].nbytes] = np.ascontiguousarray(t[5]).view(np.uint8).ravel()
+    struct.pack_into("<I", hdr, 184, nrm.crc32(b[data_off:]))
+    b[table_off:table_off + len(table)] = np.frombuffer(bytes(table), np.uint8)
+    b[192:192 + len(tok)] = np.frombuffer(tok, np.uint8)
+    c = nrm.crc32(bytes(hdr[:184]) + bytes(8))
+    c = nrm.crc32(tok, c)
+    struct.pack_into("<I", hdr, 188, nrm.crc32(bytes(table), c))
+    b[:192] = np.frombuffer(bytes(hdr), np.uint8)
+    return b
+
+
+def measure_crc(data, want=None, reps=20):
+    """nrq_dev_crc32 over the uint8 device tensor `data`, `reps` calls back to
+    back on one stream, HIP events around them."""
+    import torch
+
+    from nightrun_amd import _lib
+
+    n = data.numel()
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.Stream()
+    L = _lib.lib()
+    torch.cuda.synchronize()
+    _lib.check(L.nrq_dev_crc32(data.data_ptr(), n, 0, out.data_ptr(), stream.cuda_stream))
+    stream.synchronize()
+    got = int(out.cpu().item()) & 0xFFFFFFFF
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        _lib.check(L.nrq_dev_crc32(data.data_ptr(), n, 0, out.data_ptr(), stream.cuda_stream))
+    b.record(stream)
+    b.synchronize()
+    per = a.elapsed_time(b) / 1e3 / reps
+    r = {"bytes": n, "us": round(per * 1e6, 2), "gbs": round(n / per / 1e9, 1),
+         "frac_of_hbm_peak": round(n / per / 1e9 / HBM_PEAK_GBS, 4)}
+    if want is not None:
+        r["matches_header"] = got == want
+    return r
+
+
 def measure_decode(fill=1024, n=128):
+    """The model comes in through the .nrm path (parse, one upload of the data
+    section, CRC on the device, binding), then greedy decode."""
     import torch
 
     import nightrun_amd
-    from nightrun_amd.model import Model
+    from nightrun_amd import nrm
 
     nightrun_amd.init(0)
     cfg = LLAMA_1B
     w = synth_model(cfg, 0x5EED0005)
-    m = Model(cfg, ctx=fill + n + 8)
-    m.set_weights(w)
+    blob = nrm_blob(cfg, w)
     del w
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    f = nrm.NrmFile(blob)
+    m = f.load(fill + n + 8, verify=True)
+    load_s = time.perf_counter() - t0
+    data = f.upload()
+    crc = {"workload": "CRC-32 (IEEE) of the Llama-3.2-1B-shape Q8_0 data section in HBM",
+           **measure_crc(data, f.meta["data_crc"])}
+    del data
     first = int(np.random.default_rng(5).integers(0, cfg["vocab"]))
     # fill the KV cache (greedy continuation of one random token)
     toks = m.generate(first, fill)
@@ -251,12 +338,16 @@ def measure_decode(fill=1024, n=128):
     m.close()
     torch.cuda.empty_cache()
     mid = fill + n // 2
+    load = {"file_bytes": int(blob.size), "data_bytes": int(f.meta["data_size"]), "seconds": round(load_s, 4),
+            "gbs_pcie_inclusive": round(blob.size / load_s / 1e9, 2),
+            "what": "nrq_nrm_open + nrq_model_load_nrm(verify): parse and meta CRC on the host, one hipMemcpy of "
+                    "the data section from pageable memory, data CRC on the device, tensor binding"}
     return {"workload": "Llama-3.2-1B architecture, all Q8_0, random init (16 layers, hidden 2048, 32/8 heads x 64, "
                         f"ffn 8192, tied 128256 head), f16 KV cache at positions {fill}..{fill + n - 1}, greedy",
             "tok_s": round(n / dt, 1), "ms_per_token": round(dt / n * 1e3, 4),
             "bytes_per_token": model_bytes_per_token(cfg, mid),
             "gbs": round(model_bytes_per_token(cfg, mid) * n / dt / 1e9, 1), "tokens": int(n),
-            "first_tokens": [int(t) for t in out[:4]]}
+            "first_tokens": [int(t) for t in out[:4]], "load": load, "verify_crc": crc}
 
 
 def host_cores():
@@ -311,6 +402,22 @@ def cpu_baseline_decode(seconds):
                       f"(scalar-order kernels, {threads} threads) in {dt:.1f} s"}
 
 
+def cpu_baseline_crc(seconds):
+    """The oracle's slicing-by-8 CRC-32 (crc32.rs) on one host core over 64 MiB
+    chunks for about `seconds`."""
+    import oracle as O
+
+    chunk = np.random.default_rng(9).integers(0, 256, 64 << 20, dtype=np.uint8)
+    n, c = 0, 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        c = O.crc32(chunk, c)
+        n += chunk.size
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{n >> 20} MiB of random bytes in 64 MiB calls, {dt:.1f} s"}
+
+
 def copy_calibration(nbytes):
     """Five device-to-device copies of `nbytes` (reads nbytes, writes nbytes):
     the reference kernel for scaling FETCH_SIZE / WRITE_SIZE counter readings."""
@@ -337,11 +444,22 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--also", default="cfg1,cfg3", help="other matvec configs reported beside (comma list)")
+    ap.add_argument("--crc-only", type=int, default=0, metavar="BYTES",
+                    help="only time nrq_dev_crc32 over BYTES random device bytes (profiling the CRC kernels)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (a known-size kernel for HBM counters)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration << 20)
+        return
+    if args.crc_only:
+        import torch
+
+        import nightrun_amd
+
+        nightrun_amd.init(0)
+        data = torch.randint(0, 256, (args.crc_only,), dtype=torch.uint8, device="cuda")
+        print(json.dumps({"crc_only": measure_crc(data, reps=args.steps)}))
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding of the path is design-only"}))
@@ -359,6 +477,7 @@ def main():
         cpu = cpu_baseline_matvec(args.config, args.cpu_seconds)
         if decode is not None:
             cpu["decode"] = cpu_baseline_decode(args.cpu_seconds)
+            cpu["verify_crc"] = cpu_baseline_crc(min(args.cpu_seconds, 5.0))
     dtype, rows, cols, _, desc = CONFIGS[args.config]
     out = {
         "metric": METRIC,

@@ -34,6 +34,15 @@ extern "C" {
 #define NRQ_ERR_DEVICE (-3)      /* HIP error, or no gfx950 device */
 #define NRQ_ERR_UNSUPPORTED (-4) /* row wider than the kernels' LDS tile */
 #define NRQ_ERR_NOT_INIT (-5)    /* nrq_init was not called */
+/* .nrm files: Model::parse's ParseError variants (crates/nr-model/src/format.rs:217-224)
+ * and Model::verify_data's failure (format.rs:409-422, VerifyError::DataCrc) */
+#define NRQ_ERR_NRM_TOO_SHORT (-10)      /* ParseError::TooShort */
+#define NRQ_ERR_NRM_BAD_MAGIC (-11)      /* ParseError::BadMagic */
+#define NRQ_ERR_NRM_BAD_VERSION (-12)    /* ParseError::BadVersion(v) */
+#define NRQ_ERR_NRM_META_CRC (-13)       /* ParseError::MetaCrc { expect, got } */
+#define NRQ_ERR_NRM_BAD_TABLE (-14)      /* ParseError::BadTable */
+#define NRQ_ERR_NRM_MISSING_TENSOR (-15) /* ParseError::MissingTensor(name) */
+#define NRQ_ERR_NRM_DATA_CRC (-16)       /* the data section's CRC does not match the header */
 
 /* weight dtypes: TensorDtype ids (crates/nr-model/src/format.rs:97-102) */
 #define NRQ_Q8_0 1
@@ -142,6 +151,7 @@ int nrq_sync(void *stream);
 #define NRQ_TENSOR_TOK_EMBED 1
 #define NRQ_TENSOR_OUTPUT_NORM 2
 #define NRQ_TENSOR_OUTPUT 3
+#define NRQ_TENSOR_ROPE_FREQS 4
 #define NRQ_TENSOR_ATTN_NORM 10
 #define NRQ_TENSOR_ATTN_Q 11
 #define NRQ_TENSOR_ATTN_K 12
@@ -167,6 +177,10 @@ int nrq_model_create(const nrq_model_config *cfg, nrq_model **out);
  * embedding until an NRQ_TENSOR_OUTPUT is set (infer.rs:415-419). The
  * embedding must be Q8_0. */
 int nrq_model_set_tensor(nrq_model *m, int kind, int layer, int dtype, const void *dev_ptr);
+/* Replaces the rope table (n = head_dim / 2 host floats), as InferCtx::new
+ * fills it from Llama-3 scaling or a RopeFreqs tensor (infer.rs:433-447).
+ * nrq_model_create sets the unscaled theta^(-2i/head_dim). */
+int nrq_model_set_rope_freqs(nrq_model *m, const float *freqs, int n);
 /* InferCtx::reset (infer.rs:494-496). */
 int nrq_model_reset(nrq_model *m);
 /* InferCtx::pos. */
@@ -182,6 +196,75 @@ int nrq_model_generate(nrq_model *m, uint32_t token, int n, uint32_t *out_tokens
 /* Copies the f16 KV cache ([n_layers][ctx][kv_dim] each) to host buffers. */
 int nrq_model_kv_cache(nrq_model *m, void *k, void *v, size_t bytes);
 int nrq_model_destroy(nrq_model *m);
+
+/* ---- .nrm v3 model files (crates/nr-model/src/format.rs, crc32.rs) -------------------
+ * Layout: 192-byte header | tokenizer blob | tensor table (32-byte entries) |
+ * data section (each tensor 64-byte aligned). meta_crc covers the header (its
+ * two CRC fields as zeros), the tokenizer blob and the table; data_crc the
+ * data section. CRC-32 is IEEE (reflected 0xEDB88320). */
+
+#define NRQ_ARCH_LLAMA3 1 /* Arch (format.rs:23-29) */
+#define NRQ_ARCH_QWEN3 2
+#define NRQ_ARCH_GRANITE 3
+#define NRQ_NRM_FLAG_TIED_EMBEDDINGS 1 /* format.rs:21 */
+#define NRQ_NRM_VERIFY_DATA 1          /* nrq_model_load_nrm flag: check data_crc on the device copy */
+
+/* Meta (format.rs:126-156) and the header's section fields (format.rs:297-306). */
+typedef struct {
+  uint32_t arch, dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, vocab, ctx_train;
+  float rope_theta, norm_eps, rope_factor, rope_low, rope_high, rope_orig_ctx;
+  uint32_t flags;
+  float embed_scale, attn_scale, residual_scale, logit_scale;
+  char name[48];
+  uint64_t tok_off, tok_size, table_off;
+  uint32_t tensor_count, data_crc, meta_crc, reserved;
+  uint64_t data_off, data_size;
+} nrq_nrm_meta;
+
+/* TensorEntry (format.rs:159-169); offset is from the start of the data section. */
+typedef struct {
+  uint32_t kind, layer, dtype, rows, cols, reserved;
+  uint64_t offset, size;
+} nrq_nrm_tensor_info;
+
+typedef struct nrq_nrm nrq_nrm;
+
+/* Model::parse (format.rs:260-406): header, scale sanity, region bounds (no
+ * wrapping sums), meta CRC, then every table entry (known dtype, inside the
+ * data section, 64-byte aligned offset, size == dtype block math). Host only;
+ * the blob must outlive the handle. Errors: NRQ_ERR_NRM_*, text in nrq_last_error. */
+int nrq_nrm_open(const void *blob, size_t len, nrq_nrm **out);
+int nrq_nrm_get_meta(const nrq_nrm *f, nrq_nrm_meta *out);
+/* i-th table entry, in file order. */
+int nrq_nrm_entry(const nrq_nrm *f, uint32_t i, nrq_nrm_tensor_info *out);
+/* Model::tensor (format.rs:424-435): the first entry of this kind and layer,
+ * else NRQ_ERR_NRM_MISSING_TENSOR naming it (format.rs:444-465). */
+int nrq_nrm_tensor(const nrq_nrm *f, int kind, int layer, nrq_nrm_tensor_info *out);
+/* Model::has_tensor (format.rs:437-439): 1 or 0. */
+int nrq_nrm_has_tensor(const nrq_nrm *f, int kind);
+/* Model::verify_data (format.rs:409-422) over a device copy of the data
+ * section (data_size bytes): the CRC runs on the GPU; synchronous.
+ * NRQ_ERR_NRM_DATA_CRC on a mismatch. */
+int nrq_nrm_verify_data(const nrq_nrm *f, const void *dev_data, void *stream);
+int nrq_nrm_close(nrq_nrm *f);
+
+/* crc32::checksum / Crc32::update (crc32.rs:38-79) on host bytes, with zlib's
+ * running-value convention: nrq_crc32(nrq_crc32(0, a), b) == nrq_crc32(0, a || b). */
+uint32_t nrq_crc32(uint32_t crc, const void *data, size_t n);
+/* The same CRC over n bytes in device memory (any alignment), enqueued on
+ * `stream`; the result is written to the device word *out. Calls that overlap
+ * on one device (different streams) share the library's partial-register
+ * buffer and must not run concurrently. */
+int nrq_dev_crc32(const void *data, size_t n, uint32_t crc, uint32_t *out, void *stream);
+
+/* InferCtx::new (infer.rs:352-447) over a parsed file: checks that every
+ * tensor of the Llama recipe is present with its shape (MissingTensor errors as
+ * the reference reports them), uploads the data section once, optionally
+ * verifies it on the device (NRQ_NRM_VERIFY_DATA), binds the tensors (the head
+ * tied to the embedding under FLAG_TIED_EMBEDDINGS) and sets the rope table.
+ * The model owns the device copy. Qwen3 files and non-neutral muP scales are
+ * NRQ_ERR_UNSUPPORTED (the device decode runs the Llama recipe). */
+int nrq_model_load_nrm(const nrq_nrm *f, int ctx, int flags, nrq_model **out);
 
 #ifdef __cplusplus
 }

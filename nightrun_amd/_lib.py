@@ -17,6 +17,14 @@ NRQ_ERR_SHAPE = -2
 NRQ_ERR_DEVICE = -3
 NRQ_ERR_UNSUPPORTED = -4
 NRQ_ERR_NOT_INIT = -5
+# .nrm files: Model::parse's ParseError variants, verify_data's failure
+NRQ_ERR_NRM_TOO_SHORT = -10
+NRQ_ERR_NRM_BAD_MAGIC = -11
+NRQ_ERR_NRM_BAD_VERSION = -12
+NRQ_ERR_NRM_META_CRC = -13
+NRQ_ERR_NRM_BAD_TABLE = -14
+NRQ_ERR_NRM_MISSING_TENSOR = -15
+NRQ_ERR_NRM_DATA_CRC = -16
 
 Q8_0, Q4_K, Q6_K = 1, 2, 3
 ORDER_SCALAR, ORDER_AVX2 = 0, 1
@@ -55,6 +63,17 @@ SIGNATURES = {
     "nrq_model_generate": ([_vp, C.c_uint32, _i, _vp, _vp], _i),
     "nrq_model_kv_cache": ([_vp, _vp, _vp, _sz], _i),
     "nrq_model_destroy": ([_vp], _i),
+    "nrq_model_set_rope_freqs": ([_vp, _vp, _i], _i),
+    "nrq_nrm_open": ([_vp, _sz, C.POINTER(_vp)], _i),
+    "nrq_nrm_get_meta": ([_vp, _vp], _i),
+    "nrq_nrm_entry": ([_vp, C.c_uint32, _vp], _i),
+    "nrq_nrm_tensor": ([_vp, _i, _i, _vp], _i),
+    "nrq_nrm_has_tensor": ([_vp, _i], _i),
+    "nrq_nrm_verify_data": ([_vp, _vp, _vp], _i),
+    "nrq_nrm_close": ([_vp], _i),
+    "nrq_crc32": ([C.c_uint32, _vp, _sz], C.c_uint32),
+    "nrq_dev_crc32": ([_vp, _sz, C.c_uint32, _vp, _vp], _i),
+    "nrq_model_load_nrm": ([_vp, _i, _i, C.POINTER(_vp)], _i),
 }
 
 

@@ -5,6 +5,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+struct nrq_model;
+
 namespace nrq {
 
 enum {
@@ -89,5 +91,7 @@ int launch_block_sums(int dtype, const void* w, const void* x, int32_t* out, int
 
 // Sets the message nrq_last_error() returns on this thread (nrq_api.hip).
 void set_last_error(const char* msg);
+// The model frees `dev` (a hipMalloc'd buffer its tensors point into) when destroyed.
+void model_adopt_buffer(nrq_model* m, void* dev);
 
 }  // namespace nrq

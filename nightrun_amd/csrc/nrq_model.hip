@@ -621,7 +621,12 @@ struct nrq_model {
   hipGraph_t graph = nullptr;
   int host_pos = 0;
   size_t att_lds = 0;
+  void* owned = nullptr;  // the data section a loader uploaded; freed with the model
 };
+
+namespace nrq {
+void model_adopt_buffer(nrq_model* m, void* dev) { m->owned = dev; }
+}  // namespace nrq
 
 namespace {
 
@@ -897,6 +902,14 @@ int nrq_model_set_tensor(nrq_model* m, int kind, int layer, int dtype, const voi
   return NRQ_OK;
 }
 
+int nrq_model_set_rope_freqs(nrq_model* m, const float* freqs, int n) {
+  if (!m || !freqs) return mfail(NRQ_ERR_ARG, "nrq_model_set_rope_freqs: null argument");
+  if (n != m->cfg.head_dim / 2) return mfail(NRQ_ERR_SHAPE, "nrq_model_set_rope_freqs: need head_dim / 2 values");
+  MHIP(hipStreamSynchronize(m->stream));
+  MHIP(hipMemcpy(m->freqs, freqs, (size_t)n * 4, hipMemcpyHostToDevice));
+  return NRQ_OK;
+}
+
 int nrq_model_reset(nrq_model* m) {
   if (!m) return mfail(NRQ_ERR_ARG, "nrq_model_reset: null handle");
   MHIP(hipStreamSynchronize(m->stream));
@@ -1018,7 +1031,7 @@ int nrq_model_destroy(nrq_model* m) {
   if (m->exec) hipGraphExecDestroy(m->exec);
   if (m->graph) hipGraphDestroy(m->graph);
   void* bufs[] = {m->freqs, m->rope_cs, m->kc, m->vc, m->x, m->x2, m->xb, m->q, m->k, m->v, m->attn, m->gate, m->up, m->xb2,
-                  m->logits, m->xq, m->xq2, m->ctl, m->out_tokens};
+                  m->logits, m->xq, m->xq2, m->ctl, m->out_tokens, m->owned};
   for (void* p : bufs)
     if (p) hipFree(p);
   if (m->stream) hipStreamDestroy(m->stream);

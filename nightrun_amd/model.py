@@ -44,6 +44,18 @@ class Model:
         self.h = h
         self._keep = []  # device tensors the model points at
 
+    @classmethod
+    def from_handle(cls, h, cfg: dict, ctx: int) -> "Model":
+        """Wraps a model the C ABI already created (nrq_model_load_nrm)."""
+        m = cls.__new__(cls)
+        m.cfg, m.ctx, m.h, m._keep = dict(cfg), ctx, h, []
+        return m
+
+    def set_rope_freqs(self, freqs) -> None:
+        """Replaces the rope table (head_dim/2 floats; InferCtx::new, infer.rs:433-447)."""
+        f = np.ascontiguousarray(freqs, np.float32)
+        _lib.check(_lib.lib().nrq_model_set_rope_freqs(self.h, f.ctypes.data, f.size))
+
     def close(self):
         if getattr(self, "h", None):
             _lib.lib().nrq_model_destroy(self.h)

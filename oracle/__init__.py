@@ -286,6 +286,10 @@ def _model_lib():
         L.nro_model_reset.argtypes = [vp]
         L.nro_model_kcache.argtypes, L.nro_model_kcache.restype = [vp], C.POINTER(C.c_uint16)
         L.nro_model_vcache.argtypes, L.nro_model_vcache.restype = [vp], C.POINTER(C.c_uint16)
+        L.nro_model_set_freqs.argtypes = [vp, vp]
+        for name in ("nro_crc32", "nro_crc32_bitwise"):
+            getattr(L, name).argtypes, getattr(L, name).restype = [C.c_uint32, vp, sz], C.c_uint32
+        L.nro_infer_freqs.argtypes = [vp, sz, C.c_float, C.c_float, C.c_float, C.c_float, C.c_float, vp]
         _model_sigs_done = True
     return L
 
@@ -346,6 +350,28 @@ def rope_freqs(head_dim: int, theta: float) -> np.ndarray:
     return out
 
 
+def infer_freqs(head_dim: int, theta: float, factor: float = 0.0, low: float = 0.0, high: float = 0.0,
+                orig_ctx: float = 0.0, factors=None) -> np.ndarray:
+    """InferCtx::new's rope table (infer.rs:433-447 over rope.rs:14-34)."""
+    out = np.zeros(head_dim // 2, np.float32)
+    f = None if factors is None else np.ascontiguousarray(factors, np.float32)
+    _model_lib().nro_infer_freqs(_p(out), head_dim, theta, factor, low, high, orig_ctx,
+                                 None if f is None else _p(f))
+    return out
+
+
+def crc32(data, crc: int = 0) -> int:
+    """CRC-32 of crates/nr-model/src/crc32.rs (slicing by 8), zlib running-value convention."""
+    b = np.frombuffer(bytes(data), np.uint8) if not isinstance(data, np.ndarray) else np.ascontiguousarray(data)
+    return _model_lib().nro_crc32(crc, b.ctypes.data if b.size else None, b.nbytes)
+
+
+def crc32_bitwise(data, crc: int = 0) -> int:
+    """The classic bit-at-a-time CRC-32 (crates/nr-model/tests/verify.rs:16-30)."""
+    b = np.frombuffer(bytes(data), np.uint8) if not isinstance(data, np.ndarray) else np.ascontiguousarray(data)
+    return _model_lib().nro_crc32_bitwise(crc, b.ctypes.data if b.size else None, b.nbytes)
+
+
 def rope_apply(x: np.ndarray, head_dim: int, freqs: np.ndarray, pos: int) -> np.ndarray:
     x = np.array(x, dtype=np.float32)
     f = np.ascontiguousarray(freqs, np.float32)
@@ -394,8 +420,10 @@ class Model:
                              cfg["ffn_dim"], cfg["vocab"], ctx)
         self.cfg, self.w, self.ctx = cfg, weights, ctx
         self.h = L.nro_model_new(dims, cfg["norm_eps"], cfg["rope_theta"], threads)
-        L.nro_model_set_globals(self.h, _p(weights["embed"]), weights["embed_dtype"], _p(weights["embed"]),
-                                weights["embed_dtype"], _p(weights["out_norm"]))
+        out = weights.get("output", weights["embed"])  # infer.rs:415-419: tied unless a head is given
+        out_dt = weights.get("output_dtype", weights["embed_dtype"])
+        L.nro_model_set_globals(self.h, _p(weights["embed"]), weights["embed_dtype"], _p(out), out_dt,
+                                _p(weights["out_norm"]))
         for l, lw in enumerate(weights["layers"]):
             ptrs = (C.c_void_p * 7)(*[lw[n].ctypes.data for n in LAYER_MATS])
             dts = (C.c_int * 7)(*[lw["dtypes"][n] for n in LAYER_MATS])
@@ -409,6 +437,12 @@ class Model:
     @property
     def pos(self) -> int:
         return _model_lib().nro_model_pos(self.h)
+
+    def set_freqs(self, freqs: np.ndarray) -> None:
+        """Replaces the rope table (head_dim/2 floats), e.g. with infer_freqs' scaled one."""
+        f = np.ascontiguousarray(freqs, np.float32)
+        assert f.size == self.cfg["head_dim"] // 2
+        _model_lib().nro_model_set_freqs(self.h, _p(f))
 
     def forward(self, token: int) -> np.ndarray:
         p = _model_lib().nro_model_forward(self.h, token)

@@ -373,6 +373,9 @@ void nro_model_set_layer(nro_model *m, int l, const void *const w[7], const int 
 
 int nro_model_pos(const nro_model *m) { return m->pos; }
 void nro_model_reset(nro_model *m) { m->pos = 0; }
+void nro_model_set_freqs(nro_model *m, const float *freqs) {
+    memcpy(m->freqs, freqs, (size_t)m->head_dim / 2 * sizeof(float));
+}
 const float *nro_model_logits(const nro_model *m) { return m->logits; }
 const uint16_t *nro_model_kcache(const nro_model *m) { return m->kc; }
 const uint16_t *nro_model_vcache(const nro_model *m) { return m->vc; }

@@ -145,11 +145,22 @@ void nro_model_set_layer(nro_model *m, int l, const void *const w[7], const int 
                          const float *ffn_norm);
 const float *nro_model_forward(nro_model *m, uint32_t token);                        /* infer.rs:510-595 */
 const float *nro_model_prefill_chunk(nro_model *m, const uint32_t *tokens, int n);   /* infer.rs:601-750 */
+/* replaces the rope table (head_dim/2 floats), as InferCtx::new fills it (infer.rs:433-447) */
+void nro_model_set_freqs(nro_model *m, const float *freqs);
 int nro_model_pos(const nro_model *m);
 void nro_model_reset(nro_model *m);
 const float *nro_model_logits(const nro_model *m);
 const uint16_t *nro_model_kcache(const nro_model *m);
 const uint16_t *nro_model_vcache(const nro_model *m);
+
+/* .nrm checksum (crates/nr-model/src/crc32.rs:6-79), zlib running-value
+ * convention; the bitwise form is the classic algorithm of
+ * crates/nr-model/tests/verify.rs:16-30. */
+uint32_t nro_crc32(uint32_t crc, const void *data, size_t n);
+uint32_t nro_crc32_bitwise(uint32_t crc, const void *data, size_t n);
+/* InferCtx::new's rope table (infer.rs:433-447, rope.rs:14-34); factors may be NULL */
+void nro_infer_freqs(float *out, size_t head_dim, float theta, float factor, float low, float high, float orig_ctx,
+                     const float *factors);
 
 #ifdef __cplusplus
 }

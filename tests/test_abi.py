@@ -16,13 +16,13 @@ HEADER = os.path.join(ROOT, "include", "nrq.h")
 
 def declared_symbols():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^(?:int|const char \*)\s*(nrq_\w+)\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^(?:int|uint32_t|const char \*)\s*(nrq_\w+)\(", text, flags=re.M)))
 
 
 def test_header_declares_the_c_abi():
     syms = declared_symbols()
     assert "nrq_init" in syms and "nrq_matvec_q8" in syms and "nrq_dev_matmul" in syms
-    assert len(syms) == 31
+    assert len(syms) == 42
 
 
 def test_library_exports_every_declared_symbol():
