@@ -19,7 +19,9 @@ Beside it, in the same JSON line:
                  init) with the KV cache filled to 1024 positions, each step one
                  HIP graph replay (nrq_model_generate); the model is loaded from
                  an in-memory .nrm file (load time beside it) and its data
-                 section's CRC-32 is timed on the device (verify_crc)
+                 section's CRC-32 is timed on the device (verify_crc); the
+                 1024-token prompt goes through the batched prefill
+                 (prefill tok/s beside it)
   cpu_baseline   the CPU oracle's AVX2 restatement of the matvec, and its
                  scalar-order restatement of the full decode step, timed on a
                  bounded sample on the host cores
@@ -328,12 +330,17 @@ def measure_decode(fill=1024, n=128):
     crc = {"workload": "CRC-32 (IEEE) of the Llama-3.2-1B-shape Q8_0 data section in HBM",
            **measure_crc(data, f.meta["data_crc"])}
     del data
-    first = int(np.random.default_rng(5).integers(0, cfg["vocab"]))
-    # fill the KV cache (greedy continuation of one random token)
-    toks = m.generate(first, fill)
+    # the prompt: `fill` random tokens through the batched prefill (64-token
+    # chunks), once untimed for warm-up, then timed from position 0
+    prompt = np.random.default_rng(5).integers(0, cfg["vocab"], fill).astype(np.uint32)
+    m.prefill(prompt[:64], logits=False)
+    m.reset()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    out = m.generate(int(toks[-1]), n)
+    lg = m.prefill(prompt)
+    pf_dt = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    out = m.generate(int(np.argmax(lg)), n)
     dt = time.perf_counter() - t0
     m.close()
     torch.cuda.empty_cache()
@@ -347,7 +354,11 @@ def measure_decode(fill=1024, n=128):
             "tok_s": round(n / dt, 1), "ms_per_token": round(dt / n * 1e3, 4),
             "bytes_per_token": model_bytes_per_token(cfg, mid),
             "gbs": round(model_bytes_per_token(cfg, mid) * n / dt / 1e9, 1), "tokens": int(n),
-            "first_tokens": [int(t) for t in out[:4]], "load": load, "verify_crc": crc}
+            "first_tokens": [int(t) for t in out[:4]], "load": load, "verify_crc": crc,
+            "prefill": {"tokens": int(fill), "chunks_of": 64, "seconds": round(pf_dt, 4),
+                        "tok_s": round(fill / pf_dt, 1),
+                        "what": "nrq_model_prefill of the random prompt from position 0 (KV 0..1023), host sync "
+                                "per chunk, logits of the last token copied back"}}
 
 
 def host_cores():

@@ -188,6 +188,13 @@ int nrq_model_pos(const nrq_model *m);
 /* InferCtx::forward (infer.rs:510-595): one token at the current position;
  * copies the logits to host `logits` (vocab floats) unless NULL. */
 int nrq_model_forward(nrq_model *m, uint32_t token, float *logits);
+/* InferCtx::prefill (infer.rs:753-759): the n prompt tokens in chunks of up to
+ * MAX_BATCH = 64, each chunk as prefill_chunk (infer.rs:601-750) does it:
+ * batched norms and matmuls (int8 MFMA), every row's rope and f16 KV append,
+ * then causal attention for all (head, token) pairs in one launch. The KV
+ * cache and the last token's logits (copied to host `logits`, vocab floats,
+ * unless NULL) are bit-identical to n forward steps. */
+int nrq_model_prefill(nrq_model *m, const uint32_t *tokens, int n, float *logits);
 /* Greedy generation: n steps of forward + argmax (sample.rs:33-35), each
  * step's token feeding the next, device-resident (one HIP graph per step).
  * out_tokens gets the n sampled ids; last_logits (optional) the last step's

@@ -64,6 +64,7 @@ SIGNATURES = {
     "nrq_model_kv_cache": ([_vp, _vp, _vp, _sz], _i),
     "nrq_model_destroy": ([_vp], _i),
     "nrq_model_set_rope_freqs": ([_vp, _vp, _i], _i),
+    "nrq_model_prefill": ([_vp, _vp, _i, _vp], _i),
     "nrq_nrm_open": ([_vp, _sz, C.POINTER(_vp)], _i),
     "nrq_nrm_get_meta": ([_vp, _vp], _i),
     "nrq_nrm_entry": ([_vp, C.c_uint32, _vp], _i),

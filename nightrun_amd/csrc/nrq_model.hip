@@ -173,6 +173,26 @@ __global__ void embed_q8_0_kernel(const uint8_t* __restrict__ E, const int* __re
   x[i] = (float)(int8_t)blk[2 + (i & 31)] * d;
 }
 
+// Prefill: the embedding rows of B tokens (x[i][:]) and each token's (cos, sin)
+// table at position base + i (base = ctl[CTL_POS]); grid (dim / 256, B).
+__global__ void embed_rows_q8_0_kernel(const uint8_t* __restrict__ E, const int* __restrict__ tokens,
+                                       const int* __restrict__ ctl, int dim, float* __restrict__ x,
+                                       const float* __restrict__ freqs, int half, float* __restrict__ rope_cs) {
+  const int row = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (blockIdx.x == 0 && (int)threadIdx.x < half) {
+    float sn, cs;
+    dev_sincosf((float)(ctl[CTL_POS] + row) * freqs[threadIdx.x], &sn, &cs);
+    rope_cs[(size_t)row * 2 * half + 2 * threadIdx.x] = cs;
+    rope_cs[(size_t)row * 2 * half + 2 * threadIdx.x + 1] = sn;
+  }
+  if (i >= dim) return;
+  const size_t tok = (size_t)(uint32_t)tokens[row];
+  const uint8_t* blk = E + (tok * (dim / 32) + i / 32) * kQ8_0Bytes;
+  const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+  x[(size_t)row * dim + i] = (float)(int8_t)blk[2 + (i & 31)] * d;
+}
+
 constexpr int kNormNT = 256;
 constexpr int kNormMax = 8192;
 constexpr int kNormPT = kNormMax / kNormNT;  // values per thread
@@ -183,11 +203,19 @@ constexpr int kNormPT = kNormMax / kNormNT;  // values per thread
 // (q8.rs:27-44). One workgroup; n <= kNormMax, a multiple of 256. Thread t
 // owns the 8-value runs t + 256k (four consecutive runs, an aligned lane quad,
 // make one Q8_0 block), loaded once, all loads issued before the first use;
-// wave 0 runs the sequential sum of squares.
+// wave 0 runs the sequential sum of squares. Workgroup r takes row r of
+// [rows][n] x, add, out and xq (one row per workgroup in a prefill chunk).
 __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, const float* __restrict__ add,
                                                        const float* __restrict__ w, int n, float eps,
                                                        float* __restrict__ out, uint8_t* __restrict__ xq) {
   __shared__ __align__(16) float sq[kNormMax];
+  {
+    const size_t r = blockIdx.x;
+    x += r * n;
+    if (add) add += r * n;
+    out += r * n;
+    if (xq) xq += r * (size_t)(n / 32) * kQ8_0Bytes;
+  }
   __shared__ float s_scale;
   const int tid = threadIdx.x;
   const int nrun = n >> 3;
@@ -257,6 +285,46 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
   }
 }
 
+// Prefill: rope::apply (rope.rs:49-65) on every query and key head of token i
+// = blockIdx.x at position base + i, queries in place, and the f16 KV append of
+// its key and value rows (infer.rs:642-651). A chunk appends all its rows
+// before any of its tokens attends, as prefill_chunk does.
+__global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q, const float* __restrict__ k,
+                                                          const float* __restrict__ v,
+                                                          const float* __restrict__ rope_cs,
+                                                          const int* __restrict__ ctl, int n_heads, int n_kv_heads,
+                                                          int hd, int ctx, int layer, uint16_t* __restrict__ kc,
+                                                          uint16_t* __restrict__ vc) {
+  const int i = blockIdx.x, half = hd / 2;
+  const int pos = ctl[CTL_POS] + i;
+  const float* cst = rope_cs + (size_t)i * hd;
+  float* qi = q + (size_t)i * n_heads * hd;
+  const float* ki = k + (size_t)i * n_kv_heads * hd;
+  const float* vi = v + (size_t)i * n_kv_heads * hd;
+  const size_t ctx8 = (size_t)ctx * 8;
+  auto kvi = [&](int g, int d) {
+    return ((size_t)layer * n_kv_heads + g) * hd * ctx + (size_t)(d >> 3) * ctx8 + (size_t)pos * 8 + (d & 7);
+  };
+  for (int idx = threadIdx.x; idx < n_heads * half; idx += blockDim.x) {
+    const int h = idx / half, j = idx % half;
+    const float cs = cst[2 * j], sn = cst[2 * j + 1];
+    const float a = qi[(size_t)h * hd + 2 * j], b = qi[(size_t)h * hd + 2 * j + 1];
+    qi[(size_t)h * hd + 2 * j] = a * cs - b * sn;
+    qi[(size_t)h * hd + 2 * j + 1] = a * sn + b * cs;
+  }
+  for (int idx = threadIdx.x; idx < n_kv_heads * half; idx += blockDim.x) {
+    const int g = idx / half, j = idx % half;
+    const float cs = cst[2 * j], sn = cst[2 * j + 1];
+    const float a = ki[(size_t)g * hd + 2 * j], b = ki[(size_t)g * hd + 2 * j + 1];
+    kc[kvi(g, 2 * j)] = (uint16_t)f32_to_f16_bits(a * cs - b * sn);
+    kc[kvi(g, 2 * j + 1)] = (uint16_t)f32_to_f16_bits(a * sn + b * cs);
+  }
+  for (int idx = threadIdx.x; idx < n_kv_heads * hd; idx += blockDim.x) {
+    const int g = idx / hd, d = idx % hd;
+    vc[kvi(g, d)] = (uint16_t)f32_to_f16_bits(vi[idx]);
+  }
+}
+
 constexpr int kAttNT = 1024;
 constexpr int kAttMaxCtx = 8192;
 constexpr int kAttProd = 8704;  // floats per product stage (head_dim x (chunk + 4) <= 8704)
@@ -280,8 +348,12 @@ constexpr int kAttProd = 8704;  // floats per product stage (head_dim x (chunk +
 //     dimension) add the current chunk, four positions per 16-byte LDS read.
 //  5. out (f32) and, when out_q8 != null, its Q8_0 blocks for the output
 //     projection.
+// With PF (prefill), workgroup (h, i) serves token i of a chunk at position
+// base + i: its query was roped by rope_append_kernel and every key and
+// value row, its own included, is read from the cache (the chunk's rows were
+// all appended before this launch); out and out_q8 are row i of [B][...].
 // LDS: att[ctx] | prod[2][kAttProd] | q[hd] | kcur[hd] | vcur[hd] | red[32]
-template <int HD>
+template <int HD, bool PF = false>
 __global__ __launch_bounds__(kAttNT) void attention_kernel(
     const float* __restrict__ q_in, const float* __restrict__ k_in, const float* __restrict__ v_in,
     const float* __restrict__ rope_cs, const int* __restrict__ ctl, int n_heads, int n_kv_heads, int ctx, int layer,
@@ -298,7 +370,14 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   constexpr bool kTwoRounds = HD <= 64;  // second round of key rows held in registers
   extern __shared__ __align__(16) float sm[];
   const int h = blockIdx.x, tid = threadIdx.x;
-  const int pos = ctl[CTL_POS], n = pos + 1;
+  const int tok = PF ? (int)blockIdx.y : 0;
+  const int pos = ctl[CTL_POS] + tok, n = pos + 1;
+  const int self = PF ? -1 : pos;  // the position served from LDS rather than the cache
+  if (PF) {
+    q_in += (size_t)tok * n_heads * hd;
+    out += (size_t)tok * n_heads * hd;
+    if (out_q8) out_q8 += (size_t)tok * (n_heads * hd / 32) * kQ8_0Bytes;
+  }
   const int gqa = n_heads / n_kv_heads, g = h / gqa;
   const bool writer = (h % gqa) == 0;
   float* att = sm;
@@ -318,7 +397,7 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
 
   uint4 kr[g8], kr2[kTwoRounds ? g8 : 1];
   auto load_key = [&](int t, uint4* r) {
-    if (t < n && t != pos) {
+    if (t < n && t != self) {
       const uint4* src = (const uint4*)(kc + base + (size_t)t * 8);
 #pragma unroll
       for (int j = 0; j < g8; j++) r[j] = src[(size_t)j * ctx];
@@ -332,7 +411,7 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
       const int idx = ptid + nprod * j;
       const int tl = idx % C, i0 = 8 * (idx / C);
       const int t = c * C + tl;
-      if (idx < npc && t < n && t != pos) r[j] = *(const uint4*)(vc + kvi(t, i0));
+      if (idx < npc && t < n && t != self) r[j] = *(const uint4*)(vc + kvi(t, i0));
     }
   };
   uint4 s0[2], s1[2], s2[2];  // value rows of chunks k with k % 3 == 0, 1, 2
@@ -343,6 +422,9 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
     vload(1, s1);
     vload(2, s2);
   }
+  if (PF) {
+    for (int i = tid; i < hd; i += kAttNT) qs[i] = q_in[(size_t)h * hd + i];
+  } else {
   for (int i = tid; i < half; i += kAttNT) {
     const float cs = rope_cs[2 * i], sn = rope_cs[2 * i + 1];
     const float qa = q_in[(size_t)h * hd + 2 * i], qb = q_in[(size_t)h * hd + 2 * i + 1];
@@ -362,12 +444,13 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
     vcur[i] = f16_bits_to_f32(vb);
     if (writer) vc[kvi(pos, i)] = (uint16_t)vb;
   }
+  }
   __syncthreads();
   // Scores: thread tid takes positions tid, tid + kAttNT, ...
   float mx = -INFINITY;
   auto score = [&](int t, const uint4* r) {
     float s = 0.0f;
-    if (t == pos) {
+    if (t == self) {
       for (int i = 0; i < hd; i++) s = s + kcur[i] * qs[i];
     } else {
 #pragma unroll
@@ -423,7 +506,7 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
       if (idx >= npc || t >= n) continue;
       const float a = att[t];
       float vv[8];
-      if (t == pos) {
+      if (t == self) {
 #pragma unroll
         for (int q = 0; q < 8; q++) vv[q] = vcur[i0 + q];
       } else {
@@ -622,6 +705,11 @@ struct nrq_model {
   int host_pos = 0;
   size_t att_lds = 0;
   void* owned = nullptr;  // the data section a loader uploaded; freed with the model
+  // prefill scratch, [kMaxBatch][*], made at the first prefill
+  float *bx = nullptr, *bxb = nullptr, *bxn = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+  float *battn = nullptr, *bgate = nullptr, *bup = nullptr, *brope = nullptr;
+  uint8_t *bxq = nullptr, *bxq2 = nullptr;
+  int* btok = nullptr;
 };
 
 namespace nrq {
@@ -786,6 +874,137 @@ int enqueue_step(nrq_model* m) {
   return NRQ_OK;
 }
 
+constexpr int kMaxBatch = 64;  // MAX_BATCH (infer.rs:101)
+
+int prefill_alloc(nrq_model* m) {
+  if (m->bx) return NRQ_OK;
+  const auto& c = m->cfg;
+  const size_t B = kMaxBatch, maxd = (size_t)m->maxd;
+  struct {
+    void** p;
+    size_t bytes;
+  } allocs[] = {
+      {(void**)&m->bx, B * c.dim * 4},          {(void**)&m->bxb, B * c.dim * 4},
+      {(void**)&m->bxn, B * maxd * 4},          {(void**)&m->bq, B * m->att_dim * 4},
+      {(void**)&m->bk, B * m->kv_dim * 4},      {(void**)&m->bv, B * m->kv_dim * 4},
+      {(void**)&m->battn, B * m->att_dim * 4},  {(void**)&m->bgate, B * c.ffn_dim * 4},
+      {(void**)&m->bup, B * c.ffn_dim * 4},     {(void**)&m->brope, B * c.head_dim * 4},
+      {(void**)&m->bxq, B * act_bytes(NRQ_Q8_0, maxd) + 64}, {(void**)&m->bxq2, B * act_bytes(NRQ_Q4_K, maxd) + 64},
+      {(void**)&m->btok, B * 4},
+  };
+  for (auto& a : allocs) MHIP(hipMalloc(a.p, a.bytes));
+  return NRQ_OK;
+}
+
+int matmul_rows(nrq_model* m, const Mat& w, const uint8_t* xs, float* y, int rows, int cols, int B) {
+  nrq::MatmulLaunch L;
+  L.w = w.w;
+  L.xs = xs;
+  L.y = y;
+  L.rows = rows;
+  L.bpr = cols / qk_of(w.dt);
+  L.batch = B;
+  L.stream = m->stream;
+  const int rc = nrq::launch_matmul(w.dt, nrq::kOrderScalar, L);
+  return rc ? mfail(rc == nrq::NRQ_LAUNCH_TOO_WIDE ? NRQ_ERR_UNSUPPORTED : NRQ_ERR_DEVICE, "model: matmul launch failed")
+            : NRQ_OK;
+}
+
+// Matmuls of one [B][cols] input (Acts::matmul_group, infer.rs:180-228): the
+// rows are quantized once per format; m->bxq holds the Q8_0 blocks when
+// `have_q8` (written by the producing kernel), m->bxq2 the Q8_K ones.
+int matmul_group_rows(nrq_model* m, const Mat* const* ws, float* const* ys, const int* rows, int n, const float* x,
+                      int cols, int B, bool have_q8) {
+  bool need_q8 = false, need_q8k = false;
+  for (int i = 0; i < n; i++) (ws[i]->dt == NRQ_Q8_0 ? need_q8 : need_q8k) = true;
+  int rc;
+  if (need_q8 && !have_q8 && (rc = quantize_for(m, NRQ_Q8_0, x, B * cols, m->bxq))) return rc;
+  if (need_q8k && (rc = quantize_for(m, NRQ_Q4_K, x, B * cols, m->bxq2))) return rc;
+  for (int i = 0; i < n; i++)
+    if ((rc = matmul_rows(m, *ws[i], ws[i]->dt == NRQ_Q8_0 ? m->bxq : m->bxq2, ys[i], rows[i], cols, B))) return rc;
+  return NRQ_OK;
+}
+
+bool any_q8(const Mat* const* ws, int n) {
+  for (int i = 0; i < n; i++)
+    if (ws[i]->dt == NRQ_Q8_0) return true;
+  return false;
+}
+
+// InferCtx::prefill_chunk (infer.rs:601-750) for B tokens at positions
+// pos..pos+B-1 (ctl[CTL_POS] = pos): batched norms and matmuls, all the
+// chunk's K/V appended, then causal attention for every (head, token); the
+// last token's logits. Each kernel computes a row exactly as the decode step
+// does, so the KV cache and logits equal B forward steps bit for bit.
+int enqueue_prefill(nrq_model* m, int B) {
+  const auto& c = m->cfg;
+  const int d = c.dim, kvd = m->kv_dim, att = m->att_dim, ffn = c.ffn_dim;
+  hipLaunchKernelGGL(nrq::embed_rows_q8_0_kernel, dim3((d + 255) / 256, B), dim3(256), 0, m->stream,
+                     (const uint8_t*)m->embed.w, m->btok, m->ctl, d, m->bx, m->freqs, c.head_dim / 2, m->brope);
+  if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: embed launch failed");
+  const float scale = 1.0f / sqrtf((float)c.head_dim);
+  const float* pending = nullptr;
+  int rc;
+  for (int l = 0; l < c.n_layers; l++) {
+    const Layer& Ly = m->L[l];
+    {
+      const Mat* ws[3] = {&Ly.m[0], &Ly.m[1], &Ly.m[2]};
+      float* ys[3] = {m->bq, m->bk, m->bv};
+      const int rows[3] = {att, kvd, kvd};
+      const bool q8 = any_q8(ws, 3);
+      hipLaunchKernelGGL(nrq::norm_kernel, dim3(B), dim3(nrq::kNormNT), 0, m->stream, m->bx, pending, Ly.attn_norm,
+                         d, c.norm_eps, m->bxn, q8 ? m->bxq : nullptr);
+      if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: norm launch failed");
+      if ((rc = matmul_group_rows(m, ws, ys, rows, 3, m->bxn, d, B, q8))) return rc;
+    }
+    hipLaunchKernelGGL(nrq::rope_append_kernel, dim3(B), dim3(256), 0, m->stream, m->bq, m->bk, m->bv, m->brope,
+                       m->ctl, c.n_heads, c.n_kv_heads, c.head_dim, c.ctx, l, m->kc, m->vc);
+    if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: rope launch failed");
+    {
+      const bool q8 = Ly.m[3].dt == NRQ_Q8_0;
+      auto* kern = c.head_dim == 32   ? nrq::attention_kernel<32, true>
+                   : c.head_dim == 64 ? nrq::attention_kernel<64, true>
+                   : c.head_dim == 96 ? nrq::attention_kernel<96, true>
+                                      : nrq::attention_kernel<128, true>;
+      hipLaunchKernelGGL(kern, dim3(c.n_heads, B), dim3(nrq::kAttNT), m->att_lds, m->stream, m->bq, m->bk, m->bv,
+                         m->brope, m->ctl, c.n_heads, c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->battn,
+                         q8 ? m->bxq : nullptr);
+      if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: attention launch failed");
+      const Mat* ws[1] = {&Ly.m[3]};
+      float* ys[1] = {m->bxb};
+      const int rows[1] = {d};
+      if ((rc = matmul_group_rows(m, ws, ys, rows, 1, m->battn, att, B, q8))) return rc;
+    }
+    {
+      const Mat* ws[2] = {&Ly.m[4], &Ly.m[5]};
+      float* ys[2] = {m->bgate, m->bup};
+      const int rows[2] = {ffn, ffn};
+      const bool q8 = any_q8(ws, 2);
+      hipLaunchKernelGGL(nrq::norm_kernel, dim3(B), dim3(nrq::kNormNT), 0, m->stream, m->bx, m->bxb, Ly.ffn_norm, d,
+                         c.norm_eps, m->bxn, q8 ? m->bxq : nullptr);
+      if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: norm launch failed");
+      if ((rc = matmul_group_rows(m, ws, ys, rows, 2, m->bxn, d, B, q8))) return rc;
+    }
+    {
+      const bool q8 = Ly.m[6].dt == NRQ_Q8_0;
+      const long long n = (long long)B * ffn;
+      hipLaunchKernelGGL(nrq::swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, m->stream, m->bgate,
+                         m->bup, (int)n, q8 ? m->bxq : nullptr);
+      if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: swiglu launch failed");
+      const Mat* ws[1] = {&Ly.m[6]};
+      float* ys[1] = {m->bxb};
+      const int rows[1] = {d};
+      if ((rc = matmul_group_rows(m, ws, ys, rows, 1, m->bgate, ffn, B, q8))) return rc;
+    }
+    pending = m->bxb;
+  }
+  // only the last token's logits (infer.rs:738-745); the other rows' final
+  // residual add is never read
+  const size_t last = (size_t)(B - 1) * d;
+  if ((rc = norm_quant(m, m->bx + last, pending + last, m->out_norm, m->output.dt))) return rc;
+  return matvec(m, m->output, m->xq, m->logits, c.vocab, d);
+}
+
 int check_ready(nrq_model* m, const char* name) {
   if (!m) return mfail(NRQ_ERR_ARG, "model: null handle");
   if (!m->embed.w || !m->out_norm || !m->output.w) return mfail(NRQ_ERR_ARG, "model: embedding/output tensors not set");
@@ -940,6 +1159,35 @@ int nrq_model_forward(nrq_model* m, uint32_t token, float* logits_host) {
   return NRQ_OK;
 }
 
+int nrq_model_prefill(nrq_model* m, const uint32_t* tokens, int n, float* logits_host) {
+  int rc = check_ready(m, "nrq_model_prefill");
+  if (rc) return rc;
+  // infer.rs:754: assert!(!tokens.is_empty())
+  if (n <= 0) return mfail(NRQ_ERR_SHAPE, "assertion failed: !tokens.is_empty()");
+  if (!tokens) return mfail(NRQ_ERR_ARG, "nrq_model_prefill: null tokens");
+  for (int i = 0; i < n; i++)
+    if (tokens[i] >= (uint32_t)m->cfg.vocab) return mfail(NRQ_ERR_ARG, "nrq_model_prefill: token out of vocabulary");
+  // infer.rs:605 (checked per chunk there; the chunks are consecutive)
+  if (m->host_pos + n > m->cfg.ctx)
+    return mfail(NRQ_ERR_SHAPE, "assertion failed: self.pos + b <= d.ctx: context window exhausted");
+  if ((rc = prefill_alloc(m))) return rc;
+  for (int i0 = 0; i0 < n; i0 += kMaxBatch) {
+    const int B = std::min(kMaxBatch, n - i0);
+    const int base = m->host_pos;
+    MHIP(hipMemcpyAsync(m->btok, tokens + i0, (size_t)B * 4, hipMemcpyHostToDevice, m->stream));
+    MHIP(hipMemcpyAsync(m->ctl + nrq::CTL_POS, &base, 4, hipMemcpyHostToDevice, m->stream));
+    if ((rc = enqueue_prefill(m, B))) return rc;
+    const int next = base + B;
+    MHIP(hipMemcpyAsync(m->ctl + nrq::CTL_POS, &next, 4, hipMemcpyHostToDevice, m->stream));
+    MHIP(hipStreamSynchronize(m->stream));  // the host values copied above stay valid until here
+    m->host_pos = next;
+  }
+  if (logits_host)
+    MHIP(hipMemcpyAsync(logits_host, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost, m->stream));
+  MHIP(hipStreamSynchronize(m->stream));
+  return NRQ_OK;
+}
+
 int nrq_model_generate(nrq_model* m, uint32_t token, int n, uint32_t* out_tokens, float* last_logits) {
   int rc = check_ready(m, "nrq_model_generate");
   if (rc) return rc;
@@ -1031,7 +1279,8 @@ int nrq_model_destroy(nrq_model* m) {
   if (m->exec) hipGraphExecDestroy(m->exec);
   if (m->graph) hipGraphDestroy(m->graph);
   void* bufs[] = {m->freqs, m->rope_cs, m->kc, m->vc, m->x, m->x2, m->xb, m->q, m->k, m->v, m->attn, m->gate, m->up, m->xb2,
-                  m->logits, m->xq, m->xq2, m->ctl, m->out_tokens, m->owned};
+                  m->logits, m->xq, m->xq2, m->ctl, m->out_tokens, m->owned, m->bx, m->bxb, m->bxn, m->bq,
+                  m->bk, m->bv, m->battn, m->bgate, m->bup, m->brope, m->bxq, m->bxq2, m->btok};
   for (void* p : bufs)
     if (p) hipFree(p);
   if (m->stream) hipStreamDestroy(m->stream);

@@ -5,6 +5,7 @@ tensors that live in HBM.
     m = Model(cfg, ctx=1152)
     m.set_weights(weights)            # numpy block arrays -> HBM, bound once
     logits = m.forward(token)          # InferCtx::forward
+    logits = m.prefill(prompt)         # InferCtx::prefill, 64-token batched chunks
     toks = m.generate(token, n)        # greedy (sample.rs:33-35), one HIP graph per step
 
 torch provides the device memory; every computation is a libnrq kernel.
@@ -96,6 +97,14 @@ class Model:
     def forward(self, token: int, logits: bool = True):
         out = np.empty(self.cfg["vocab"], np.float32) if logits else None
         _lib.check(_lib.lib().nrq_model_forward(self.h, int(token), out.ctypes.data if logits else None))
+        return out
+
+    def prefill(self, tokens, logits: bool = True):
+        """InferCtx::prefill (infer.rs:753-759): the prompt in 64-token chunks, each one
+        batched pass; returns the last token's logits."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty(self.cfg["vocab"], np.float32) if logits else None
+        _lib.check(_lib.lib().nrq_model_prefill(self.h, t.ctypes.data, t.size, out.ctypes.data if logits else None))
         return out
 
     def generate(self, token: int, n: int, logits: bool = False):

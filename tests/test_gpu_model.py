@@ -65,15 +65,17 @@ def test_device_expf_sincosf_bitexact(gpu, oracle):
         assert_bitwise(got[~nan], want[~nan], name)
 
 
-def run_pair(oracle, cfg, weights, ctx, prompt, n_gen, check_kv=True):
+def run_pair(oracle, cfg, weights, ctx, prompt, n_gen, check_kv=True, prefill=False):
     """Feeds `prompt` then generates n_gen tokens greedily on both sides.
-    The GPU takes the prompt one forward step at a time, the oracle in
-    64-token prefill chunks (bitwise equal by the reference's prefill
-    invariant, crates/nr-model/tests/prefill.rs)."""
+    The oracle takes the prompt in 64-token prefill chunks; the GPU one
+    forward step at a time, or with `prefill` in its own 64-token batched
+    chunks (bitwise equal by the reference's prefill invariant,
+    crates/nr-model/tests/prefill.rs)."""
     from nightrun_amd.model import Model
 
     ref = oracle.Model(cfg, weights, ctx=ctx, threads=THREADS)
     want_logits = ref.prefill(prompt)
+    ref_prompt_logits = want_logits.copy()
     tok = oracle.argmax(want_logits)
     want_tokens = []
     for _ in range(n_gen):
@@ -85,8 +87,13 @@ def run_pair(oracle, cfg, weights, ctx, prompt, n_gen, check_kv=True):
     m = Model(cfg, ctx)
     try:
         m.set_weights(weights)
-        for i, t in enumerate(prompt):
-            lg = m.forward(int(t), logits=(i == len(prompt) - 1))
+        if prefill:
+            lg = m.prefill(prompt)
+            assert m.pos == len(prompt)
+            assert_bitwise(lg, ref_prompt_logits, "prompt logits")
+        else:
+            for i, t in enumerate(prompt):
+                lg = m.forward(int(t), logits=(i == len(prompt) - 1))
         first = int(np.argmax(lg)) if lg is not None else None
         # the first generated token comes from the prompt's last logits
         assert first == want_tokens[0], (first, want_tokens[0])
@@ -165,4 +172,72 @@ def test_llama_1b_greedy_token_identical(gpu, oracle):
     cfg = oracle.LLAMA_1B
     w = oracle.gen_model(cfg, 0x5EED0005)
     prompt = np.random.default_rng(0x5EED0005).integers(0, cfg["vocab"], 1024).astype(np.uint32)
-    run_pair(oracle, cfg, w, 1152, prompt, 128)
+    run_pair(oracle, cfg, w, 1152, prompt, 128, prefill=True)
+
+
+@pytest.mark.parametrize("n", [1, 5, 63, 64, 65, 70, 130])
+def test_tiny_model_prefill(gpu, oracle, n):
+    """Device prefill (64-token batched chunks) == the oracle's prefill: the
+    prompt's last logits, the KV cache, and the greedy continuation."""
+    w = oracle.gen_model(TINY, 2000 + n)
+    prompt = np.random.default_rng(n).integers(0, TINY["vocab"], n).astype(np.uint32)
+    run_pair(oracle, TINY, w, 160, prompt, 6, prefill=True)
+
+
+def test_tiny_model_prefill_kquant(gpu, oracle):
+    """Q4_K q/k/v/o/gate/up and Q6_K down (Q8_K activations through the 32x32
+    MFMA kernels), an untied Q6_K head."""
+    w = oracle.gen_model(TINY, 4322)
+    shapes = oracle.layer_shapes(TINY)
+    for l, lw in enumerate(w["layers"]):
+        for i, name in enumerate(oracle.LAYER_MATS):
+            dt = 3 if name == "w_down" else 2
+            rows, cols = shapes[name]
+            lw[name] = oracle.gen_weights(dt, 1777 + 16 * l + i, rows, cols)
+            lw["dtypes"][name] = dt
+    w["output"] = oracle.gen_weights(3, 4444, TINY["vocab"], TINY["dim"])
+    w["output_dtype"] = 3
+    prompt = np.random.default_rng(9).integers(0, TINY["vocab"], 100).astype(np.uint32)
+    run_pair(oracle, TINY, w, 128, prompt, 5, prefill=True)
+
+
+def test_prefill_after_decode_steps(gpu, oracle):
+    """Prefill at a non-zero position: forward steps, then a 67-token prefill
+    (chunks of 64 and 3 starting at position 3), then decode."""
+    from nightrun_amd.model import Model
+
+    w = oracle.gen_model(TINY, 77)
+    toks = np.random.default_rng(77).integers(0, TINY["vocab"], 70).astype(np.uint32)
+    ref = oracle.Model(TINY, w, ctx=96, threads=THREADS)
+    m = Model(TINY, 96)
+    try:
+        m.set_weights(w)
+        for t in toks[:3]:
+            assert_bitwise(m.forward(int(t)), ref.forward(int(t)), "forward")
+        assert_bitwise(m.prefill(toks[3:]), ref.prefill(toks[3:]), "prefill at position 3")
+        assert m.pos == 70
+        k, v = m.kv_cache()
+        rk, rv = ref.kv_cache()
+        assert np.array_equal(k, rk) and np.array_equal(v, rv), "KV cache differs"
+        assert_bitwise(m.forward(5), ref.forward(5), "decode after prefill")
+    finally:
+        m.close()
+
+
+def test_prefill_context_exhausted_panics(gpu, oracle):
+    """infer.rs:605: a chunk past the context asserts; an empty prompt asserts (infer.rs:754)."""
+    from nightrun_amd import NrPanic
+    from nightrun_amd.model import Model
+
+    w = oracle.gen_model(TINY, 6)
+    m = Model(TINY, 40)
+    try:
+        m.set_weights(w)
+        m.prefill(np.arange(30, dtype=np.uint32), logits=False)
+        with pytest.raises(NrPanic, match="context window exhausted"):
+            m.prefill(np.arange(11, dtype=np.uint32), logits=False)
+        with pytest.raises(NrPanic, match="is_empty"):
+            m.prefill(np.arange(0, dtype=np.uint32), logits=False)
+        assert m.pos == 30
+    finally:
+        m.close()
