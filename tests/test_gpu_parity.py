@@ -424,24 +424,28 @@ def test_matmul_adversarial_and_saturated(gpu, oracle, dtype):
                        oracle.matmul(dtype, 0, ws, xs, rows, cols, batch))
 
 
-@pytest.mark.parametrize("dtype", [2, 3])
+@pytest.mark.parametrize("dtype", [1, 2, 3])
 def test_matmul_every_split_count(gpu, oracle, dtype, monkeypatch):
-    """The K-quant prefill kernel splits a 32 x 32 tile's blocks over 1, 2, 4 or
-    8 waves and holds one or two blocks of loads in registers (chosen by shape;
-    NRQ_MMT_SPLITS and NRQ_MMT_DB force them). Every combination gives the
+    """The 32 x 32 prefill kernel (Q8_0, Q4_K, Q6_K) splits a tile's blocks over 1, 2, 4 or
+    8 waves and holds one, two or (Q8_0) four blocks of loads in registers
+    (chosen by shape; NRQ_MMT_SPLITS and NRQ_MMT_NB force them). Every combination gives the
     oracle's bits: odd block counts (the last round partly empty), a
     partial token tile, batches past 64 and fewer than 32 tokens."""
     qk = oracle.QK[dtype]
     cases = []
-    for rows, bpr, batch in ((96, 8, 64), (40, 37, 33), (50, 3, 130), (20, 11, 5)):
+    shapes = ((96, 8, 64), (40, 37, 33), (50, 3, 130), (20, 11, 5))
+    if dtype == 1:  # Q8_0 takes these tiles from 1024 rows
+        shapes = ((1024, 8, 64), (1100, 37, 33), (1030, 3, 130), (1056, 11, 5))
+    for rows, bpr, batch in shapes:
         cols = bpr * qk
         w = oracle.gen_weights(dtype, 800 + bpr, rows, cols)
         xs = oracle.quantize_act(dtype, oracle.Rng(801 + bpr).normal(batch * cols))
         cases.append((rows, cols, batch, w, xs, oracle.matmul(dtype, 0, w, xs, rows, cols, batch, threads=THREADS)))
-    for db in ("0", "1"):
-        monkeypatch.setenv("NRQ_MMT_DB", db)
+    # register buffers of block loads: 1 or 2, and a ring of 4 for Q8_0
+    for nb in ("1", "2", "4") if dtype == 1 else ("1", "2"):
+        monkeypatch.setenv("NRQ_MMT_NB", nb)
         for ks in ("1", "2", "4", "8"):
             monkeypatch.setenv("NRQ_MMT_SPLITS", ks)
             for rows, cols, batch, w, xs, want in cases:
                 assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, batch), want,
-                               f"splits {ks} double buffer {db} rows {rows} cols {cols} batch {batch}")
+                               f"splits {ks} buffers {nb} rows {rows} cols {cols} batch {batch}")
