@@ -200,6 +200,19 @@ int nrq_model_prefill(nrq_model *m, const uint32_t *tokens, int n, float *logits
  * out_tokens gets the n sampled ids; last_logits (optional) the last step's
  * logits. */
 int nrq_model_generate(nrq_model *m, uint32_t token, int n, uint32_t *out_tokens, float *last_logits);
+/* Sampler::new (sample.rs:15-21) for nrq_model_generate: temperature <= 0 is
+ * greedy (argmax, the default); otherwise each step draws from the 64 largest
+ * logits at `temperature`, cut to the shortest prefix whose probability
+ * reaches top_p (sample.rs:32-96), with the xorshift state seed | 1 kept on
+ * the device. Exact logit ties among the candidates are ordered by token id. */
+int nrq_model_set_sampler(nrq_model *m, float temperature, float top_p, uint64_t seed);
+/* The sampler's state after the draws so far. */
+int nrq_model_sampler_state(nrq_model *m, uint64_t *state);
+/* Sampler::sample over n device logits: the drawn id to the device word
+ * *token; *rng (device) is the state, advanced once per draw at temperature
+ * > 0. Enqueued on `stream`. */
+int nrq_dev_sample(const float *logits, int n, float temperature, float top_p, uint64_t *rng, uint32_t *token,
+                   void *stream);
 /* Copies the f16 KV cache ([n_layers][ctx][kv_dim] each) to host buffers. */
 int nrq_model_kv_cache(nrq_model *m, void *k, void *v, size_t bytes);
 int nrq_model_destroy(nrq_model *m);

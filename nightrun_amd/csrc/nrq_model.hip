@@ -568,7 +568,8 @@ __global__ __launch_bounds__(256) void swiglu_kernel(float* __restrict__ gate, c
 constexpr int kArgNT = 1024;
 
 // vec.rs:80-90 (first index of the largest value; NaN never wins), then the
-// step's bookkeeping: next token, output slot, position + 1.
+// step's bookkeeping: next token, output slot, position + 1 (without ctl, only
+// out_tokens[0]).
 __global__ __launch_bounds__(kArgNT) void argmax_kernel(const float* __restrict__ x, int n, int* __restrict__ ctl,
                                                         uint32_t* __restrict__ out_tokens, int max_out) {
   __shared__ float sv[kArgNT / 64];
@@ -627,11 +628,198 @@ __global__ __launch_bounds__(kArgNT) void argmax_kernel(const float* __restrict_
         bi = si[wv];
       }
     const int best = bi == 0x7fffffff ? 0 : bi;
+    if (!ctl) {  // a lone draw (nrq_dev_sample): the id only
+      out_tokens[0] = (uint32_t)best;
+      return;
+    }
     ctl[CTL_TOKEN] = best;
     const int step = ctl[CTL_STEP];
     if (out_tokens && step < max_out) out_tokens[step] = (uint32_t)best;
     ctl[CTL_STEP] = step + 1;
     ctl[CTL_POS] = ctl[CTL_POS] + 1;
+  }
+}
+
+constexpr int kSampNT = 1024;
+constexpr int kTopK = 64;  // sample.rs:12
+
+// Sampler::next_f32 (sample.rs:23-30)
+__device__ inline float sampler_next_f32(unsigned long long* rng) {
+  unsigned long long x = *rng;
+  x ^= x << 13;
+  x ^= x >> 7;
+  x ^= x << 17;
+  *rng = x;
+  return (float)(x >> 40) / (float)(1u << 24);
+}
+
+// Sampler::sample (sample.rs:32-96) for temperature > 0, one workgroup.
+//  1. The 64 largest logits (NaN and -inf never qualify, as the heap's strict
+//     > never admits them): an 8-bit radix select over order-preserving keys
+//     finds the 64th largest key K (per-wave histograms, four passes); every
+//     logit above K and the first (by token id) of those equal to K are taken.
+//     Exact ties are thus ordered by token id; the reference's unstable sort
+//     leaves their order open, and is matched whenever the drawn logit is not
+//     tied. Fewer than 64 valid logits leave (-inf, 0) slots, as the heap's
+//     initial entries do.
+//  2. Descending order: each candidate's rank among the others.
+//  3. One lane, in the reference's order: p_i = expf((v_i - max) / T), the
+//     running sums, the nucleus cut, r = next_f32() * cum, the draw.
+// With ctl, the step's bookkeeping of argmax_kernel; else the id goes to *token.
+__global__ __launch_bounds__(kSampNT) void sample_kernel(const float* __restrict__ x, int n, float temperature,
+                                                         float top_p, unsigned long long* __restrict__ rng,
+                                                         int* __restrict__ ctl, uint32_t* __restrict__ out_tokens,
+                                                         int max_out, uint32_t* __restrict__ token) {
+  constexpr int NW = kSampNT / 64;
+  __shared__ int hist[NW][256];
+  __shared__ int total[256];
+  __shared__ uint32_t s_prefix, s_mask;
+  __shared__ int s_need, s_all, s_slot;
+  __shared__ int scan[kSampNT];
+  __shared__ float cv[kTopK], sv[kTopK], pr[kTopK];
+  __shared__ uint32_t ci[kTopK], si[kTopK];
+  const int tid = threadIdx.x, wv = tid >> 6;
+  const int chunk = (n + kSampNT - 1) / kSampNT;
+  const int c0 = min(n, tid * chunk), c1 = min(n, c0 + chunk);
+  auto key_of = [](float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  };
+  if (tid == 0) {
+    s_prefix = 0;
+    s_mask = 0;
+    s_need = kTopK;
+    s_all = 0;
+    s_slot = 0;
+  }
+  __syncthreads();
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int b = tid; b < NW * 256; b += kSampNT) (&hist[0][0])[b] = 0;
+    __syncthreads();
+    const uint32_t prefix = s_prefix, mask = s_mask;
+    for (int i = c0; i < c1; i++) {
+      const float v = x[i];
+      if (!(v > -INFINITY)) continue;
+      const uint32_t k = key_of(v);
+      if ((k & mask) == prefix) atomicAdd(&hist[wv][(k >> shift) & 255u], 1);
+    }
+    __syncthreads();
+    if (tid < 256) {
+      int c = 0;
+      for (int w = 0; w < NW; w++) c += hist[w][tid];
+      total[tid] = c;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int need = s_need, above = 0, b = 255;
+      for (; b >= 0; b--) {
+        if (above + total[b] >= need) break;
+        above += total[b];
+      }
+      if (b < 0) {
+        s_all = 1;  // fewer than `need` keys match: every valid logit is a candidate
+      } else {
+        s_need = need - above;
+        s_prefix = prefix | ((uint32_t)b << shift);
+        s_mask = mask | (255u << shift);
+      }
+    }
+    __syncthreads();
+    if (s_all) break;
+  }
+  const bool all = s_all != 0;
+  const uint32_t K = s_prefix;
+  const int need = s_need;  // logits equal to K to take, the lowest ids first
+  int eq = 0;
+  for (int i = c0; i < c1; i++) {
+    const float v = x[i];
+    if (!(v > -INFINITY)) continue;
+    const uint32_t k = key_of(v);
+    if (all || k > K) {
+      const int slot = atomicAdd(&s_slot, 1);
+      cv[slot] = v;
+      ci[slot] = (uint32_t)i;
+    } else if (k == K) {
+      eq++;
+    }
+  }
+  scan[tid] = eq;
+  __syncthreads();
+  if (tid == 0) {  // exclusive prefix over the threads, in id order
+    int run = 0;
+    for (int t = 0; t < kSampNT; t++) {
+      const int c = scan[t];
+      scan[t] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  if (!all && eq) {
+    int rank = scan[tid];
+    const int base = kTopK - need;
+    for (int i = c0; i < c1 && rank < need; i++) {
+      const float v = x[i];
+      if (!(v > -INFINITY) || key_of(v) != K) continue;
+      cv[base + rank] = v;
+      ci[base + rank] = (uint32_t)i;
+      rank++;
+    }
+  }
+  __syncthreads();
+  const int nv = all ? s_slot : kTopK;  // valid candidates
+  if (tid < kTopK) {
+    if (tid < nv) {
+      const float v = cv[tid];
+      const uint32_t id = ci[tid];
+      int r = 0;
+      for (int j = 0; j < nv; j++) r += (cv[j] > v || (cv[j] == v && ci[j] < id)) ? 1 : 0;
+      sv[r] = v;
+      si[r] = id;
+    } else {
+      sv[tid] = -INFINITY;
+      si[tid] = 0;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float* p = pr;
+    const float mx = sv[0];
+    float sum = 0.0f;
+    for (int k = 0; k < kTopK; k++) {
+      p[k] = dev_expf((sv[k] - mx) / temperature);
+      sum = sum + p[k];
+    }
+    const float cut = top_p * sum;
+    float cum = 0.0f;
+    int nn = kTopK;
+    for (int k = 0; k < kTopK; k++) {
+      cum = cum + p[k];
+      if (cum >= cut) {
+        nn = k + 1;
+        break;
+      }
+    }
+    unsigned long long st = *rng;
+    const float r = sampler_next_f32(&st) * cum;
+    *rng = st;
+    uint32_t pick = si[nn - 1];
+    float acc = 0.0f;
+    for (int k = 0; k < nn; k++) {
+      acc = acc + p[k];
+      if (r <= acc) {
+        pick = si[k];
+        break;
+      }
+    }
+    if (ctl) {
+      ctl[CTL_TOKEN] = (int)pick;
+      const int step = ctl[CTL_STEP];
+      if (out_tokens && step < max_out) out_tokens[step] = pick;
+      ctl[CTL_STEP] = step + 1;
+      ctl[CTL_POS] = ctl[CTL_POS] + 1;
+    } else {
+      *token = pick;
+    }
   }
 }
 
@@ -710,6 +898,9 @@ struct nrq_model {
   float *battn = nullptr, *bgate = nullptr, *bup = nullptr, *brope = nullptr;
   uint8_t *bxq = nullptr, *bxq2 = nullptr;
   int* btok = nullptr;
+  // Sampler (sample.rs:5-21): temperature <= 0 is greedy
+  float samp_t = 0.0f, samp_p = 1.0f;
+  unsigned long long* rng = nullptr;  // device word, seed | 1
 };
 
 namespace nrq {
@@ -868,6 +1059,12 @@ int enqueue_step(nrq_model* m) {
   }
   if ((rc = norm_quant(m, xr, pending, m->out_norm, m->output.dt))) return rc;
   if ((rc = matvec(m, m->output, m->xq, m->logits, c.vocab, d))) return rc;
+  if (m->samp_t > 0.0f) {
+    hipLaunchKernelGGL(nrq::sample_kernel, dim3(1), dim3(nrq::kSampNT), 0, m->stream, m->logits, c.vocab, m->samp_t,
+                       m->samp_p, m->rng, m->ctl, m->out_tokens, m->max_out, nullptr);
+    if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: sampler launch failed");
+    return NRQ_OK;
+  }
   hipLaunchKernelGGL(nrq::argmax_kernel, dim3(1), dim3(nrq::kArgNT), 0, m->stream, m->logits, c.vocab, m->ctl,
                      m->out_tokens, m->max_out);
   if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: argmax launch failed");
@@ -1062,6 +1259,7 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
       {(void**)&m->xq, act_bytes(NRQ_Q8_0, m->maxd) + act_bytes(NRQ_Q4_K, m->maxd) + 64},
       {(void**)&m->xq2, act_bytes(NRQ_Q8_0, m->maxd) + act_bytes(NRQ_Q4_K, m->maxd) + 64},
       {(void**)&m->ctl, nrq::CTL_WORDS * 4},
+      {(void**)&m->rng, 8},
   };
   for (auto& a : allocs) {
     if ((e = hipMalloc(a.p, a.bytes)) != hipSuccess) return bail(e, "hipMalloc");
@@ -1127,6 +1325,46 @@ int nrq_model_set_rope_freqs(nrq_model* m, const float* freqs, int n) {
   MHIP(hipStreamSynchronize(m->stream));
   MHIP(hipMemcpy(m->freqs, freqs, (size_t)n * 4, hipMemcpyHostToDevice));
   return NRQ_OK;
+}
+
+int nrq_model_set_sampler(nrq_model* m, float temperature, float top_p, uint64_t seed) {
+  if (!m) return mfail(NRQ_ERR_ARG, "nrq_model_set_sampler: null handle");
+  MHIP(hipStreamSynchronize(m->stream));
+  const unsigned long long st = (unsigned long long)(seed | 1u);  // sample.rs:19
+  MHIP(hipMemcpy(m->rng, &st, 8, hipMemcpyHostToDevice));
+  const bool was = m->samp_t > 0.0f, now = temperature > 0.0f;
+  m->samp_t = temperature;
+  m->samp_p = top_p;
+  if (m->exec && (was || now)) {  // the captured step's last kernel (or its arguments) changes
+    hipGraphExecDestroy(m->exec);
+    hipGraphDestroy(m->graph);
+    m->exec = nullptr;
+    m->graph = nullptr;
+  }
+  return NRQ_OK;
+}
+
+int nrq_model_sampler_state(nrq_model* m, uint64_t* state) {
+  if (!m || !state) return mfail(NRQ_ERR_ARG, "nrq_model_sampler_state: null argument");
+  MHIP(hipStreamSynchronize(m->stream));
+  unsigned long long st = 0;
+  MHIP(hipMemcpy(&st, m->rng, 8, hipMemcpyDeviceToHost));
+  *state = st;
+  return NRQ_OK;
+}
+
+int nrq_dev_sample(const float* logits, int n, float temperature, float top_p, uint64_t* rng, uint32_t* token,
+                   void* stream) {
+  if (!logits || !token || (temperature > 0.0f && !rng)) return mfail(NRQ_ERR_ARG, "nrq_dev_sample: null pointer");
+  if (n <= 0) return mfail(NRQ_ERR_ARG, "nrq_dev_sample: empty logits");
+  if (temperature > 0.0f) {
+    hipLaunchKernelGGL(nrq::sample_kernel, dim3(1), dim3(nrq::kSampNT), 0, (hipStream_t)stream, logits, n,
+                       temperature, top_p, (unsigned long long*)rng, nullptr, nullptr, 0, token);
+  } else {
+    hipLaunchKernelGGL(nrq::argmax_kernel, dim3(1), dim3(nrq::kArgNT), 0, (hipStream_t)stream, logits, n, nullptr,
+                       token, 1);
+  }
+  return hipGetLastError() == hipSuccess ? NRQ_OK : mfail(NRQ_ERR_DEVICE, "nrq_dev_sample: launch failed");
 }
 
 int nrq_model_reset(nrq_model* m) {
@@ -1280,7 +1518,7 @@ int nrq_model_destroy(nrq_model* m) {
   if (m->graph) hipGraphDestroy(m->graph);
   void* bufs[] = {m->freqs, m->rope_cs, m->kc, m->vc, m->x, m->x2, m->xb, m->q, m->k, m->v, m->attn, m->gate, m->up, m->xb2,
                   m->logits, m->xq, m->xq2, m->ctl, m->out_tokens, m->owned, m->bx, m->bxb, m->bxn, m->bq,
-                  m->bk, m->bv, m->battn, m->bgate, m->bup, m->brope, m->bxq, m->bxq2, m->btok};
+                  m->bk, m->bv, m->battn, m->bgate, m->bup, m->brope, m->bxq, m->bxq2, m->btok, m->rng};
   for (void* p : bufs)
     if (p) hipFree(p);
   if (m->stream) hipStreamDestroy(m->stream);

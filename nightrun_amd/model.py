@@ -107,6 +107,15 @@ class Model:
         _lib.check(_lib.lib().nrq_model_prefill(self.h, t.ctypes.data, t.size, out.ctypes.data if logits else None))
         return out
 
+    def set_sampler(self, temperature: float, top_p: float, seed: int) -> None:
+        """Sampler::new (sample.rs:15-21) for generate(): temperature <= 0 is greedy."""
+        _lib.check(_lib.lib().nrq_model_set_sampler(self.h, temperature, top_p, seed & 0xFFFFFFFFFFFFFFFF))
+
+    def sampler_state(self) -> int:
+        st = C.c_uint64()
+        _lib.check(_lib.lib().nrq_model_sampler_state(self.h, C.byref(st)))
+        return st.value
+
     def generate(self, token: int, n: int, logits: bool = False):
         toks = np.empty(n, np.uint32)
         last = np.empty(self.cfg["vocab"], np.float32) if logits else None
@@ -120,6 +129,19 @@ class Model:
         v = np.empty(n, np.uint16)
         _lib.check(_lib.lib().nrq_model_kv_cache(self.h, k.ctypes.data, v.ctypes.data, n * 2))
         return k, v
+
+
+def sample(logits, temperature: float, top_p: float, rng):
+    """Sampler::sample (sample.rs:32-96) on the device over a torch f32 tensor;
+    rng: a one-element torch int64 tensor on the device holding the state
+    (advanced in place). Returns the drawn id."""
+    import torch
+
+    _lib.init(torch.cuda.current_device())
+    tok = torch.zeros(1, dtype=torch.int32, device=logits.device)
+    _lib.check(_lib.lib().nrq_dev_sample(logits.data_ptr(), logits.numel(), temperature, top_p, rng.data_ptr(),
+                                         tok.data_ptr(), torch.cuda.current_stream().cuda_stream))
+    return int(tok.cpu().item())
 
 
 def mathf(fn: int, x):

@@ -287,6 +287,9 @@ def _model_lib():
         L.nro_model_kcache.argtypes, L.nro_model_kcache.restype = [vp], C.POINTER(C.c_uint16)
         L.nro_model_vcache.argtypes, L.nro_model_vcache.restype = [vp], C.POINTER(C.c_uint16)
         L.nro_model_set_freqs.argtypes = [vp, vp]
+        L.nro_sampler_next_f32.argtypes, L.nro_sampler_next_f32.restype = [C.POINTER(C.c_uint64)], C.c_float
+        L.nro_sample.argtypes = [C.c_float, C.c_float, C.POINTER(C.c_uint64), vp, sz]
+        L.nro_sample.restype = C.c_uint32
         for name in ("nro_crc32", "nro_crc32_bitwise"):
             getattr(L, name).argtypes, getattr(L, name).restype = [C.c_uint32, vp, sz], C.c_uint32
         L.nro_infer_freqs.argtypes = [vp, sz, C.c_float, C.c_float, C.c_float, C.c_float, C.c_float, vp]
@@ -358,6 +361,21 @@ def infer_freqs(head_dim: int, theta: float, factor: float = 0.0, low: float = 0
     _model_lib().nro_infer_freqs(_p(out), head_dim, theta, factor, low, high, orig_ctx,
                                  None if f is None else _p(f))
     return out
+
+
+class Sampler:
+    """sample.rs:5-96 restated: Sampler::new(temperature, top_p, seed) keeps seed | 1."""
+
+    def __init__(self, temperature: float, top_p: float, seed: int):
+        self.temperature, self.top_p = temperature, top_p
+        self.rng = C.c_uint64((seed | 1) & 0xFFFFFFFFFFFFFFFF)
+
+    def next_f32(self) -> float:
+        return _model_lib().nro_sampler_next_f32(C.byref(self.rng))
+
+    def sample(self, logits: np.ndarray) -> int:
+        x = np.ascontiguousarray(logits, np.float32)
+        return _model_lib().nro_sample(self.temperature, self.top_p, C.byref(self.rng), _p(x), x.size)
 
 
 def crc32(data, crc: int = 0) -> int:

@@ -514,3 +514,84 @@ void nro_expf_n(const float *x, float *y, size_t n) {
 void nro_sincosf_n(const float *x, float *s, float *c, size_t n) {
     for (size_t i = 0; i < n; i++) nro_sincosf(x[i], s + i, c + i);
 }
+
+/* ---- Sampler (crates/nr-model/src/sample.rs) ---------------------------------------- */
+
+#define NRO_TOP_K 64 /* sample.rs:12 */
+
+/* sample.rs:23-30: xorshift64 (13, 7, 17), then the top 24 bits as a fraction */
+float nro_sampler_next_f32(uint64_t *rng) {
+    uint64_t x = *rng;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *rng = x;
+    return (float)(x >> 40) / (float)(1u << 24);
+}
+
+/* sample.rs:32-96. Greedy below temperature 0+; else a 64-slot min-heap keyed
+ * on the logit (strict > admits, NaN and -inf never do), the candidates in
+ * descending logit order, expf((v - max) / T) summed in that order, the
+ * shortest prefix whose running sum reaches top_p * sum, and a draw of
+ * next_f32() * that prefix sum. Exact ties among the candidates are ordered
+ * by token id here (the reference's unstable sort leaves their order open). */
+uint32_t nro_sample(float temperature, float top_p, uint64_t *rng, const float *logits, size_t n) {
+    if (temperature <= 0.0f) return nro_argmax(logits, n);
+    float hv[NRO_TOP_K];
+    uint32_t hi[NRO_TOP_K];
+    for (int k = 0; k < NRO_TOP_K; k++) {
+        hv[k] = -INFINITY;
+        hi[k] = 0;
+    }
+    for (size_t i = 0; i < n; i++) {
+        float v = logits[i];
+        if (!(v > hv[0])) continue;
+        hv[0] = v;
+        hi[0] = (uint32_t)i;
+        int j = 0; /* sift down */
+        for (;;) {
+            int l = 2 * j + 1, r = 2 * j + 2, m = j;
+            if (l < NRO_TOP_K && hv[l] < hv[m]) m = l;
+            if (r < NRO_TOP_K && hv[r] < hv[m]) m = r;
+            if (m == j) break;
+            float tv = hv[j]; hv[j] = hv[m]; hv[m] = tv;
+            uint32_t ti = hi[j]; hi[j] = hi[m]; hi[m] = ti;
+            j = m;
+        }
+    }
+    /* descending by logit (insertion sort; ties by token id) */
+    float cv[NRO_TOP_K];
+    uint32_t ci[NRO_TOP_K];
+    for (int k = 0; k < NRO_TOP_K; k++) {
+        float v = hv[k];
+        uint32_t id = hi[k];
+        int p = k;
+        while (p > 0 && (cv[p - 1] < v || (cv[p - 1] == v && ci[p - 1] > id))) {
+            cv[p] = cv[p - 1];
+            ci[p] = ci[p - 1];
+            p--;
+        }
+        cv[p] = v;
+        ci[p] = id;
+    }
+    float mx = cv[0], sum = 0.0f, probs[NRO_TOP_K];
+    for (int k = 0; k < NRO_TOP_K; k++) {
+        probs[k] = nro_expf((cv[k] - mx) / temperature);
+        sum += probs[k];
+    }
+    float cut = top_p * sum, cum = 0.0f;
+    int nn = NRO_TOP_K;
+    for (int k = 0; k < NRO_TOP_K; k++) {
+        cum += probs[k];
+        if (cum >= cut) {
+            nn = k + 1;
+            break;
+        }
+    }
+    float r = nro_sampler_next_f32(rng) * cum, acc = 0.0f;
+    for (int k = 0; k < nn; k++) {
+        acc += probs[k];
+        if (r <= acc) return ci[k];
+    }
+    return ci[nn - 1];
+}

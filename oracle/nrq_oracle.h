@@ -153,6 +153,12 @@ const float *nro_model_logits(const nro_model *m);
 const uint16_t *nro_model_kcache(const nro_model *m);
 const uint16_t *nro_model_vcache(const nro_model *m);
 
+/* Sampler (crates/nr-model/src/sample.rs:23-96); rng is the sampler's state
+ * (Sampler::new sets seed | 1). Exact logit ties among the top 64 are ordered
+ * by token id. */
+float nro_sampler_next_f32(uint64_t *rng);
+uint32_t nro_sample(float temperature, float top_p, uint64_t *rng, const float *logits, size_t n);
+
 /* .nrm checksum (crates/nr-model/src/crc32.rs:6-79), zlib running-value
  * convention; the bitwise form is the classic algorithm of
  * crates/nr-model/tests/verify.rs:16-30. */
