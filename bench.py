@@ -455,6 +455,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--also", default="cfg1,cfg3", help="other matvec configs reported beside (comma list)")
+    ap.add_argument("--prefill-only", type=int, default=0, metavar="TOKENS",
+                    help="only time nrq_model_prefill of TOKENS tokens on the Llama-3.2-1B-shape model")
     ap.add_argument("--crc-only", type=int, default=0, metavar="BYTES",
                     help="only time nrq_dev_crc32 over BYTES random device bytes (profiling the CRC kernels)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -462,6 +464,27 @@ def main():
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration << 20)
+        return
+    if args.prefill_only:
+        import torch
+
+        import nightrun_amd
+        from nightrun_amd.model import Model
+
+        nightrun_amd.init(0)
+        cfg = LLAMA_1B
+        m = Model(cfg, ctx=args.prefill_only + 8)
+        m.set_weights(synth_model(cfg, 0x5EED0005))
+        prompt = np.random.default_rng(5).integers(0, cfg["vocab"], args.prefill_only).astype(np.uint32)
+        m.prefill(prompt[:64], logits=False)
+        m.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        m.prefill(prompt)
+        dt = time.perf_counter() - t0
+        m.close()
+        print(json.dumps({"prefill_only": {"tokens": args.prefill_only, "seconds": round(dt, 4),
+                                           "tok_s": round(args.prefill_only / dt, 1)}}))
         return
     if args.crc_only:
         import torch
