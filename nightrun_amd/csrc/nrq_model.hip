@@ -20,6 +20,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <utility>
@@ -552,6 +553,182 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   }
 }
 
+// Prefill attention for all GH query heads of one KV head: workgroup (g, i)
+// serves token i of a chunk (position base + i) for heads g*GH .. g*GH+GH-1.
+// Each key row is loaded once for the GH scores and each value piece once for
+// the GH heads' products, so a launch reads the cached keys and values GH
+// times less than one workgroup per head would. Per head, everything else is
+// attention_kernel's, in the same order: dot_f16 in dimension order times the
+// scale, the max, expf, the exp-sum in position order (one wave per head),
+// a = e * inv, and out[d] += a_t * v_t[d] in position order (one chain lane
+// per head and dimension, fed by producer waves in chunks of C positions).
+// LDS: att[GH][ctx128] | prod[2][GH * HD * CP] | q[GH * HD] | red[64]
+constexpr int kGrpProd = 9216;  // floats per product stage
+
+template <int HD, int GH>
+struct AttGroup {
+  static constexpr int C = (kGrpProd / (GH * HD) - 4) & ~3;  // positions per chunk
+  static constexpr int CP = C + 4;
+  static constexpr int stage = GH * HD * CP;
+  static constexpr int cw = GH * HD / 64;  // chain waves
+  static constexpr int nprod = kAttNT - 64 * cw;
+  static constexpr int npc = C * (HD / 8);  // 16-byte value pieces per chunk
+  static size_t lds_bytes(int ctx) {
+    return ((size_t)GH * ((ctx + 127) & ~127) + 2 * (size_t)stage + (size_t)GH * HD + 64) * 4;
+  }
+};
+
+template <int HD, int GH>
+__global__ __launch_bounds__(kAttNT) void attention_group_kernel(
+    const float* __restrict__ q_in, const int* __restrict__ ctl, int n_heads, int n_kv_heads, int ctx, int layer,
+    float scale, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, float* __restrict__ out,
+    uint8_t* __restrict__ out_q8) {
+  using A = AttGroup<HD, GH>;
+  constexpr int hd = HD, g8 = HD / 8, C = A::C, CP = A::CP, cw = A::cw, nprod = A::nprod, npc = A::npc;
+  static_assert(C >= 4, "product chunk too small");
+  static_assert(npc <= nprod, "one value piece per producer thread");
+  static_assert(GH <= kAttNT / 64, "one wave per head for the exp-sum");
+  extern __shared__ __align__(16) float sm[];
+  const int g = blockIdx.x, tok = blockIdx.y, tid = threadIdx.x;
+  const int pos = ctl[CTL_POS] + tok, n = pos + 1;
+  const int n128 = (n + 127) & ~127;
+  const int ctx128 = (ctx + 127) & ~127;
+  float* att = sm;  // [GH][ctx128]
+  float* prod = sm + (size_t)GH * ctx128;
+  float* qs = prod + 2 * A::stage;  // [GH][hd]
+  float* red = qs + GH * hd;         // [64]
+  q_in += (size_t)tok * n_heads * hd + (size_t)g * GH * hd;
+  out += (size_t)tok * n_heads * hd + (size_t)g * GH * hd;
+  if (out_q8) out_q8 += ((size_t)tok * n_heads * hd + (size_t)g * GH * hd) / 32 * kQ8_0Bytes;
+  const size_t base = ((size_t)layer * n_kv_heads + g) * hd * ctx;
+  const size_t ctx8 = (size_t)ctx * 8;
+  for (int i = tid; i < GH * hd; i += kAttNT) qs[i] = q_in[i];
+  __syncthreads();
+  // scores: thread tid takes positions tid, tid + kAttNT, ...
+  float mx[GH];
+#pragma unroll
+  for (int j = 0; j < GH; j++) mx[j] = -INFINITY;
+  for (int t = tid; t < n; t += kAttNT) {
+    uint4 kr[g8];
+    const uint4* src = (const uint4*)(kc + base + (size_t)t * 8);
+#pragma unroll
+    for (int p8 = 0; p8 < g8; p8++) kr[p8] = src[(size_t)p8 * ctx];
+#pragma unroll 1
+    for (int j = 0; j < GH; j++) {  // one head at a time beside the packed key
+      const float* q = qs + j * hd;
+      float sc = 0.0f;
+#pragma unroll
+      for (int p8 = 0; p8 < g8; p8++) {
+        const uint32_t kw[4] = {kr[p8].x, kr[p8].y, kr[p8].z, kr[p8].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          sc = sc + f16_bits_to_f32(kw[e] & 0xffffu) * q[8 * p8 + 2 * e];
+          sc = sc + f16_bits_to_f32(kw[e] >> 16) * q[8 * p8 + 2 * e + 1];
+        }
+      }
+      const float a = sc * scale;
+      att[(size_t)j * ctx128 + t] = a;
+    }
+  }
+  // each thread's maximum per head over the scores it wrote
+  for (int t = tid; t < n; t += kAttNT) {
+#pragma unroll
+    for (int j = 0; j < GH; j++) mx[j] = fmaxf(mx[j], att[(size_t)j * ctx128 + t]);
+  }
+#pragma unroll
+  for (int j = 0; j < GH; j++) {
+    const float m = wave_max(mx[j]);
+    if ((tid & 63) == 0) red[j * 16 + (tid >> 6)] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < GH; j++) {
+    float m = red[j * 16];
+    for (int w = 1; w < kAttNT / 64; w++) m = fmaxf(m, red[j * 16 + w]);
+    mx[j] = m;
+  }
+  __syncthreads();  // red is reused below
+  for (int t = tid; t < n128; t += kAttNT) {
+#pragma unroll
+    for (int j = 0; j < GH; j++)
+      att[(size_t)j * ctx128 + t] = t < n ? dev_expf(att[(size_t)j * ctx128 + t] - mx[j]) : 0.0f;
+  }
+  __syncthreads();
+  {
+    const int w = tid >> 6;  // wave w < GH sums head w's exps in position order
+    if (w < GH) {
+      const float tot = wave_chain_from(att + (size_t)w * ctx128, n128, 0.0f);
+      if ((tid & 63) == 0) red[w] = 1.0f / tot;
+    }
+  }
+  __syncthreads();
+  for (int t = tid; t < n; t += kAttNT) {
+#pragma unroll
+    for (int j = 0; j < GH; j++) att[(size_t)j * ctx128 + t] = att[(size_t)j * ctx128 + t] * red[j];
+  }
+  // chunked axpy: producers form a_j(t) * v_t[d] for every head, chain lanes add
+  const int ptid = tid - 64 * cw;
+  const bool producer = ptid >= 0;
+  const int nchunks = (n + C - 1) / C;
+  auto vload = [&](int c, uint4& r) {
+    const int tl = ptid % C, i0 = 8 * (ptid / C);
+    const int t = c * C + tl;
+    if (ptid < npc && t < n) r = *(const uint4*)(vc + base + (size_t)(i0 >> 3) * ctx8 + (size_t)t * 8);
+  };
+  auto vprod = [&](int c, const uint4& r) {
+    const int tl = ptid % C, i0 = 8 * (ptid / C);
+    const int t = c * C + tl;
+    if (ptid >= npc || t >= n) return;
+    float* pb = prod + (c & 1) * A::stage;
+    float vv[8];
+    const uint32_t vw[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      vv[2 * q] = f16_bits_to_f32(vw[q] & 0xffffu);
+      vv[2 * q + 1] = f16_bits_to_f32(vw[q] >> 16);
+    }
+#pragma unroll
+    for (int j = 0; j < GH; j++) {
+      const float a = att[(size_t)j * ctx128 + t];
+#pragma unroll
+      for (int q = 0; q < 8; q++) pb[(j * hd + i0 + q) * CP + tl] = a * vv[q];
+    }
+  };
+  uint4 s0 = make_uint4(0, 0, 0, 0), s1 = s0, s2 = s0;  // value pieces of chunks k with k % 3 == 0, 1, 2
+  if (producer) {
+    vload(0, s0);
+    vload(1, s1);
+    vload(2, s2);
+  }
+  __syncthreads();  // att[] normalized
+  if (producer) {
+    vprod(0, s0);
+    vload(3, s0);
+  }
+  __syncthreads();
+  float o = 0.0f;
+  auto step = [&](int cc, uint4& slot) {
+    if (producer) {
+      if (cc + 1 < nchunks) {
+        vprod(cc + 1, slot);
+        vload(cc + 4, slot);
+      }
+    } else {
+      o = chain_from(prod + (cc & 1) * A::stage + tid * CP, min(C, n - cc * C), o);
+    }
+    __syncthreads();
+  };
+  for (int c = 0; c < nchunks; c += 3) {
+    step(c, s1);
+    if (c + 1 < nchunks) step(c + 1, s2);
+    if (c + 2 < nchunks) step(c + 2, s0);
+  }
+  if (tid < GH * hd) {
+    out[tid] = o;
+    if (out_q8) quant_q8_0_lane(o, tid & 31, out_q8 + (size_t)(tid >> 5) * kQ8_0Bytes);
+  }
+}
+
 // vec.rs:45-52: gate = gate / (1 + expf(-gate)) * up; with xq != null also its
 // Q8_0 blocks (n is a multiple of 256).
 __global__ __launch_bounds__(256) void swiglu_kernel(float* __restrict__ gate, const float* __restrict__ up, int n,
@@ -1073,6 +1250,35 @@ int enqueue_step(nrq_model* m) {
 
 constexpr int kMaxBatch = 64;  // MAX_BATCH (infer.rs:101)
 
+using AttGroupFn = void (*)(const float*, const int*, int, int, int, int, float, const uint16_t*, const uint16_t*,
+                            float*, uint8_t*);
+
+template <int HD>
+AttGroupFn att_group_for(int gh, size_t* lds, int ctx) {
+  switch (gh) {
+    case 2: *lds = nrq::AttGroup<HD, 2>::lds_bytes(ctx); return nrq::attention_group_kernel<HD, 2>;
+    case 3: *lds = nrq::AttGroup<HD, 3>::lds_bytes(ctx); return nrq::attention_group_kernel<HD, 3>;
+    case 4: *lds = nrq::AttGroup<HD, 4>::lds_bytes(ctx); return nrq::attention_group_kernel<HD, 4>;
+    default: *lds = 0; return nullptr;
+  }
+}
+
+// The grouped prefill attention for this model's shape, or null (then one
+// workgroup per query head); NRQ_ATT_GROUP=0 forces the latter.
+AttGroupFn att_group(const nrq_model_config& c, size_t* lds) {
+  *lds = 0;
+  const char* env = getenv("NRQ_ATT_GROUP");
+  if (env && env[0] == '0') return nullptr;
+  const int gh = c.n_heads / c.n_kv_heads;
+  // head_dim 64 only: at 128 the key row and the chains exceed 128 registers
+  AttGroupFn f = c.head_dim == 64 ? att_group_for<64>(gh, lds, c.ctx) : nullptr;
+  if (!f || *lds > 160 * 1024) {
+    *lds = 0;
+    return nullptr;
+  }
+  return f;
+}
+
 int prefill_alloc(nrq_model* m) {
   if (m->bx) return NRQ_OK;
   const auto& c = m->cfg;
@@ -1159,13 +1365,20 @@ int enqueue_prefill(nrq_model* m, int B) {
     if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: rope launch failed");
     {
       const bool q8 = Ly.m[3].dt == NRQ_Q8_0;
-      auto* kern = c.head_dim == 32   ? nrq::attention_kernel<32, true>
-                   : c.head_dim == 64 ? nrq::attention_kernel<64, true>
-                   : c.head_dim == 96 ? nrq::attention_kernel<96, true>
-                                      : nrq::attention_kernel<128, true>;
-      hipLaunchKernelGGL(kern, dim3(c.n_heads, B), dim3(nrq::kAttNT), m->att_lds, m->stream, m->bq, m->bk, m->bv,
-                         m->brope, m->ctl, c.n_heads, c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->battn,
-                         q8 ? m->bxq : nullptr);
+      size_t glds = 0;
+      const AttGroupFn gk = att_group(c, &glds);
+      if (gk) {
+        hipLaunchKernelGGL(gk, dim3(c.n_kv_heads, B), dim3(nrq::kAttNT), glds, m->stream, m->bq, m->ctl, c.n_heads,
+                           c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->battn, q8 ? m->bxq : nullptr);
+      } else {
+        auto* kern = c.head_dim == 32   ? nrq::attention_kernel<32, true>
+                     : c.head_dim == 64 ? nrq::attention_kernel<64, true>
+                     : c.head_dim == 96 ? nrq::attention_kernel<96, true>
+                                        : nrq::attention_kernel<128, true>;
+        hipLaunchKernelGGL(kern, dim3(c.n_heads, B), dim3(nrq::kAttNT), m->att_lds, m->stream, m->bq, m->bk, m->bv,
+                           m->brope, m->ctl, c.n_heads, c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->battn,
+                           q8 ? m->bxq : nullptr);
+      }
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: attention launch failed");
       const Mat* ws[1] = {&Ly.m[3]};
       float* ys[1] = {m->bxb};

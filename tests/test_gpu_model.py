@@ -184,6 +184,22 @@ def test_tiny_model_prefill(gpu, oracle, n):
     run_pair(oracle, TINY, w, 160, prompt, 6, prefill=True)
 
 
+TINY_GQA4 = dict(dim=512, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=1000, norm_eps=1e-5,
+                 rope_theta=500000.0)
+
+
+@pytest.mark.parametrize("group", ["1", "0"])
+def test_prefill_attention_paths(gpu, oracle, monkeypatch, group):
+    """Prefill attention with one workgroup per KV group (all its query heads,
+    the default for head_dim 64) and with one workgroup per query head
+    (NRQ_ATT_GROUP=0): GQA 4:1 and 2:1, prompts across a chunk boundary."""
+    monkeypatch.setenv("NRQ_ATT_GROUP", group)
+    for cfg, seed in ((TINY_GQA4, 41), (TINY, 42)):
+        w = oracle.gen_model(cfg, seed)
+        prompt = np.random.default_rng(seed).integers(0, cfg["vocab"], 100).astype(np.uint32)
+        run_pair(oracle, cfg, w, 128, prompt, 4, prefill=True)
+
+
 def test_tiny_model_prefill_kquant(gpu, oracle):
     """Q4_K q/k/v/o/gate/up and Q6_K down (Q8_K activations through the 32x32
     MFMA kernels), an untied Q6_K head."""
