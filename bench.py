@@ -165,7 +165,8 @@ def measure_matvec(name, steps, warmup, order):
 
 
 def measure_prefill(reps=3):
-    """One Qwen3-4B layer's seven matmuls at M = 64 (Q8_K activations), as one
+    """One Qwen3-4B layer's seven matmuls at M = 64 (Q8_K activations) in its
+    four groups (q|k|v and gate|up share an activation and one launch), as one
     graph of `reps` layers over rotating weight copies."""
     import torch
 
@@ -180,18 +181,26 @@ def measure_prefill(reps=3):
         for j, (name, dt, rows, cols) in enumerate(QWEN3_4B_LAYER):
             w = torch.from_numpy(synth_weights(dt, rows, cols, 0x5EED0004 + j)).cuda()
             ws = [w] + [w.clone() for _ in range(copies - 1)]
-            xf = torch.from_numpy(np.random.default_rng(40 + j).normal(0, 1, 64 * cols).astype(np.float32)).cuda()
-            xq = torch.empty(64 * cols // 256 * 292, dtype=torch.uint8, device="cuda")
-            device.quantize_q8k(xf, xq, stream=stream)
+            if j in (1, 2, 5):  # k, v, up take the activation of q and gate
+                xq = mats[-1][4]
+            else:
+                xf = torch.from_numpy(np.random.default_rng(40 + j).normal(0, 1, 64 * cols).astype(np.float32)).cuda()
+                xq = torch.empty(64 * cols // 256 * 292, dtype=torch.uint8, device="cuda")
+                device.quantize_q8k(xf, xq, stream=stream)
             y = torch.empty(64 * rows, dtype=torch.float32, device="cuda")
             mats.append((dt, rows, cols, ws, xq, y))
-            tot_bytes += algorithmic_bytes(dt, rows, cols, 64)
+            tot_bytes += algorithmic_bytes(dt, rows, cols, 64) - (64 * (cols // 256) * 292 if j in (1, 2, 5) else 0)
             tot_ops += 2.0 * 64 * rows * cols
     stream.synchronize()
 
+    # the layer's matmul groups (q|k|v, gate|up share their input, as Acts::matmul_group runs them)
+    groups = [[0, 1, 2], [3], [4, 5], [6]]
+
     def layer(i):
-        for dt, rows, cols, ws, xq, y in mats:
-            device.matmul(dt, 0, y, ws[i % copies], xq, rows, cols, 64, stream=stream)
+        for g in groups:
+            dt, cols, xq = mats[g[0]][0], mats[g[0]][2], mats[g[0]][4]
+            device.matmul_group(dt, [mats[j][5] for j in g], [mats[j][3][i % copies] for j in g],
+                                [mats[j][1] for j in g], xq, cols, 64, stream=stream)
 
     layer(0)
     stream.synchronize()

@@ -121,6 +121,13 @@ int nrq_dev_matvec(int dtype, int order, float *y, const void *w, const void *x,
                    void *stream);
 int nrq_dev_matmul(int dtype, int order, float *y, const void *w, const void *xs, size_t rows, size_t cols,
                    size_t batch, void *stream);
+/* Acts::matmul_group (crates/nr-model/src/infer.rs:180-228) on the device: n
+ * (1-3) matrices of one dtype and width over the same activation blocks,
+ * ys[i] = [batch][rows[i]], each bitwise equal to nrq_dev_matmul of that
+ * matrix in the scalar order. One launch covers the group where the prefill
+ * kernel takes it (else one launch per matrix). */
+int nrq_dev_matmul_group(int dtype, int n, float *const *ys, const void *const *ws, const size_t *rows,
+                         const void *xs, size_t cols, size_t batch, void *stream);
 /* q8::quantize / kquant::quantize_q8k over n f32 values already in HBM */
 int nrq_dev_quantize_q8_0(const float *src, size_t n, void *out, void *stream);
 int nrq_dev_quantize_q8k(const float *src, size_t n, void *out, void *stream);

@@ -50,6 +50,7 @@ SIGNATURES = {
     "nrq_quantize_q8k": ([_vp, _sz, _vp, _sz], _i),
     "nrq_dev_matvec": ([_i, _i, _vp, _vp, _vp, _sz, _sz, _vp], _i),
     "nrq_dev_matmul": ([_i, _i, _vp, _vp, _vp, _sz, _sz, _sz, _vp], _i),
+    "nrq_dev_matmul_group": ([_i, _i, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_sz), _vp, _sz, _sz, _vp], _i),
     "nrq_dev_quantize_q8_0": ([_vp, _sz, _vp, _vp], _i),
     "nrq_dev_quantize_q8k": ([_vp, _sz, _vp, _vp], _i),
     "nrq_dev_block_sums": ([_i, _vp, _vp, _vp, _sz, _sz, _vp], _i),

@@ -379,6 +379,43 @@ int nrq_dev_matmul(int dtype, int order, float* y, const void* w, const void* xs
   return launch_rc(nrq::launch_matmul(dtype, order, L), "nrq_dev_matmul");
 }
 
+int nrq_dev_matmul_group(int dtype, int n, float* const* ys, const void* const* ws, const size_t* rows,
+                         const void* xs, size_t cols, size_t batch, void* stream) {
+  int rc = dev_check("nrq_dev_matmul_group", dtype, nrq::kOrderScalar);
+  if (rc) return rc;
+  if (n < 1 || n > 3 || !ys || !ws || !rows) return fail(NRQ_ERR_ARG, "nrq_dev_matmul_group: 1 to 3 matrices");
+  const size_t bpr = cols / qk_of(dtype);
+  if (batch == 0) return NRQ_OK;
+  bool whole = bpr > 0 && (size_t)cols % qk_of(dtype) == 0;
+  for (int i = 0; i < n; i++) {
+    if (!ys[i] || (bpr && !ws[i])) return fail(NRQ_ERR_ARG, "nrq_dev_matmul_group: null pointer");
+    if (((uintptr_t)ws[i] & 15) != 0) return fail(NRQ_ERR_ARG, "nrq_dev_matmul_group: weights not 16-byte aligned");
+    if (rows[i] == 0 || rows[i] > 0x7fffffff) whole = false;
+  }
+  if (bpr && !xs) return fail(NRQ_ERR_ARG, "nrq_dev_matmul_group: null pointer");
+  if (((uintptr_t)xs & (dtype == NRQ_Q8_0 ? 1 : 3)) != 0)
+    return fail(NRQ_ERR_ARG, "nrq_dev_matmul_group: activation blocks not aligned like their Rust type");
+  if (bpr > 0x7fffffff || batch > 0x7fffffff) return fail(NRQ_ERR_UNSUPPORTED, "nrq_dev_matmul_group: dimension exceeds 2^31");
+  if (whole && n > 1) {
+    nrq::MatmulGroupLaunch G{};
+    for (int i = 0; i < n; i++) {
+      G.w[i] = ws[i];
+      G.y[i] = ys[i];
+      G.rows[i] = (int)rows[i];
+    }
+    G.nmat = n;
+    G.xs = xs;
+    G.bpr = (int)bpr;
+    G.batch = (int)batch;
+    G.stream = stream_or_default(stream);
+    const int lr = nrq::launch_mmt_group(dtype, G);
+    if (lr != nrq::NRQ_LAUNCH_BAD_ARG) return launch_rc(lr, "nrq_dev_matmul_group");
+  }
+  for (int i = 0; i < n; i++)  // the group as separate launches
+    if ((rc = nrq_dev_matmul(dtype, nrq::kOrderScalar, ys[i], ws[i], xs, rows[i], cols, batch, stream))) return rc;
+  return NRQ_OK;
+}
+
 int nrq_dev_quantize_q8_0(const float* src, size_t n, void* out, void* stream) {
   if (!S().init) return fail(NRQ_ERR_NOT_INIT, "nrq_dev_quantize_q8_0: nrq_init was not called");
   if (n % 32) return fail(NRQ_ERR_SHAPE, "nrq_dev_quantize_q8_0: n = %zu is not a multiple of 32", n);

@@ -78,10 +78,24 @@ int launch_norm_matvec_q8_0(const NormMatvecLaunch& L);
 int launch_matmul(int dtype, int order, const MatmulLaunch& L);
 // Scalar-order batched matmul on int8 MFMA (nrq_mmq.hip).
 int launch_mmq(int dtype, const MatmulLaunch& L);
-// Q4_K/Q6_K prefill on 32-row x 32-token wave tiles (nrq_mmt.hip); mmt_fits:
-// the kernel handles the format.
+// Prefill on 32-row x 32-token wave tiles (nrq_mmt.hip); mmt_fits: the kernel
+// handles the format and shape.
 bool mmt_fits(int dtype, const MatmulLaunch& L);
 int launch_mmt(int dtype, const MatmulLaunch& L);
+// Up to three matrices of one format and width sharing one activation (q|k|v,
+// gate|up) in one launch of the same kernel, y[i] = [batch][rows[i]].
+// NRQ_LAUNCH_BAD_ARG when the kernel does not take the group.
+struct MatmulGroupLaunch {
+  const void* w[3];
+  float* y[3];
+  int rows[3];
+  int nmat;
+  const void* xs;
+  int bpr;
+  int batch;
+  void* stream;
+};
+int launch_mmt_group(int dtype, const MatmulGroupLaunch& G);
 int launch_quantize_q8_0(const QuantLaunch& L);
 // y[0..n) = +0.0 (a kernel, not hipMemsetAsync, so it is safe under graph capture)
 int launch_fill_zero(float* y, long long n, void* stream);

@@ -373,13 +373,23 @@ __device__ __forceinline__ void md_q6k(MdLoad<kQ6K>& L, uint32_t sh, uint32_t* s
 
 }  // namespace
 
+// The matrices of one launch: up to three of one format and width that share
+// the activation (q|k|v, gate|up), their row tiles laid end to end; matrix m
+// owns row tiles tile0_m .. tile0_{m+1} - 1. Separate fields, selected with
+// uniform conditions (an indexed array would live in private memory).
+struct MdMats {
+  const uint8_t *w0, *w1, *w2;
+  float *y0, *y1, *y2;
+  int rows0, rows1, rows2;
+  int tile1, tile2;  // first row tile of matrices 1 and 2
+};
+
 // NB register buffers of block loads: NB = 1 reloads the one buffer as soon as
 // its operands are consumed; NB = 2 or 4 is a ring whose loads run NB - 1
 // rounds ahead of the block being computed.
 template <int FMT, int KS, int NB>
-__global__ __launch_bounds__(64 * KS) void mmd_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ X,
-                                                      float* __restrict__ Y, int rows, int bpr, int batch, int ntt,
-                                                      int nrt) {
+__global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* __restrict__ X, int bpr, int batch,
+                                                      int ntt, int nrt) {
   constexpr int OWN = 16 / KS;  // chain elements per lane when KS > 1
   constexpr size_t BS = FMT == kQ4K ? kQ4KBytes : FMT == kQ6K ? kQ6KBytes : kQ8_0Bytes;
   constexpr size_t XS = FMT == kQ8_0 ? kQ8_0Bytes : kQ8KBytes;  // activation block bytes
@@ -390,10 +400,14 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(const uint8_t* __restrict_
   const int tt = slot % ntt;
   const int rt = (slot / ntt) * 8 + xcd;
   if (rt >= nrt) return;  // padding workgroup (uniform, before any barrier)
+  const int m = rt >= M.tile2 ? 2 : rt >= M.tile1 ? 1 : 0;
+  const uint8_t* __restrict__ W = m == 2 ? M.w2 : m == 1 ? M.w1 : M.w0;
+  float* __restrict__ Y = m == 2 ? M.y2 : m == 1 ? M.y1 : M.y0;
+  const int rows = m == 2 ? M.rows2 : m == 1 ? M.rows1 : M.rows0;
   const int lane = threadIdx.x & 63;
   const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ta = lane & 31, kg = lane >> 5;
-  const int r0 = rt * 32, t0 = tt * 32;
+  const int r0 = (rt - (m == 2 ? M.tile2 : m == 1 ? M.tile1 : 0)) * 32, t0 = tt * 32;
   // rows and tokens past the end load valid memory (the last row / token) and store nothing
   const uint8_t* xrow = X + (size_t)min(t0 + ta, batch - 1) * bpr * XS;
   const uint8_t* wrow = W + (size_t)min(r0 + ta, rows - 1) * bpr * BS;
@@ -553,20 +567,43 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(const uint8_t* __restrict_
 
 namespace {
 
+// A launch's matrices, and its total row tiles.
+MdMats md_mats(const MatmulGroupLaunch& G, int* nrt) {
+  MdMats M{};
+  const int t0 = (G.rows[0] + 31) / 32;
+  const int t1 = G.nmat > 1 ? (G.rows[1] + 31) / 32 : 0;
+  const int t2 = G.nmat > 2 ? (G.rows[2] + 31) / 32 : 0;
+  M.w0 = (const uint8_t*)G.w[0];
+  M.y0 = G.y[0];
+  M.rows0 = G.rows[0];
+  M.w1 = G.nmat > 1 ? (const uint8_t*)G.w[1] : M.w0;
+  M.y1 = G.nmat > 1 ? G.y[1] : M.y0;
+  M.rows1 = G.nmat > 1 ? G.rows[1] : M.rows0;
+  M.w2 = G.nmat > 2 ? (const uint8_t*)G.w[2] : M.w0;
+  M.y2 = G.nmat > 2 ? G.y[2] : M.y0;
+  M.rows2 = G.nmat > 2 ? G.rows[2] : M.rows0;
+  M.tile1 = G.nmat > 1 ? t0 : 0x7fffffff;
+  M.tile2 = G.nmat > 2 ? t0 + t1 : 0x7fffffff;
+  *nrt = t0 + t1 + t2;
+  return M;
+}
+
 template <int FMT, int KS, int NB>
-int md_launch_t(const MatmulLaunch& L) {
-  const int nrt = (L.rows + 31) / 32, ntt = (L.batch + 31) / 32;
+int md_launch_t(const MatmulGroupLaunch& G) {
+  int nrt = 0;
+  const MdMats M = md_mats(G, &nrt);
+  const int ntt = (G.batch + 31) / 32;
   const long rt_pad = (long)((nrt + 7) / 8) * 8;
   const long nwg = rt_pad * ntt;
   if (nwg > 0x7fffffffL) return NRQ_LAUNCH_BAD_ARG;
   const size_t lds = (size_t)KS * kMdScalDw * 4 + (KS > 1 ? (size_t)2 * KS * 1024 * 4 : 0);
-  hipLaunchKernelGGL((mmd_kernel<FMT, KS, NB>), dim3((unsigned)nwg), dim3(64 * KS), lds, (hipStream_t)L.stream,
-                     (const uint8_t*)L.w, (const uint8_t*)L.xs, L.y, L.rows, L.bpr, L.batch, ntt, nrt);
+  hipLaunchKernelGGL((mmd_kernel<FMT, KS, NB>), dim3((unsigned)nwg), dim3(64 * KS), lds, (hipStream_t)G.stream, M,
+                     (const uint8_t*)G.xs, G.bpr, G.batch, ntt, nrt);
   return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
 }
 
 template <int FMT, int NB>
-int md_launch_ks(const MatmulLaunch& L, int ks) {
+int md_launch_ks(const MatmulGroupLaunch& L, int ks) {
   if (ks >= 8) return md_launch_t<FMT, 8, NB>(L);
   if (ks == 4) return md_launch_t<FMT, 4, NB>(L);
   if (ks == 2) return md_launch_t<FMT, 2, NB>(L);
@@ -576,7 +613,7 @@ int md_launch_ks(const MatmulLaunch& L, int ks) {
 // K-quant blocks (256 values) need one or two buffers; Q8_0 blocks (32
 // values) take a ring of four to keep enough loads in flight.
 template <int FMT>
-int md_launch(const MatmulLaunch& L, int ks, int nb) {
+int md_launch(const MatmulGroupLaunch& L, int ks, int nb) {
   if constexpr (FMT == kQ8_0) {
     if (nb >= 4) return md_launch_ks<FMT, 4>(L, ks);
   }
@@ -588,20 +625,31 @@ int md_launch(const MatmulLaunch& L, int ks, int nb) {
 // on 9728 x 2560); else the fewest that give about one wave per SIMD (4 per
 // CU), and at most 4 for rows of 16 blocks or fewer (more splits leave each
 // wave one or two blocks). Measured on the Qwen3-4B layer shapes at M = 64.
-int md_choose(int dtype, const MatmulLaunch& L) {
+int md_choose(int dtype, long row_tiles, int batch, int bpr) {
   const char* env = getenv("NRQ_MMT_SPLITS");  // tuning override: 1, 2, 4 or 8
   if (env && env[0]) {
     const int ks = atoi(env);
     if (ks == 1 || ks == 2 || ks == 4 || ks == 8) return ks;
   }
-  const long tiles = (long)((L.rows + 31) / 32) * ((L.batch + 31) / 32);
-  const int cap = L.bpr <= 16 ? 4 : 8;
+  const long tiles = row_tiles * ((batch + 31) / 32);
+  const int cap = bpr <= 16 ? 4 : 8;
   // Q8_0 blocks are an eighth of a K-quant block's work: aim for twice the waves
   const long want = dtype == kQ8_0 ? 8L * 256 : 4L * 256;
   if (dtype != kQ8_0 && tiles >= 2L * 256) return 1;
   int ks = 1;
-  while (ks < cap && ks < L.bpr && tiles * ks < want) ks *= 2;
+  while (ks < cap && ks < bpr && tiles * ks < want) ks *= 2;
   return ks;
+}
+
+int md_buffers(int dtype, int ks);
+
+int md_group(int dtype, const MatmulGroupLaunch& G) {
+  long row_tiles = 0;
+  for (int i = 0; i < G.nmat; i++) row_tiles += (G.rows[i] + 31) / 32;
+  const int ks = md_choose(dtype, row_tiles, G.batch, G.bpr);
+  const int nb = md_buffers(dtype, ks);
+  if (dtype == kQ8_0) return md_launch<kQ8_0>(G, ks, nb);
+  return dtype == kQ4K ? md_launch<kQ4K>(G, ks, nb) : md_launch<kQ6K>(G, ks, nb);
 }
 
 // Register buffers of block loads. K-quants: two (a block's loads issued a
@@ -629,10 +677,32 @@ bool mmt_fits(int dtype, const MatmulLaunch& L) {
 
 int launch_mmt(int dtype, const MatmulLaunch& L) {
   if (L.rows <= 0 || L.bpr <= 0 || L.batch <= 0) return 0;
-  const int ks = md_choose(dtype, L);
-  const int nb = md_buffers(dtype, ks);
-  if (dtype == kQ8_0) return md_launch<kQ8_0>(L, ks, nb);
-  return dtype == kQ4K ? md_launch<kQ4K>(L, ks, nb) : md_launch<kQ6K>(L, ks, nb);
+  MatmulGroupLaunch G{};
+  G.w[0] = L.w;
+  G.y[0] = L.y;
+  G.rows[0] = L.rows;
+  G.nmat = 1;
+  G.xs = L.xs;
+  G.bpr = L.bpr;
+  G.batch = L.batch;
+  G.stream = L.stream;
+  return md_group(dtype, G);
+}
+
+// Every matrix of the group in one launch when the 32 x 32 kernel takes their
+// format and the group's rows (Q8_0: 1024 in all, 4-byte aligned bases).
+int launch_mmt_group(int dtype, const MatmulGroupLaunch& G) {
+  if (G.nmat < 1 || G.nmat > 3 || G.bpr <= 0 || G.batch <= 0) return NRQ_LAUNCH_BAD_ARG;
+  if (dtype != kQ8_0 && dtype != kQ4K && dtype != kQ6K) return NRQ_LAUNCH_BAD_ARG;
+  int total = 0;
+  uintptr_t bases = (uintptr_t)G.xs;
+  for (int i = 0; i < G.nmat; i++) {
+    if (G.rows[i] <= 0) return NRQ_LAUNCH_BAD_ARG;
+    total += G.rows[i];
+    bases |= (uintptr_t)G.w[i];
+  }
+  if (dtype == kQ8_0 && (total < 1024 || (bases & 3u))) return NRQ_LAUNCH_BAD_ARG;
+  return md_group(dtype, G);
 }
 
 }  // namespace nrq

@@ -40,6 +40,18 @@ def matmul(dtype: int, order: int, y: torch.Tensor, w: torch.Tensor, xs: torch.T
                                          batch, _stream(stream)))
 
 
+def matmul_group(dtype: int, ys, ws, rows, xs: torch.Tensor, cols: int, batch: int, stream=None) -> None:
+    """Acts::matmul_group (infer.rs:180-228): 1-3 matrices over one activation, scalar order."""
+    import ctypes as C
+
+    _lib.init(torch.cuda.current_device())
+    n = len(ws)
+    yp = (C.c_void_p * n)(*[_dev(y, "y") for y in ys])
+    wp = (C.c_void_p * n)(*[_dev(w, "w") for w in ws])
+    rp = (C.c_size_t * n)(*rows)
+    _lib.check(_lib.lib().nrq_dev_matmul_group(dtype, n, yp, wp, rp, _dev(xs, "xs"), cols, batch, _stream(stream)))
+
+
 def quantize_q8_0(src: torch.Tensor, out: torch.Tensor, stream=None) -> None:
     _lib.init(torch.cuda.current_device())
     _lib.check(_lib.lib().nrq_dev_quantize_q8_0(_dev(src, "src"), src.numel(), _dev(out, "out"), _stream(stream)))

@@ -449,3 +449,30 @@ def test_matmul_every_split_count(gpu, oracle, dtype, monkeypatch):
             for rows, cols, batch, w, xs, want in cases:
                 assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, batch), want,
                                f"splits {ks} buffers {nb} rows {rows} cols {cols} batch {batch}")
+
+
+@pytest.mark.parametrize("dtype", [1, 2, 3])
+def test_matmul_group(gpu, oracle, dtype):
+    """nrq_dev_matmul_group (Acts::matmul_group, infer.rs:180-228): every
+    matrix of a group over one activation equals the oracle's matmul bit for
+    bit, whether the group runs as one launch of the 32 x 32 kernel (ragged
+    rows, partial tiles, batches past 64) or as separate launches (Q8_0 below
+    1024 rows in all, one matrix)."""
+    import torch
+
+    from nightrun_amd import device
+
+    qk = oracle.QK[dtype]
+    big = (1100, 300, 40) if dtype == 1 else (96, 40, 33)
+    small = (300, 200) if dtype == 1 else (50,)
+    for rows_list, bpr, batch in ((big, 8, 64), (big, 3, 70), (small, 5, 17)):
+        cols = bpr * qk
+        xs = oracle.quantize_act(dtype, oracle.Rng(900 + bpr).normal(batch * cols))
+        ws = [oracle.gen_weights(dtype, 910 + i + bpr, r, cols) for i, r in enumerate(rows_list)]
+        ys = [torch.empty(batch * r, dtype=torch.float32, device="cuda") for r in rows_list]
+        device.matmul_group(dtype, ys, [torch.from_numpy(w).cuda() for w in ws], list(rows_list),
+                            torch.from_numpy(xs).cuda(), cols, batch)
+        torch.cuda.synchronize()
+        for i, r in enumerate(rows_list):
+            want = oracle.matmul(dtype, 0, ws[i], xs, r, cols, batch, threads=THREADS)
+            assert_bitwise(ys[i].cpu().numpy(), want, f"matrix {i} rows {r} bpr {bpr} batch {batch}")
