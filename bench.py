@@ -351,6 +351,19 @@ def measure_decode(fill=1024, n=128):
     t0 = time.perf_counter()
     out = m.generate(int(np.argmax(lg)), n)
     dt = time.perf_counter() - t0
+    # the same steps drawing from the top 64 at temperature 0.7, top-p 0.9 (the
+    # reference's chat defaults, crates/nr-boot/src/app.rs:290): the sampler
+    # kernel in place of argmax inside the step graph
+    m.reset()
+    m.prefill(prompt, logits=False)
+    m.set_sampler(0.7, 0.9, 0x5EED0006)
+    m.generate(int(np.argmax(lg)), 8)  # captures the sampling step
+    m.reset()
+    m.prefill(prompt, logits=False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    m.generate(int(np.argmax(lg)), n)
+    sdt = time.perf_counter() - t0
     m.close()
     torch.cuda.empty_cache()
     mid = fill + n // 2
@@ -364,6 +377,7 @@ def measure_decode(fill=1024, n=128):
             "bytes_per_token": model_bytes_per_token(cfg, mid),
             "gbs": round(model_bytes_per_token(cfg, mid) * n / dt / 1e9, 1), "tokens": int(n),
             "first_tokens": [int(t) for t in out[:4]], "load": load, "verify_crc": crc,
+            "sampled_tok_s": round(n / sdt, 1),
             "prefill": {"tokens": int(fill), "chunks_of": 64, "seconds": round(pf_dt, 4),
                         "tok_s": round(fill / pf_dt, 1),
                         "what": "nrq_model_prefill of the random prompt from position 0 (KV 0..1023), host sync "

@@ -817,8 +817,12 @@ __global__ __launch_bounds__(kArgNT) void argmax_kernel(const float* __restrict_
   }
 }
 
-constexpr int kSampNT = 1024;
-constexpr int kTopK = 64;  // sample.rs:12
+constexpr int kTopK = 64;                      // sample.rs:12
+constexpr int kSelPartWaves = 4;               // waves per workgroup of the first kernel
+constexpr int kSelPer = 8;                     // logits per lane in the first kernel
+constexpr int kSelSlice = kSelPartWaves * 64 * kSelPer;  // logits per workgroup of the first kernel
+constexpr int kSelWaves = 16;                  // waves of the second kernel
+constexpr int kSelPart = 2 * kTopK;            // words per partial list (64 packed candidates)
 
 // Sampler::next_f32 (sample.rs:23-30)
 __device__ inline float sampler_next_f32(unsigned long long* rng) {
@@ -830,164 +834,208 @@ __device__ inline float sampler_next_f32(unsigned long long* rng) {
   return (float)(x >> 40) / (float)(1u << 24);
 }
 
-// Sampler::sample (sample.rs:32-96) for temperature > 0, one workgroup.
-//  1. The 64 largest logits (NaN and -inf never qualify, as the heap's strict
-//     > never admits them): an 8-bit radix select over order-preserving keys
-//     finds the 64th largest key K (per-wave histograms, four passes); every
-//     logit above K and the first (by token id) of those equal to K are taken.
-//     Exact ties are thus ordered by token id; the reference's unstable sort
-//     leaves their order open, and is matched whenever the drawn logit is not
-//     tied. Fewer than 64 valid logits leave (-inf, 0) slots, as the heap's
-//     initial entries do.
-//  2. Descending order: each candidate's rank among the others.
-//  3. One lane, in the reference's order: p_i = expf((v_i - max) / T), the
-//     running sums, the nucleus cut, r = next_f32() * cum, the draw.
+// Order-preserving key of a logit: larger logit, larger key; -0 and +0 share a
+// key (they compare equal); NaN and -inf get 0, "no candidate" (the heap's
+// strict > never admits them, sample.rs:41-49).
+__device__ inline uint32_t logit_key(float v) {
+  if (!(v > -INFINITY)) return 0u;
+  uint32_t u = __float_as_uint(v);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// A candidate packed as key << 32 | ~id: a larger word is a larger logit, or an
+// equal one with a lower id; 0 is an empty slot (below every candidate).
+__device__ inline unsigned long long cand_pack(uint32_t key, uint32_t id) {
+  return key ? ((unsigned long long)key << 32) | (uint32_t)~id : 0ull;
+}
+
+__device__ inline void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ inline int lanes_below(unsigned long long m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// The exact 64 largest of a wave's 64*E (key, id) pairs (ids distinct among
+// present keys; key 0 = absent), returned sorted: lane l holds the l-th
+// largest packed candidate. A bisection over the key bits, counting with
+// ballots, finds the 64th largest key T; every key above T is taken, and of
+// those equal to T the lowest ids, by a second bisection over the id bits when
+// there are more than are needed. The set is packed into sc (this wave's 64
+// words of LDS), then each candidate moves to its rank. Fewer than 64 present
+// keys leave empty slots at the end.
+template <int E>
+__device__ inline unsigned long long wave_sorted64(const uint32_t (&k)[E], const uint32_t (&id)[E],
+                                                   unsigned long long* sc) {
+  const int lane = threadIdx.x & 63;
+  uint32_t T = 0;
+  for (int b = 31; b >= 0; b--) {
+    const uint32_t c = T | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int e = 0; e < E; e++) cnt += __popcll(__ballot(k[e] >= c));
+    if (cnt >= kTopK) T = c;
+  }
+  uint32_t J = 0xffffffffu;  // of the keys equal to T, the ids up to J
+  if (T != 0) {              // T is at most the key of +inf, so T + 1 does not wrap
+    int gt = 0, eq = 0;
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+      gt += __popcll(__ballot(k[e] > T));
+      eq += __popcll(__ballot(k[e] == T));
+    }
+    const int need = kTopK - gt;
+    if (eq > need) {
+      J = 0;
+      for (int b = 31; b >= 0; b--) {
+        const uint32_t c = J | (1u << b);
+        int cnt = 0;
+#pragma unroll
+        for (int e = 0; e < E; e++) cnt += __popcll(__ballot(k[e] == T && id[e] < c));
+        if (cnt < need) J = c;
+      }
+    }
+  }
+  int base = 0;
+#pragma unroll
+  for (int e = 0; e < E; e++) {
+    const bool sel = T == 0 ? k[e] != 0 : (k[e] > T || (k[e] == T && id[e] <= J));
+    const unsigned long long m = __ballot(sel);
+    if (sel) sc[base + lanes_below(m)] = cand_pack(k[e], id[e]);
+    base += __popcll(m);
+  }
+  if (lane >= base) sc[lane] = 0ull;
+  wave_sync();
+  const unsigned long long c = sc[lane];
+  int r = 0;
+  const ulonglong2* s2 = (const ulonglong2*)sc;
+#pragma unroll
+  for (int j = 0; j < kTopK / 2; j++) {
+    const ulonglong2 t = s2[j];
+    r += (t.x > c ? 1 : 0) + (t.y > c ? 1 : 0);
+  }
+  if (c == 0ull) r = lane;  // empty slots already follow the present ones
+  wave_sync();
+  sc[r] = c;
+  wave_sync();
+  return sc[lane];
+}
+
+// The 64 largest of two sorted lists (lane l holds each one's l-th largest),
+// sorted: max(a_l, b_{63-l}) is bitonic and holds the 64 largest of the union;
+// a bitonic merge orders it.
+__device__ inline unsigned long long merge64(unsigned long long a, unsigned long long b) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long rb = __shfl(b, 63 - lane);
+  unsigned long long c = a > rb ? a : rb;
+#pragma unroll
+  for (int j = 32; j > 0; j >>= 1) {
+    const unsigned long long o = __shfl_xor(c, j);
+    const bool keep_max = (lane & j) == 0;
+    c = keep_max ? (c > o ? c : o) : (c < o ? c : o);
+  }
+  return c;
+}
+
+// First half of Sampler::sample (sample.rs:38-61) for temperature > 0: each
+// workgroup takes kSelSlice logits, each wave selects the 64 largest of its
+// 512, the four sorted lists merge in a tree, and the workgroup writes its
+// sorted 64 as one partial list.
+__global__ __launch_bounds__(kSelPartWaves * 64) void top64_part_kernel(const float* __restrict__ x, int n,
+                                                                        unsigned long long* __restrict__ part) {
+  __shared__ unsigned long long sc[kSelPartWaves][kTopK];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int base = blockIdx.x * kSelSlice + w * 64 * kSelPer;
+  uint32_t k[kSelPer], id[kSelPer];
+  float v[kSelPer];
+#pragma unroll
+  for (int e = 0; e < kSelPer; e++) v[e] = x[min(base + e * 64 + lane, n - 1)];  // all loads in flight
+#pragma unroll
+  for (int e = 0; e < kSelPer; e++) {
+    const int i = base + e * 64 + lane;
+    id[e] = (uint32_t)i;
+    k[e] = i < n ? logit_key(v[e]) : 0u;
+  }
+  unsigned long long c = wave_sorted64<kSelPer>(k, id, sc[w]);
+  __syncthreads();
+#pragma unroll
+  for (int h = kSelPartWaves / 2; h >= 1; h >>= 1) {
+    if (w < h) {
+      c = merge64(c, sc[w + h][lane]);
+      sc[w][lane] = c;
+    }
+    __syncthreads();
+  }
+  if (w == 0) part[(size_t)blockIdx.x * kTopK + lane] = c;
+}
+
+// Second half of Sampler::sample (sample.rs:38-96), one workgroup over the
+// nparts sorted partial lists:
+//  1. The 64 largest of the lists: wave w merges lists w, w + 16, ..., then the
+//     16 waves' lists merge in a tree. The logits of the reference's heap are
+//     thus found exactly, in descending order; exact ties are ordered by token
+//     id, where the reference's unstable sort leaves their order open (matched
+//     whenever the drawn logit is not tied). Fewer than 64 valid logits leave
+//     (-inf, 0) slots, as the heap's initial entries do.
+//  2. In the reference's order: p_k = expf((v_k - max) / T) (one per lane),
+//     the running sums s_k = s_{k-1} + p_k (in order), the nucleus n = first k
+//     with s_k >= top_p * s_63, r = next_f32() * s_{n-1}, and the first k < n
+//     with r <= s_k (else the last of the nucleus).
 // With ctl, the step's bookkeeping of argmax_kernel; else the id goes to *token.
-__global__ __launch_bounds__(kSampNT) void sample_kernel(const float* __restrict__ x, int n, float temperature,
-                                                         float top_p, unsigned long long* __restrict__ rng,
-                                                         int* __restrict__ ctl, uint32_t* __restrict__ out_tokens,
-                                                         int max_out, uint32_t* __restrict__ token) {
-  constexpr int NW = kSampNT / 64;
-  __shared__ int hist[NW][256];
-  __shared__ int total[256];
-  __shared__ uint32_t s_prefix, s_mask;
-  __shared__ int s_need, s_all, s_slot;
-  __shared__ int scan[kSampNT];
-  __shared__ float cv[kTopK], sv[kTopK], pr[kTopK];
-  __shared__ uint32_t ci[kTopK], si[kTopK];
-  const int tid = threadIdx.x, wv = tid >> 6;
-  const int chunk = (n + kSampNT - 1) / kSampNT;
-  const int c0 = min(n, tid * chunk), c1 = min(n, c0 + chunk);
-  auto key_of = [](float v) {
-    const uint32_t u = __float_as_uint(v);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+__global__ __launch_bounds__(kSelWaves * 64) void top64_sample_kernel(
+    const unsigned long long* __restrict__ part, int nparts, const float* __restrict__ x, float temperature,
+    float top_p, unsigned long long* __restrict__ rng, int* __restrict__ ctl, uint32_t* __restrict__ out_tokens,
+    int max_out, uint32_t* __restrict__ token) {
+  __shared__ unsigned long long sc[kSelWaves][kTopK];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // list q, or an empty one past the last (clamped loads, four in flight)
+  auto list = [&](int q) {
+    const unsigned long long c = part[(size_t)min(q, nparts - 1) * kTopK + lane];
+    return q < nparts ? c : 0ull;
   };
-  if (tid == 0) {
-    s_prefix = 0;
-    s_mask = 0;
-    s_need = kTopK;
-    s_all = 0;
-    s_slot = 0;
+  unsigned long long c = list(w);
+  for (int q = w + kSelWaves; q < nparts; q += 3 * kSelWaves) {
+    const unsigned long long l1 = list(q), l2 = list(q + kSelWaves), l3 = list(q + 2 * kSelWaves);
+    c = merge64(c, l1);
+    if (q + kSelWaves < nparts) c = merge64(c, l2);
+    if (q + 2 * kSelWaves < nparts) c = merge64(c, l3);
   }
+  sc[w][lane] = c;
   __syncthreads();
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int b = tid; b < NW * 256; b += kSampNT) (&hist[0][0])[b] = 0;
-    __syncthreads();
-    const uint32_t prefix = s_prefix, mask = s_mask;
-    for (int i = c0; i < c1; i++) {
-      const float v = x[i];
-      if (!(v > -INFINITY)) continue;
-      const uint32_t k = key_of(v);
-      if ((k & mask) == prefix) atomicAdd(&hist[wv][(k >> shift) & 255u], 1);
+#pragma unroll
+  for (int h = kSelWaves / 2; h >= 1; h >>= 1) {
+    if (w < h) {
+      c = merge64(c, sc[w + h][lane]);
+      sc[w][lane] = c;
     }
     __syncthreads();
-    if (tid < 256) {
-      int c = 0;
-      for (int w = 0; w < NW; w++) c += hist[w][tid];
-      total[tid] = c;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      int need = s_need, above = 0, b = 255;
-      for (; b >= 0; b--) {
-        if (above + total[b] >= need) break;
-        above += total[b];
-      }
-      if (b < 0) {
-        s_all = 1;  // fewer than `need` keys match: every valid logit is a candidate
-      } else {
-        s_need = need - above;
-        s_prefix = prefix | ((uint32_t)b << shift);
-        s_mask = mask | (255u << shift);
-      }
-    }
-    __syncthreads();
-    if (s_all) break;
   }
-  const bool all = s_all != 0;
-  const uint32_t K = s_prefix;
-  const int need = s_need;  // logits equal to K to take, the lowest ids first
-  int eq = 0;
-  for (int i = c0; i < c1; i++) {
-    const float v = x[i];
-    if (!(v > -INFINITY)) continue;
-    const uint32_t k = key_of(v);
-    if (all || k > K) {
-      const int slot = atomicAdd(&s_slot, 1);
-      cv[slot] = v;
-      ci[slot] = (uint32_t)i;
-    } else if (k == K) {
-      eq++;
-    }
+  if (w != 0) return;
+  const uint32_t cid = c ? ~(uint32_t)c : 0u;
+  const float v = c ? x[cid] : -INFINITY;
+  const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float p = dev_expf((v - mx) / temperature);
+  // s_q = s_{q-1} + p_q in order, every lane running the chain; lane q keeps s_q
+  float s = 0.0f, mine = 0.0f;
+#pragma unroll
+  for (int q = 0; q < kTopK; q++) {
+    s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), q));
+    mine = lane == q ? s : mine;
   }
-  scan[tid] = eq;
-  __syncthreads();
-  if (tid == 0) {  // exclusive prefix over the threads, in id order
-    int run = 0;
-    for (int t = 0; t < kSampNT; t++) {
-      const int c = scan[t];
-      scan[t] = run;
-      run += c;
-    }
-  }
-  __syncthreads();
-  if (!all && eq) {
-    int rank = scan[tid];
-    const int base = kTopK - need;
-    for (int i = c0; i < c1 && rank < need; i++) {
-      const float v = x[i];
-      if (!(v > -INFINITY) || key_of(v) != K) continue;
-      cv[base + rank] = v;
-      ci[base + rank] = (uint32_t)i;
-      rank++;
-    }
-  }
-  __syncthreads();
-  const int nv = all ? s_slot : kTopK;  // valid candidates
-  if (tid < kTopK) {
-    if (tid < nv) {
-      const float v = cv[tid];
-      const uint32_t id = ci[tid];
-      int r = 0;
-      for (int j = 0; j < nv; j++) r += (cv[j] > v || (cv[j] == v && ci[j] < id)) ? 1 : 0;
-      sv[r] = v;
-      si[r] = id;
-    } else {
-      sv[tid] = -INFINITY;
-      si[tid] = 0;
-    }
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float* p = pr;
-    const float mx = sv[0];
-    float sum = 0.0f;
-    for (int k = 0; k < kTopK; k++) {
-      p[k] = dev_expf((sv[k] - mx) / temperature);
-      sum = sum + p[k];
-    }
-    const float cut = top_p * sum;
-    float cum = 0.0f;
-    int nn = kTopK;
-    for (int k = 0; k < kTopK; k++) {
-      cum = cum + p[k];
-      if (cum >= cut) {
-        nn = k + 1;
-        break;
-      }
-    }
-    unsigned long long st = *rng;
-    const float r = sampler_next_f32(&st) * cum;
+  const float cut = top_p * s;
+  const unsigned long long inn = __ballot(mine >= cut);
+  const int nn = inn ? __builtin_ctzll(inn) + 1 : kTopK;
+  const float cum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), nn - 1));
+  unsigned long long st = *rng;
+  const float rr = sampler_next_f32(&st) * cum;
+  const unsigned long long hit = __ballot(lane < nn && rr <= mine);
+  const uint32_t pick = (uint32_t)__builtin_amdgcn_readlane((int)cid, hit ? __builtin_ctzll(hit) : nn - 1);
+  if (lane == 0) {
     *rng = st;
-    uint32_t pick = si[nn - 1];
-    float acc = 0.0f;
-    for (int k = 0; k < nn; k++) {
-      acc = acc + p[k];
-      if (r <= acc) {
-        pick = si[k];
-        break;
-      }
-    }
     if (ctl) {
       ctl[CTL_TOKEN] = (int)pick;
       const int step = ctl[CTL_STEP];
@@ -1078,6 +1126,7 @@ struct nrq_model {
   // Sampler (sample.rs:5-21): temperature <= 0 is greedy
   float samp_t = 0.0f, samp_p = 1.0f;
   unsigned long long* rng = nullptr;  // device word, seed | 1
+  unsigned long long* samp_part = nullptr;  // the sampler's partial top-64 lists
 };
 
 namespace nrq {
@@ -1237,8 +1286,12 @@ int enqueue_step(nrq_model* m) {
   if ((rc = norm_quant(m, xr, pending, m->out_norm, m->output.dt))) return rc;
   if ((rc = matvec(m, m->output, m->xq, m->logits, c.vocab, d))) return rc;
   if (m->samp_t > 0.0f) {
-    hipLaunchKernelGGL(nrq::sample_kernel, dim3(1), dim3(nrq::kSampNT), 0, m->stream, m->logits, c.vocab, m->samp_t,
-                       m->samp_p, m->rng, m->ctl, m->out_tokens, m->max_out, nullptr);
+    const int np = (c.vocab + nrq::kSelSlice - 1) / nrq::kSelSlice;
+    hipLaunchKernelGGL(nrq::top64_part_kernel, dim3(np), dim3(nrq::kSelPartWaves * 64), 0, m->stream, m->logits,
+                       c.vocab, m->samp_part);
+    hipLaunchKernelGGL(nrq::top64_sample_kernel, dim3(1), dim3(nrq::kSelWaves * 64), 0, m->stream, m->samp_part, np,
+                       m->logits,
+                       m->samp_t, m->samp_p, m->rng, m->ctl, m->out_tokens, m->max_out, nullptr);
     if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: sampler launch failed");
     return NRQ_OK;
   }
@@ -1491,6 +1544,7 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
       {(void**)&m->xq2, act_bytes(NRQ_Q8_0, m->maxd) + act_bytes(NRQ_Q4_K, m->maxd) + 64},
       {(void**)&m->ctl, nrq::CTL_WORDS * 4},
       {(void**)&m->rng, 8},
+      {(void**)&m->samp_part, (size_t)(c.vocab + nrq::kSelSlice - 1) / nrq::kSelSlice * nrq::kSelPart * 4},
   };
   for (auto& a : allocs) {
     if ((e = hipMalloc(a.p, a.bytes)) != hipSuccess) return bail(e, "hipMalloc");
@@ -1589,8 +1643,21 @@ int nrq_dev_sample(const float* logits, int n, float temperature, float top_p, u
   if (!logits || !token || (temperature > 0.0f && !rng)) return mfail(NRQ_ERR_ARG, "nrq_dev_sample: null pointer");
   if (n <= 0) return mfail(NRQ_ERR_ARG, "nrq_dev_sample: empty logits");
   if (temperature > 0.0f) {
-    hipLaunchKernelGGL(nrq::sample_kernel, dim3(1), dim3(nrq::kSampNT), 0, (hipStream_t)stream, logits, n,
-                       temperature, top_p, (unsigned long long*)rng, nullptr, nullptr, 0, token);
+    // the partial lists live in stream-ordered memory, so calls on different
+    // streams do not share them
+    hipStream_t s = (hipStream_t)stream;
+    const int np = (n + nrq::kSelSlice - 1) / nrq::kSelSlice;
+    unsigned long long* part = nullptr;
+    if (hipMallocAsync((void**)&part, (size_t)np * nrq::kSelPart * 4, s) != hipSuccess)
+      return mfail(NRQ_ERR_DEVICE, "nrq_dev_sample: hipMallocAsync failed");
+    hipLaunchKernelGGL(nrq::top64_part_kernel, dim3(np), dim3(nrq::kSelPartWaves * 64), 0, s, logits, n, part);
+    hipLaunchKernelGGL(nrq::top64_sample_kernel, dim3(1), dim3(nrq::kSelWaves * 64), 0, s, part, np, logits,
+                       temperature,
+                       top_p, (unsigned long long*)rng, nullptr, nullptr, 0, token);
+    const hipError_t le = hipGetLastError();
+    if (hipFreeAsync(part, s) != hipSuccess || le != hipSuccess)
+      return mfail(NRQ_ERR_DEVICE, "nrq_dev_sample: launch failed");
+    return NRQ_OK;
   } else {
     hipLaunchKernelGGL(nrq::argmax_kernel, dim3(1), dim3(nrq::kArgNT), 0, (hipStream_t)stream, logits, n, nullptr,
                        token, 1);
@@ -1749,7 +1816,7 @@ int nrq_model_destroy(nrq_model* m) {
   if (m->graph) hipGraphDestroy(m->graph);
   void* bufs[] = {m->freqs, m->rope_cs, m->kc, m->vc, m->x, m->x2, m->xb, m->q, m->k, m->v, m->attn, m->gate, m->up, m->xb2,
                   m->logits, m->xq, m->xq2, m->ctl, m->out_tokens, m->owned, m->bx, m->bxb, m->bxn, m->bq,
-                  m->bk, m->bv, m->battn, m->bgate, m->bup, m->brope, m->bxq, m->bxq2, m->btok, m->rng};
+                  m->bk, m->bv, m->battn, m->bgate, m->bup, m->brope, m->bxq, m->bxq2, m->btok, m->rng, m->samp_part};
   for (void* p : bufs)
     if (p) hipFree(p);
   if (m->stream) hipStreamDestroy(m->stream);

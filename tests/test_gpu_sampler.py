@@ -96,3 +96,35 @@ def test_generate_with_sampler_matches_oracle(gpu, oracle):
         assert list(m.generate(int(got[-1]), 5)) == greedy_want
     finally:
         m.close()
+
+
+def test_device_sampler_ties_at_the_top(gpu, oracle):
+    """More than 64 logits tied at the maximum: the reference's heap admits them
+    in index order and never evicts one (strict >), so its candidates are the 64
+    lowest ids of the tie, as the device's id bisection picks them (in each
+    wave's slice, each workgroup's, and the final list)."""
+    import torch
+
+    from nightrun_amd.model import sample
+
+    rng = np.random.default_rng(77)
+    cases = [np.full(1000, 0.5, np.float32), np.zeros(128256, np.float32)]
+    x = rng.normal(0, 1, 128256).astype(np.float32)
+    x[rng.choice(128256, 300, replace=False)] = 9.0  # 300 ties above every other logit
+    cases.append(x)
+    y = rng.normal(0, 1, 151936).astype(np.float32)
+    y[rng.choice(151936, 70, replace=False)] = -0.0
+    y[y > 0] = -1.0 - y[y > 0]
+    y[rng.choice(151936, 20, replace=False)] = 0.0  # 90 ties of -0 and +0 at the top
+    cases.append(y)
+    for ci, logits in enumerate(cases):
+        dev = torch.from_numpy(logits).cuda()
+        for T, top_p in [(1.0, 1.0), (0.7, 0.9)]:
+            seed = 31 * ci + 5
+            ref = oracle.Sampler(T, top_p, seed)
+            st = torch.tensor([np.uint64(seed | 1).view(np.int64)], dtype=torch.int64, device="cuda")
+            for d in range(8):
+                want = ref.sample(logits)
+                got = sample(dev, T, top_p, st)
+                assert got == want, (ci, T, top_p, d, got, want)
+                assert int(st.cpu().numpy().view(np.uint64)[0]) == ref.rng.value
