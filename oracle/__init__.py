@@ -276,6 +276,10 @@ def _model_lib():
         L.nro_argmax.argtypes, L.nro_argmax.restype = [vp, sz], C.c_uint32
         L.nro_rope_freqs.argtypes = [vp, sz, C.c_float]
         L.nro_rope_apply.argtypes = [vp, sz, sz, vp, sz]
+        L.nro_rope_apply_style.argtypes = [vp, sz, sz, vp, sz, C.c_int]
+        L.nro_rmsnorm_inplace.argtypes = [vp, vp, sz, C.c_float]
+        L.nro_model_set_recipe.argtypes = [vp, C.c_int, C.c_float, C.c_float, C.c_float, C.c_float]
+        L.nro_model_set_qk_norm.argtypes = [vp, C.c_int, vp, vp]
         L.nro_model_new.argtypes, L.nro_model_new.restype = [C.POINTER(C.c_int), C.c_float, C.c_float, C.c_int], vp
         L.nro_model_free.argtypes = [vp]
         L.nro_model_set_globals.argtypes = [vp, vp, C.c_int, vp, C.c_int, vp]
@@ -327,6 +331,14 @@ def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     out = np.zeros_like(x)
     _model_lib().nro_rmsnorm(_p(out), _p(x), _p(w), x.size, eps)
     return out
+
+
+def rmsnorm_inplace(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """vec.rs:17-28: x * (scale * w), scale = 1/sqrtf(mean(x^2) + eps)."""
+    x = np.array(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    _model_lib().nro_rmsnorm_inplace(_p(x), _p(w), x.size, eps)
+    return x
 
 
 def softmax(x: np.ndarray) -> np.ndarray:
@@ -390,10 +402,10 @@ def crc32_bitwise(data, crc: int = 0) -> int:
     return _model_lib().nro_crc32_bitwise(crc, b.ctypes.data if b.size else None, b.nbytes)
 
 
-def rope_apply(x: np.ndarray, head_dim: int, freqs: np.ndarray, pos: int) -> np.ndarray:
+def rope_apply(x: np.ndarray, head_dim: int, freqs: np.ndarray, pos: int, neox: bool = False) -> np.ndarray:
     x = np.array(x, dtype=np.float32)
     f = np.ascontiguousarray(freqs, np.float32)
-    _model_lib().nro_rope_apply(_p(x), x.size, head_dim, _p(f), pos)
+    _model_lib().nro_rope_apply_style(_p(x), x.size, head_dim, _p(f), pos, int(neox))
     return x
 
 
@@ -411,10 +423,12 @@ def layer_shapes(cfg: dict):
             "w_down": (d, ffn)}
 
 
-def gen_model(cfg: dict, seed: int, dtype: int = Q8_0) -> dict:
+def gen_model(cfg: dict, seed: int, dtype: int = Q8_0, qk_norm: bool = False) -> dict:
     """Random-init weights of the given architecture: every matrix with the
     synthetic generator of its dtype (distinct seed per tensor), RMSNorm
-    weights 1.0, output head tied to the embedding."""
+    weights 1.0, output head tied to the embedding. With qk_norm, each layer
+    also gets Qwen3's per-head q/k RMSNorm weights, drawn from [0.5, 1.5) so
+    that a norm left out changes the result."""
     w = {"embed": gen_weights(dtype, seed, cfg["vocab"], cfg["dim"]), "embed_dtype": dtype,
          "out_norm": np.ones(cfg["dim"], np.float32), "layers": []}
     shapes = layer_shapes(cfg)
@@ -425,6 +439,10 @@ def gen_model(cfg: dict, seed: int, dtype: int = Q8_0) -> dict:
             rows, cols = shapes[name]
             lw[name] = gen_weights(dtype, seed + 1 + 16 * l + i, rows, cols)
             lw["dtypes"][name] = dtype
+        if qk_norm:
+            r = np.random.default_rng(seed + 9000 + l)
+            lw["q_norm"] = r.uniform(0.5, 1.5, cfg["head_dim"]).astype(np.float32)
+            lw["k_norm"] = r.uniform(0.5, 1.5, cfg["head_dim"]).astype(np.float32)
         w["layers"].append(lw)
     return w
 
@@ -446,6 +464,12 @@ class Model:
             ptrs = (C.c_void_p * 7)(*[lw[n].ctypes.data for n in LAYER_MATS])
             dts = (C.c_int * 7)(*[lw["dtypes"][n] for n in LAYER_MATS])
             L.nro_model_set_layer(self.h, l, ptrs, dts, _p(lw["attn_norm"]), _p(lw["ffn_norm"]))
+            if "q_norm" in lw:
+                L.nro_model_set_qk_norm(self.h, l, _p(lw["q_norm"]), _p(lw["k_norm"]))
+        r = cfg.get("recipe")
+        if r:
+            L.nro_model_set_recipe(self.h, int(r.get("rope") == "neox"), r.get("embed_scale", 1.0),
+                                   r.get("attn_scale", 0.0), r.get("residual_scale", 1.0), r.get("logit_scale", 1.0))
 
     def __del__(self):
         if getattr(self, "h", None):

@@ -233,6 +233,14 @@ uint32_t nro_argmax(const float *x, size_t n) {
     return (uint32_t)best;
 }
 
+/* vec.rs:17-28 (rmsnorm_inplace): ss in element order, then x *= scale * w */
+void nro_rmsnorm_inplace(float *x, const float *w, size_t n, float eps) {
+    float ss = 0.0f;
+    for (size_t i = 0; i < n; i++) ss += x[i] * x[i];
+    float scale = 1.0f / sqrtf(ss / (float)n + eps);
+    for (size_t i = 0; i < n; i++) x[i] *= scale * w[i];
+}
+
 /* rope.rs:14-34 without Llama-3 scaling: freqs[i] = theta^(-2i/head_dim) */
 void nro_rope_freqs(float *out, size_t head_dim, float theta) {
     for (size_t i = 0; i < head_dim / 2; i++) {
@@ -241,8 +249,9 @@ void nro_rope_freqs(float *out, size_t head_dim, float theta) {
     }
 }
 
-/* rope.rs:49-65, adjacent pairs */
-void nro_rope_apply(float *x, size_t n, size_t head_dim, const float *freqs, size_t pos) {
+/* rope.rs:49-65: pair i is (2i, 2i+1) (Adjacent, Llama/Granite) or
+ * (i, i + head_dim/2) (Neox, Qwen3) */
+void nro_rope_apply_style(float *x, size_t n, size_t head_dim, const float *freqs, size_t pos, int neox) {
     size_t half = head_dim / 2;
     for (size_t h = 0; h + head_dim <= n; h += head_dim) {
         float *head = x + h;
@@ -250,11 +259,15 @@ void nro_rope_apply(float *x, size_t n, size_t head_dim, const float *freqs, siz
             float angle = (float)pos * freqs[i];
             float s, c;
             nro_sincosf(angle, &s, &c);
-            float a = head[2 * i], b = head[2 * i + 1];
-            head[2 * i] = a * c - b * s;
-            head[2 * i + 1] = a * s + b * c;
+            size_t ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
+            float a = head[ia], b = head[ib];
+            head[ia] = a * c - b * s;
+            head[ib] = a * s + b * c;
         }
     }
+}
+void nro_rope_apply(float *x, size_t n, size_t head_dim, const float *freqs, size_t pos) {
+    nro_rope_apply_style(x, n, head_dim, freqs, pos, 0);
 }
 
 /* kernels.rs:146-160 (scalar path) */
@@ -277,6 +290,9 @@ static void axpy_f16_(float *out, float a, const uint16_t *v, size_t n) {
 struct nro_model {
     int dim, n_layers, n_heads, n_kv_heads, head_dim, kv_dim, ffn_dim, vocab, ctx, threads;
     float eps;
+    /* the recipe (infer.rs:447-461): rope style, muP scalars */
+    int neox;
+    float embed_scale, att_scale, residual_scale, logit_recip;
     float *freqs;
     const uint8_t *embed, *output;
     int embed_dt, output_dt;
@@ -285,6 +301,7 @@ struct nro_model {
         const uint8_t *w[7]; /* q, k, v, o, gate, up, down */
         int dt[7];
         const float *attn_norm, *ffn_norm;
+        const float *q_norm, *k_norm; /* Qwen3 per-head RMSNorm weights, head_dim each */
     } L[NRO_MAX_LAYERS];
     uint16_t *kc, *vc;
     float *x, *xb, *xb2, *q, *k, *v, *att, *attn_out, *gate, *up, *logits;
@@ -317,6 +334,11 @@ nro_model *nro_model_new(const int dims[8], float eps, float theta, int threads)
     if ((size_t)m->ffn_dim > maxd) maxd = (size_t)m->ffn_dim;
     m->freqs = (float *)calloc((size_t)m->head_dim / 2, sizeof(float));
     nro_rope_freqs(m->freqs, (size_t)m->head_dim, theta);
+    m->neox = 0;
+    m->embed_scale = 1.0f;
+    m->att_scale = 1.0f / sqrtf((float)m->head_dim);
+    m->residual_scale = 1.0f;
+    m->logit_recip = 1.0f;
     size_t kvn = (size_t)m->n_layers * m->ctx * m->kv_dim;
     m->kc = (uint16_t *)calloc(kvn, 2);
     m->vc = (uint16_t *)calloc(kvn, 2);
@@ -371,6 +393,22 @@ void nro_model_set_layer(nro_model *m, int l, const void *const w[7], const int 
     m->L[l].ffn_norm = ffn_norm;
 }
 
+/* InferCtx::new's recipe fields (infer.rs:447-461): attn_scale 0 means
+ * 1/sqrtf(head_dim); logit_recip = 1/logit_scale */
+void nro_model_set_recipe(nro_model *m, int neox, float embed_scale, float attn_scale, float residual_scale,
+                          float logit_scale) {
+    m->neox = neox;
+    m->embed_scale = embed_scale;
+    m->att_scale = attn_scale != 0.0f ? attn_scale : 1.0f / sqrtf((float)m->head_dim);
+    m->residual_scale = residual_scale;
+    m->logit_recip = 1.0f / logit_scale;
+}
+
+void nro_model_set_qk_norm(nro_model *m, int l, const float *q_norm, const float *k_norm) {
+    m->L[l].q_norm = q_norm;
+    m->L[l].k_norm = k_norm;
+}
+
 int nro_model_pos(const nro_model *m) { return m->pos; }
 void nro_model_reset(nro_model *m) { m->pos = 0; }
 void nro_model_set_freqs(nro_model *m, const float *freqs) {
@@ -414,7 +452,7 @@ static void acts_matmul_(nro_model *m, float *y, const uint8_t *w, int dt, const
 /* causal attention of one token at `pos` over layer l's cache (infer.rs:553-572) */
 static void attend_(nro_model *m, int l, size_t pos, const float *q, float *out) {
     size_t hd = (size_t)m->head_dim, gqa = (size_t)(m->n_heads / m->n_kv_heads);
-    float scale = 1.0f / sqrtf((float)hd);
+    float scale = m->att_scale;
     for (size_t h = 0; h < (size_t)m->n_heads; h++) {
         const float *qh = q + h * hd;
         size_t kvh = (h / gqa) * hd;
@@ -433,21 +471,32 @@ static void attend_(nro_model *m, int l, size_t pos, const float *q, float *out)
     }
 }
 
-/* InferCtx::forward (infer.rs:510-595), Llama recipe: no qk-norm, adjacent
- * rope, embed/residual/logit scales neutral (1.0). */
+/* Qwen3's per-head RMSNorm of q and k before rope (infer.rs:533-541) */
+static void qk_norm_(nro_model *m, int l, float *q, float *k) {
+    size_t hd = (size_t)m->head_dim;
+    if (!m->L[l].q_norm || !m->L[l].k_norm) return;
+    for (size_t h = 0; h < (size_t)m->n_heads; h++) nro_rmsnorm_inplace(q + h * hd, m->L[l].q_norm, hd, m->eps);
+    for (size_t h = 0; h < (size_t)m->n_kv_heads; h++) nro_rmsnorm_inplace(k + h * hd, m->L[l].k_norm, hd, m->eps);
+}
+
+/* InferCtx::forward (infer.rs:510-595), with the recipe: muP embedding scale,
+ * qk-norm, rope style, attention score scale, residual scale, logit scale. */
 const float *nro_model_forward(nro_model *m, uint32_t token) {
     size_t d = (size_t)m->dim, kvd = (size_t)m->kv_dim, ffn = (size_t)m->ffn_dim;
     size_t att_dim = (size_t)m->n_heads * m->head_dim;
     size_t pos = (size_t)m->pos;
     dequant_row_(m->embed, m->embed_dt, token, d, m->x);
+    if (m->embed_scale != 1.0f)
+        for (size_t i = 0; i < d; i++) m->x[i] *= m->embed_scale; /* vec.rs:61-65 */
     for (int l = 0; l < m->n_layers; l++) {
         nro_rmsnorm(m->xb, m->x, m->L[l].attn_norm, d, m->eps);
         /* matvec_group: all three weights share the activation quantized once */
         acts_matvec_(m, m->q, m->L[l].w[0], m->L[l].dt[0], m->xb, att_dim, d);
         acts_matvec_(m, m->k, m->L[l].w[1], m->L[l].dt[1], m->xb, kvd, d);
         acts_matvec_(m, m->v, m->L[l].w[2], m->L[l].dt[2], m->xb, kvd, d);
-        nro_rope_apply(m->q, att_dim, (size_t)m->head_dim, m->freqs, pos);
-        nro_rope_apply(m->k, kvd, (size_t)m->head_dim, m->freqs, pos);
+        qk_norm_(m, l, m->q, m->k);
+        nro_rope_apply_style(m->q, att_dim, (size_t)m->head_dim, m->freqs, pos, m->neox);
+        nro_rope_apply_style(m->k, kvd, (size_t)m->head_dim, m->freqs, pos, m->neox);
         size_t row = ((size_t)l * m->ctx + pos) * kvd;
         for (size_t i = 0; i < kvd; i++) {
             m->kc[row + i] = nro_f32_to_f16(m->k[i]);
@@ -455,16 +504,18 @@ const float *nro_model_forward(nro_model *m, uint32_t token) {
         }
         attend_(m, l, pos, m->q, m->attn_out);
         acts_matvec_(m, m->xb2, m->L[l].w[3], m->L[l].dt[3], m->attn_out, d, att_dim);
-        for (size_t i = 0; i < d; i++) m->x[i] += 1.0f * m->xb2[i]; /* saxpy, residual_scale 1 */
+        for (size_t i = 0; i < d; i++) m->x[i] += m->residual_scale * m->xb2[i]; /* saxpy, vec.rs:68-72 */
         nro_rmsnorm(m->xb, m->x, m->L[l].ffn_norm, d, m->eps);
         acts_matvec_(m, m->gate, m->L[l].w[4], m->L[l].dt[4], m->xb, ffn, d);
         acts_matvec_(m, m->up, m->L[l].w[5], m->L[l].dt[5], m->xb, ffn, d);
         nro_swiglu(m->gate, m->up, ffn);
         acts_matvec_(m, m->xb2, m->L[l].w[6], m->L[l].dt[6], m->gate, d, ffn);
-        for (size_t i = 0; i < d; i++) m->x[i] += 1.0f * m->xb2[i];
+        for (size_t i = 0; i < d; i++) m->x[i] += m->residual_scale * m->xb2[i];
     }
     nro_rmsnorm(m->xb, m->x, m->out_norm, d, m->eps);
     acts_matvec_(m, m->logits, m->output, m->output_dt, m->xb, (size_t)m->vocab, d);
+    if (m->logit_recip != 1.0f)
+        for (size_t i = 0; i < (size_t)m->vocab; i++) m->logits[i] *= m->logit_recip;
     m->pos += 1;
     return m->logits;
 }
@@ -475,7 +526,11 @@ const float *nro_model_prefill_chunk(nro_model *m, const uint32_t *tokens, int n
     size_t d = (size_t)m->dim, kvd = (size_t)m->kv_dim, ffn = (size_t)m->ffn_dim;
     size_t att_dim = (size_t)m->n_heads * m->head_dim;
     size_t b = (size_t)nb, base = (size_t)m->pos;
-    for (size_t i = 0; i < b; i++) dequant_row_(m->embed, m->embed_dt, tokens[i], d, m->bx + i * d);
+    for (size_t i = 0; i < b; i++) {
+        dequant_row_(m->embed, m->embed_dt, tokens[i], d, m->bx + i * d);
+        if (m->embed_scale != 1.0f)
+            for (size_t j = 0; j < d; j++) m->bx[i * d + j] *= m->embed_scale;
+    }
     for (int l = 0; l < m->n_layers; l++) {
         for (size_t i = 0; i < b; i++) nro_rmsnorm(m->bxb + i * d, m->bx + i * d, m->L[l].attn_norm, d, m->eps);
         acts_matmul_(m, m->bq, m->L[l].w[0], m->L[l].dt[0], m->bxb, att_dim, d, b);
@@ -483,8 +538,9 @@ const float *nro_model_prefill_chunk(nro_model *m, const uint32_t *tokens, int n
         acts_matmul_(m, m->bv, m->L[l].w[2], m->L[l].dt[2], m->bxb, kvd, d, b);
         for (size_t i = 0; i < b; i++) {
             size_t pos = base + i;
-            nro_rope_apply(m->bq + i * att_dim, att_dim, (size_t)m->head_dim, m->freqs, pos);
-            nro_rope_apply(m->bk + i * kvd, kvd, (size_t)m->head_dim, m->freqs, pos);
+            qk_norm_(m, l, m->bq + i * att_dim, m->bk + i * kvd);
+            nro_rope_apply_style(m->bq + i * att_dim, att_dim, (size_t)m->head_dim, m->freqs, pos, m->neox);
+            nro_rope_apply_style(m->bk + i * kvd, kvd, (size_t)m->head_dim, m->freqs, pos, m->neox);
             size_t row = ((size_t)l * m->ctx + pos) * kvd;
             for (size_t j = 0; j < kvd; j++) {
                 m->kc[row + j] = nro_f32_to_f16(m->bk[i * kvd + j]);
@@ -493,16 +549,18 @@ const float *nro_model_prefill_chunk(nro_model *m, const uint32_t *tokens, int n
         }
         for (size_t i = 0; i < b; i++) attend_(m, l, base + i, m->bq + i * att_dim, m->battn + i * att_dim);
         acts_matmul_(m, m->bxb, m->L[l].w[3], m->L[l].dt[3], m->battn, d, att_dim, b);
-        for (size_t i = 0; i < b * d; i++) m->bx[i] += 1.0f * m->bxb[i];
+        for (size_t i = 0; i < b * d; i++) m->bx[i] += m->residual_scale * m->bxb[i];
         for (size_t i = 0; i < b; i++) nro_rmsnorm(m->bxb + i * d, m->bx + i * d, m->L[l].ffn_norm, d, m->eps);
         acts_matmul_(m, m->bgate, m->L[l].w[4], m->L[l].dt[4], m->bxb, ffn, d, b);
         acts_matmul_(m, m->bup, m->L[l].w[5], m->L[l].dt[5], m->bxb, ffn, d, b);
         for (size_t i = 0; i < b; i++) nro_swiglu(m->bgate + i * ffn, m->bup + i * ffn, ffn);
         acts_matmul_(m, m->bxb, m->L[l].w[6], m->L[l].dt[6], m->bgate, d, ffn, b);
-        for (size_t i = 0; i < b * d; i++) m->bx[i] += 1.0f * m->bxb[i];
+        for (size_t i = 0; i < b * d; i++) m->bx[i] += m->residual_scale * m->bxb[i];
     }
     nro_rmsnorm(m->xb, m->bx + (b - 1) * d, m->out_norm, d, m->eps);
     acts_matvec_(m, m->logits, m->output, m->output_dt, m->xb, (size_t)m->vocab, d);
+    if (m->logit_recip != 1.0f)
+        for (size_t i = 0; i < (size_t)m->vocab; i++) m->logits[i] *= m->logit_recip;
     m->pos += nb;
     return m->logits;
 }

@@ -139,6 +139,11 @@ void nro_rope_apply(float *x, size_t n, size_t head_dim, const float *freqs, siz
 typedef struct nro_model nro_model;
 nro_model *nro_model_new(const int dims[8], float eps, float theta, int threads);
 void nro_model_free(nro_model *m);
+void nro_model_set_recipe(nro_model *m, int neox, float embed_scale, float attn_scale, float residual_scale,
+                          float logit_scale);
+void nro_model_set_qk_norm(nro_model *m, int l, const float *q_norm, const float *k_norm);
+void nro_rmsnorm_inplace(float *x, const float *w, size_t n, float eps);
+void nro_rope_apply_style(float *x, size_t n, size_t head_dim, const float *freqs, size_t pos, int neox);
 void nro_model_set_globals(nro_model *m, const void *embed, int embed_dt, const void *output, int output_dt,
                            const float *out_norm);
 void nro_model_set_layer(nro_model *m, int l, const void *const w[7], const int dt[7], const float *attn_norm,
