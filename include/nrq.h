@@ -168,6 +168,11 @@ int nrq_sync(void *stream);
 #define NRQ_TENSOR_FFN_GATE 16
 #define NRQ_TENSOR_FFN_UP 17
 #define NRQ_TENSOR_FFN_DOWN 18
+#define NRQ_TENSOR_ATTN_Q_NORM 19 /* Qwen3 per-head RMSNorm weights, f32[head_dim] */
+#define NRQ_TENSOR_ATTN_K_NORM 20
+
+#define NRQ_ROPE_ADJACENT 0 /* RopeStyle (rope.rs:37-44): pairs (2i, 2i+1), Llama / Granite */
+#define NRQ_ROPE_NEOX 1     /* pairs (i, i + head_dim/2), Qwen3 */
 
 typedef struct nrq_model nrq_model;
 
@@ -188,6 +193,15 @@ int nrq_model_set_tensor(nrq_model *m, int kind, int layer, int dtype, const voi
  * fills it from Llama-3 scaling or a RopeFreqs tensor (infer.rs:433-447).
  * nrq_model_create sets the unscaled theta^(-2i/head_dim). */
 int nrq_model_set_rope_freqs(nrq_model *m, const float *freqs, int n);
+/* The recipe InferCtx::new derives from the file (infer.rs:447-461;
+ * replaces its rope_style / embed_scale / att_score_scale / residual_scale /
+ * logit_recip fields): rope pairs, muP embedding scale, attention score scale
+ * (0 = 1/sqrtf(head_dim)), residual scale (x += s * branch) and logit scale
+ * (logits /= s, as * (1/s)). nrq_model_create sets the Llama recipe
+ * (NRQ_ROPE_ADJACENT, 1, 0, 1, 1). Qwen3's per-head q/k RMSNorm runs when a
+ * layer has NRQ_TENSOR_ATTN_Q_NORM and NRQ_TENSOR_ATTN_K_NORM. */
+int nrq_model_set_recipe(nrq_model *m, int rope_style, float embed_scale, float attn_scale, float residual_scale,
+                         float logit_scale);
 /* InferCtx::reset (infer.rs:494-496). */
 int nrq_model_reset(nrq_model *m);
 /* InferCtx::pos. */

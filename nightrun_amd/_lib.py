@@ -65,6 +65,7 @@ SIGNATURES = {
     "nrq_model_kv_cache": ([_vp, _vp, _vp, _sz], _i),
     "nrq_model_destroy": ([_vp], _i),
     "nrq_model_set_rope_freqs": ([_vp, _vp, _i], _i),
+    "nrq_model_set_recipe": ([_vp, _i, C.c_float, C.c_float, C.c_float, C.c_float], _i),
     "nrq_model_prefill": ([_vp, _vp, _i, _vp], _i),
     "nrq_model_set_sampler": ([_vp, C.c_float, C.c_float, C.c_uint64], _i),
     "nrq_model_sampler_state": ([_vp, C.POINTER(C.c_uint64)], _i),

@@ -65,6 +65,7 @@ struct NormMatvecLaunch {
   const float* norm_w;
   int n;
   float eps;
+  float rscale = 1.0f;  // x + rscale * add
   int nmat;
   const void* w[3];
   float* y[3];

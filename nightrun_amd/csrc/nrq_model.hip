@@ -159,7 +159,7 @@ enum { CTL_TOKEN = 0, CTL_POS = 1, CTL_STEP = 2, CTL_WORDS = 4 };
 // takes sincosf(pos * freq_i) for every head and layer alike (rope.rs:49-65).
 __global__ void embed_q8_0_kernel(const uint8_t* __restrict__ E, const int* __restrict__ ctl, int dim,
                                   float* __restrict__ x, const float* __restrict__ freqs, int half,
-                                  float* __restrict__ rope_cs) {
+                                  float* __restrict__ rope_cs, float escale) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (blockIdx.x == 0 && (int)threadIdx.x < half) {
     float sn, cs;
@@ -171,14 +171,16 @@ __global__ void embed_q8_0_kernel(const uint8_t* __restrict__ E, const int* __re
   const size_t tok = (size_t)(uint32_t)ctl[CTL_TOKEN];
   const uint8_t* blk = E + (tok * (dim / 32) + i / 32) * kQ8_0Bytes;
   const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-  x[i] = (float)(int8_t)blk[2 + (i & 31)] * d;
+  const float v = (float)(int8_t)blk[2 + (i & 31)] * d;
+  x[i] = escale != 1.0f ? v * escale : v;  // muP embedding scale (infer.rs:519-521)
 }
 
 // Prefill: the embedding rows of B tokens (x[i][:]) and each token's (cos, sin)
 // table at position base + i (base = ctl[CTL_POS]); grid (dim / 256, B).
 __global__ void embed_rows_q8_0_kernel(const uint8_t* __restrict__ E, const int* __restrict__ tokens,
                                        const int* __restrict__ ctl, int dim, float* __restrict__ x,
-                                       const float* __restrict__ freqs, int half, float* __restrict__ rope_cs) {
+                                       const float* __restrict__ freqs, int half, float* __restrict__ rope_cs,
+                                       float escale) {
   const int row = blockIdx.y;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (blockIdx.x == 0 && (int)threadIdx.x < half) {
@@ -191,14 +193,15 @@ __global__ void embed_rows_q8_0_kernel(const uint8_t* __restrict__ E, const int*
   const size_t tok = (size_t)(uint32_t)tokens[row];
   const uint8_t* blk = E + (tok * (dim / 32) + i / 32) * kQ8_0Bytes;
   const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-  x[(size_t)row * dim + i] = (float)(int8_t)blk[2 + (i & 31)] * d;
+  const float v = (float)(int8_t)blk[2 + (i & 31)] * d;
+  x[(size_t)row * dim + i] = escale != 1.0f ? v * escale : v;  // muP embedding scale (infer.rs:608-615)
 }
 
 constexpr int kNormNT = 256;
 constexpr int kNormMax = 8192;
 constexpr int kNormPT = kNormMax / kNormNT;  // values per thread
 
-// Optional residual x += 1.0 * add (vec.rs:63-67, residual_scale 1), then
+// Optional residual x += rs * add (saxpy, vec.rs:68-72; rs is residual_scale), then
 // rmsnorm (vec.rs:4-14): ss += v*v in element order, scale = 1/sqrtf(ss/n + eps),
 // out = x * scale * w. Writes out (f32) and, when xq != null, its Q8_0 blocks
 // (q8.rs:27-44). One workgroup; n <= kNormMax, a multiple of 256. Thread t
@@ -207,7 +210,7 @@ constexpr int kNormPT = kNormMax / kNormNT;  // values per thread
 // wave 0 runs the sequential sum of squares. Workgroup r takes row r of
 // [rows][n] x, add, out and xq (one row per workgroup in a prefill chunk).
 __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, const float* __restrict__ add,
-                                                       const float* __restrict__ w, int n, float eps,
+                                                       const float* __restrict__ w, int n, float eps, float rs,
                                                        float* __restrict__ out, uint8_t* __restrict__ xq) {
   __shared__ __align__(16) float sq[kNormMax];
   {
@@ -245,10 +248,10 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
         float4& p = v[2 * k + h];
         if (add) {
           const float4 q = a[2 * k + h];
-          p.x = p.x + 1.0f * q.x;
-          p.y = p.y + 1.0f * q.y;
-          p.z = p.z + 1.0f * q.z;
-          p.w = p.w + 1.0f * q.w;
+          p.x = p.x + rs * q.x;
+          p.y = p.y + rs * q.y;
+          p.z = p.z + rs * q.z;
+          p.w = p.w + rs * q.w;
           ((float4*)x)[2 * j + h] = p;
         }
         ((float4*)sq)[2 * j + h] = make_float4(p.x * p.x, p.y * p.y, p.z * p.z, p.w * p.w);
@@ -289,13 +292,20 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
 // Prefill: rope::apply (rope.rs:49-65) on every query and key head of token i
 // = blockIdx.x at position base + i, queries in place, and the f16 KV append of
 // its key and value rows (infer.rs:642-651). A chunk appends all its rows
-// before any of its tokens attends, as prefill_chunk does.
+// before any of its tokens attends, as prefill_chunk does. With qn/kn (Qwen3),
+// each head is first RMS-normalized in place (vec.rs:17-28, infer.rs:643-650):
+// its squares go to LDS, one thread per head sums them in element order, and
+// x * (scale * w) is applied as the pair is rotated. Pair j of a head is
+// (2j, 2j+1), or (j, j + hd/2) with neox. LDS: (n_heads + n_kv_heads) * (hd + 1)
+// floats with qn, else none.
 __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q, const float* __restrict__ k,
                                                           const float* __restrict__ v,
                                                           const float* __restrict__ rope_cs,
                                                           const int* __restrict__ ctl, int n_heads, int n_kv_heads,
                                                           int hd, int ctx, int layer, uint16_t* __restrict__ kc,
-                                                          uint16_t* __restrict__ vc) {
+                                                          uint16_t* __restrict__ vc, const float* __restrict__ qn,
+                                                          const float* __restrict__ kn, float eps, int neox) {
+  extern __shared__ __align__(16) float rsm[];
   const int i = blockIdx.x, half = hd / 2;
   const int pos = ctl[CTL_POS] + i;
   const float* cst = rope_cs + (size_t)i * hd;
@@ -306,19 +316,39 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q,
   auto kvi = [&](int g, int d) {
     return ((size_t)layer * n_kv_heads + g) * hd * ctx + (size_t)(d >> 3) * ctx8 + (size_t)pos * 8 + (d & 7);
   };
+  const int nq = n_heads * hd, nhh = n_heads + n_kv_heads;
+  float* hscale = rsm + (size_t)nhh * hd;  // per-head norm scale: q heads, then k heads
+  if (qn) {
+    for (int idx = threadIdx.x; idx < nq; idx += blockDim.x) rsm[idx] = qi[idx] * qi[idx];
+    for (int idx = threadIdx.x; idx < n_kv_heads * hd; idx += blockDim.x) rsm[nq + idx] = ki[idx] * ki[idx];
+    __syncthreads();
+    for (int t = threadIdx.x; t < nhh; t += blockDim.x)
+      hscale[t] = 1.0f / sqrtf(chain_sum(rsm + (size_t)t * hd, hd) / (float)hd + eps);
+    __syncthreads();
+  }
   for (int idx = threadIdx.x; idx < n_heads * half; idx += blockDim.x) {
     const int h = idx / half, j = idx % half;
+    const int ia = neox ? j : 2 * j, ib = neox ? j + half : 2 * j + 1;
     const float cs = cst[2 * j], sn = cst[2 * j + 1];
-    const float a = qi[(size_t)h * hd + 2 * j], b = qi[(size_t)h * hd + 2 * j + 1];
-    qi[(size_t)h * hd + 2 * j] = a * cs - b * sn;
-    qi[(size_t)h * hd + 2 * j + 1] = a * sn + b * cs;
+    float a = qi[(size_t)h * hd + ia], b = qi[(size_t)h * hd + ib];
+    if (qn) {
+      a = a * (hscale[h] * qn[ia]);
+      b = b * (hscale[h] * qn[ib]);
+    }
+    qi[(size_t)h * hd + ia] = a * cs - b * sn;
+    qi[(size_t)h * hd + ib] = a * sn + b * cs;
   }
   for (int idx = threadIdx.x; idx < n_kv_heads * half; idx += blockDim.x) {
     const int g = idx / half, j = idx % half;
+    const int ia = neox ? j : 2 * j, ib = neox ? j + half : 2 * j + 1;
     const float cs = cst[2 * j], sn = cst[2 * j + 1];
-    const float a = ki[(size_t)g * hd + 2 * j], b = ki[(size_t)g * hd + 2 * j + 1];
-    kc[kvi(g, 2 * j)] = (uint16_t)f32_to_f16_bits(a * cs - b * sn);
-    kc[kvi(g, 2 * j + 1)] = (uint16_t)f32_to_f16_bits(a * sn + b * cs);
+    float a = ki[(size_t)g * hd + ia], b = ki[(size_t)g * hd + ib];
+    if (qn) {
+      a = a * (hscale[n_heads + g] * kn[ia]);
+      b = b * (hscale[n_heads + g] * kn[ib]);
+    }
+    kc[kvi(g, ia)] = (uint16_t)f32_to_f16_bits(a * cs - b * sn);
+    kc[kvi(g, ib)] = (uint16_t)f32_to_f16_bits(a * sn + b * cs);
   }
   for (int idx = threadIdx.x; idx < n_kv_heads * hd; idx += blockDim.x) {
     const int g = idx / hd, d = idx % hd;
@@ -359,7 +389,7 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
     const float* __restrict__ q_in, const float* __restrict__ k_in, const float* __restrict__ v_in,
     const float* __restrict__ rope_cs, const int* __restrict__ ctl, int n_heads, int n_kv_heads, int ctx, int layer,
     float scale, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, float* __restrict__ out,
-    uint8_t* __restrict__ out_q8) {
+    uint8_t* __restrict__ out_q8, const float* __restrict__ qn, const float* __restrict__ kn, float eps, int neox) {
   constexpr int hd = HD, half = HD / 2, g8 = HD / 8;
   constexpr int C = (8192 / HD) & ~63 ? (8192 / HD) & ~63 : 64;  // positions per product chunk
   constexpr int CP = C + 4;
@@ -425,6 +455,53 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   }
   if (PF) {
     for (int i = tid; i < hd; i += kAttNT) qs[i] = q_in[(size_t)h * hd + i];
+  } else if (qn || neox) {
+    // Qwen3: the head's q and its KV head's k RMS-normalized (vec.rs:17-28,
+    // infer.rs:533-541; squares in the product stage, free until the scores),
+    // then rope with pair j = (j, j + hd/2) when neox; in LDS, in place.
+    for (int i = tid; i < hd; i += kAttNT) {
+      qs[i] = q_in[(size_t)h * hd + i];
+      kcur[i] = k_in[(size_t)g * hd + i];
+    }
+    __syncthreads();
+    if (qn) {
+      float* sqq = prod;
+      float* sqk = prod + hd;
+      for (int i = tid; i < hd; i += kAttNT) {
+        sqq[i] = qs[i] * qs[i];
+        sqk[i] = kcur[i] * kcur[i];
+      }
+      __syncthreads();
+      if (tid == 0) red[0] = 1.0f / sqrtf(chain_sum(sqq, hd) / (float)hd + eps);
+      if (tid == 64) red[1] = 1.0f / sqrtf(chain_sum(sqk, hd) / (float)hd + eps);
+      __syncthreads();
+      const float sq_ = red[0], sk_ = red[1];
+      for (int i = tid; i < hd; i += kAttNT) {
+        qs[i] = qs[i] * (sq_ * qn[i]);
+        kcur[i] = kcur[i] * (sk_ * kn[i]);
+      }
+      __syncthreads();
+    }
+    for (int i = tid; i < half; i += kAttNT) {
+      const int ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
+      const float cs = rope_cs[2 * i], sn = rope_cs[2 * i + 1];
+      const float qa = qs[ia], qb = qs[ib];
+      qs[ia] = qa * cs - qb * sn;
+      qs[ib] = qa * sn + qb * cs;
+      const float ka = kcur[ia], kb = kcur[ib];
+      const uint32_t k0 = f32_to_f16_bits(ka * cs - kb * sn), k1 = f32_to_f16_bits(ka * sn + kb * cs);
+      kcur[ia] = f16_bits_to_f32(k0);
+      kcur[ib] = f16_bits_to_f32(k1);
+      if (writer) {
+        kc[kvi(pos, ia)] = (uint16_t)k0;
+        kc[kvi(pos, ib)] = (uint16_t)k1;
+      }
+    }
+    for (int i = tid; i < hd; i += kAttNT) {
+      const uint32_t vb = f32_to_f16_bits(v_in[(size_t)g * hd + i]);
+      vcur[i] = f16_bits_to_f32(vb);
+      if (writer) vc[kvi(pos, i)] = (uint16_t)vb;
+    }
   } else {
   for (int i = tid; i < half; i += kAttNT) {
     const float cs = rope_cs[2 * i], sn = rope_cs[2 * i + 1];
@@ -740,6 +817,12 @@ __global__ __launch_bounds__(256) void swiglu_kernel(float* __restrict__ gate, c
   const float v = silu * up[i];
   gate[i] = v;
   if (xq) quant_q8_0_lane(v, threadIdx.x & 31, xq + (size_t)(i >> 5) * kQ8_0Bytes);
+}
+
+// scale_inplace (vec.rs:61-65): x[i] *= s
+__global__ void scale_kernel(float* __restrict__ x, int n, float s) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = x[i] * s;
 }
 
 constexpr int kArgNT = 1024;
@@ -1090,6 +1173,8 @@ struct Layer {
   Mat m[7];  // q, k, v, o, gate, up, down
   const float* attn_norm = nullptr;
   const float* ffn_norm = nullptr;
+  const float* q_norm = nullptr;  // Qwen3 per-head RMSNorm weights, head_dim each
+  const float* k_norm = nullptr;
 };
 
 size_t act_bytes(int dt, size_t n) { return dt == NRQ_Q8_0 ? n / 32 * 34 : n / 256 * 292; }
@@ -1127,6 +1212,9 @@ struct nrq_model {
   float samp_t = 0.0f, samp_p = 1.0f;
   unsigned long long* rng = nullptr;  // device word, seed | 1
   unsigned long long* samp_part = nullptr;  // the sampler's partial top-64 lists
+  // the recipe (infer.rs:447-461): Neox rope pairs, muP scalars
+  int rope_neox = 0;
+  float embed_scale = 1.0f, att_scale = 0.0f, res_scale = 1.0f, logit_recip = 1.0f;
 };
 
 namespace nrq {
@@ -1160,7 +1248,7 @@ int matvec(nrq_model* m, const Mat& w, const uint8_t* xq, float* y, int rows, in
 int norm_quant(nrq_model* m, float* xr, const float* add, const float* w, int dt) {
   const auto& c = m->cfg;
   hipLaunchKernelGGL(nrq::norm_kernel, dim3(1), dim3(nrq::kNormNT), 0, m->stream, xr, add, w, c.dim, c.norm_eps,
-                     m->xb, dt == NRQ_Q8_0 ? m->xq : nullptr);
+                     m->res_scale, m->xb, dt == NRQ_Q8_0 ? m->xq : nullptr);
   if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: norm launch failed");
   if (dt != NRQ_Q8_0) return quantize_for(m, dt, m->xb, c.dim, m->xq);
   return NRQ_OK;
@@ -1203,6 +1291,7 @@ int fused_norm_group(nrq_model* m, float** xr, float** xo, const float* add, con
   L.norm_w = normw;
   L.n = m->cfg.dim;
   L.eps = m->cfg.norm_eps;
+  L.rscale = m->res_scale;
   L.nmat = n;
   for (int i = 0; i < n; i++) {
     L.w[i] = ws[i]->w;
@@ -1218,14 +1307,23 @@ int fused_norm_group(nrq_model* m, float** xr, float** xo, const float* add, con
   return NRQ_OK;
 }
 
+// muP logit scale (infer.rs:589-591): logits *= 1/logit_scale when it is not 1
+int scale_logits(nrq_model* m) {
+  if (m->logit_recip == 1.0f) return NRQ_OK;
+  const int n = m->cfg.vocab;
+  hipLaunchKernelGGL(nrq::scale_kernel, dim3((n + 255) / 256), dim3(256), 0, m->stream, m->logits, n, m->logit_recip);
+  return hipGetLastError() == hipSuccess ? NRQ_OK : mfail(NRQ_ERR_DEVICE, "model: logit scale launch failed");
+}
+
 // One decode step, enqueued on m->stream (infer.rs:510-595 + argmax).
 int enqueue_step(nrq_model* m) {
   const auto& c = m->cfg;
   const int d = c.dim, kvd = m->kv_dim, att = m->att_dim, ffn = c.ffn_dim;
   hipLaunchKernelGGL(nrq::embed_q8_0_kernel, dim3((d + 255) / 256), dim3(256), 0, m->stream,
-                     (const uint8_t*)m->embed.w, m->ctl, d, m->x, m->freqs, c.head_dim / 2, m->rope_cs);
+                     (const uint8_t*)m->embed.w, m->ctl, d, m->x, m->freqs, c.head_dim / 2, m->rope_cs,
+                     m->embed_scale);
   if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: embed launch failed");
-  const float scale = 1.0f / sqrtf((float)c.head_dim);
+  const float scale = m->att_scale;
   const float* pending = nullptr;  // residual not yet added into *xr
   float* xr = m->x;                // the residual stream
   float* xo = m->x2;               // where a fused norm writes xr + pending
@@ -1252,7 +1350,7 @@ int enqueue_step(nrq_model* m) {
                                       : nrq::attention_kernel<128>;
       hipLaunchKernelGGL(kern, dim3(c.n_heads), dim3(nrq::kAttNT), m->att_lds, m->stream, m->q, m->k, m->v,
                          m->rope_cs, m->ctl, c.n_heads, c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->attn,
-                         q8 ? m->xq : nullptr);
+                         q8 ? m->xq : nullptr, Ly.q_norm, Ly.k_norm, c.norm_eps, m->rope_neox);
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: attention launch failed");
       if (!q8 && (rc = quantize_for(m, Ly.m[3].dt, m->attn, att, m->xq))) return rc;
     }
@@ -1285,6 +1383,7 @@ int enqueue_step(nrq_model* m) {
   }
   if ((rc = norm_quant(m, xr, pending, m->out_norm, m->output.dt))) return rc;
   if ((rc = matvec(m, m->output, m->xq, m->logits, c.vocab, d))) return rc;
+  if ((rc = scale_logits(m))) return rc;
   if (m->samp_t > 0.0f) {
     const int np = (c.vocab + nrq::kSelSlice - 1) / nrq::kSelSlice;
     hipLaunchKernelGGL(nrq::top64_part_kernel, dim3(np), dim3(nrq::kSelPartWaves * 64), 0, m->stream, m->logits,
@@ -1414,9 +1513,10 @@ int enqueue_prefill(nrq_model* m, int B) {
   const auto& c = m->cfg;
   const int d = c.dim, kvd = m->kv_dim, att = m->att_dim, ffn = c.ffn_dim;
   hipLaunchKernelGGL(nrq::embed_rows_q8_0_kernel, dim3((d + 255) / 256, B), dim3(256), 0, m->stream,
-                     (const uint8_t*)m->embed.w, m->btok, m->ctl, d, m->bx, m->freqs, c.head_dim / 2, m->brope);
+                     (const uint8_t*)m->embed.w, m->btok, m->ctl, d, m->bx, m->freqs, c.head_dim / 2, m->brope,
+                     m->embed_scale);
   if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: embed launch failed");
-  const float scale = 1.0f / sqrtf((float)c.head_dim);
+  const float scale = m->att_scale;
   const float* pending = nullptr;
   int rc;
   for (int l = 0; l < c.n_layers; l++) {
@@ -1427,12 +1527,14 @@ int enqueue_prefill(nrq_model* m, int B) {
       const int rows[3] = {att, kvd, kvd};
       const bool q8 = any_q8(ws, 3);
       hipLaunchKernelGGL(nrq::norm_kernel, dim3(B), dim3(nrq::kNormNT), 0, m->stream, m->bx, pending, Ly.attn_norm,
-                         d, c.norm_eps, m->bxn, q8 ? m->bxq : nullptr);
+                         d, c.norm_eps, m->res_scale, m->bxn, q8 ? m->bxq : nullptr);
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: norm launch failed");
       if ((rc = matmul_group_rows(m, ws, ys, rows, 3, m->bxn, d, B, q8))) return rc;
     }
-    hipLaunchKernelGGL(nrq::rope_append_kernel, dim3(B), dim3(256), 0, m->stream, m->bq, m->bk, m->bv, m->brope,
-                       m->ctl, c.n_heads, c.n_kv_heads, c.head_dim, c.ctx, l, m->kc, m->vc);
+    const size_t rlds = Ly.q_norm ? (size_t)(c.n_heads + c.n_kv_heads) * (c.head_dim + 1) * 4 : 0;
+    hipLaunchKernelGGL(nrq::rope_append_kernel, dim3(B), dim3(256), rlds, m->stream, m->bq, m->bk, m->bv, m->brope,
+                       m->ctl, c.n_heads, c.n_kv_heads, c.head_dim, c.ctx, l, m->kc, m->vc, Ly.q_norm, Ly.k_norm,
+                       c.norm_eps, m->rope_neox);
     if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: rope launch failed");
     {
       const bool q8 = Ly.m[3].dt == NRQ_Q8_0;
@@ -1448,7 +1550,7 @@ int enqueue_prefill(nrq_model* m, int B) {
                                         : nrq::attention_kernel<128, true>;
         hipLaunchKernelGGL(kern, dim3(c.n_heads, B), dim3(nrq::kAttNT), m->att_lds, m->stream, m->bq, m->bk, m->bv,
                            m->brope, m->ctl, c.n_heads, c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->battn,
-                           q8 ? m->bxq : nullptr);
+                           q8 ? m->bxq : nullptr, nullptr, nullptr, 0.0f, 0);
       }
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: attention launch failed");
       const Mat* ws[1] = {&Ly.m[3]};
@@ -1462,7 +1564,7 @@ int enqueue_prefill(nrq_model* m, int B) {
       const int rows[2] = {ffn, ffn};
       const bool q8 = any_q8(ws, 2);
       hipLaunchKernelGGL(nrq::norm_kernel, dim3(B), dim3(nrq::kNormNT), 0, m->stream, m->bx, m->bxb, Ly.ffn_norm, d,
-                         c.norm_eps, m->bxn, q8 ? m->bxq : nullptr);
+                         c.norm_eps, m->res_scale, m->bxn, q8 ? m->bxq : nullptr);
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: norm launch failed");
       if ((rc = matmul_group_rows(m, ws, ys, rows, 2, m->bxn, d, B, q8))) return rc;
     }
@@ -1483,7 +1585,8 @@ int enqueue_prefill(nrq_model* m, int B) {
   // residual add is never read
   const size_t last = (size_t)(B - 1) * d;
   if ((rc = norm_quant(m, m->bx + last, pending + last, m->out_norm, m->output.dt))) return rc;
-  return matvec(m, m->output, m->xq, m->logits, c.vocab, d);
+  if ((rc = matvec(m, m->output, m->xq, m->logits, c.vocab, d))) return rc;
+  return scale_logits(m);
 }
 
 int check_ready(nrq_model* m, const char* name) {
@@ -1494,7 +1597,11 @@ int check_ready(nrq_model* m, const char* name) {
     for (int i = 0; i < 7; i++)
       if (!Ly.m[i].w) return mfail(NRQ_ERR_ARG, "model: a layer matrix is not set");
     if (!Ly.attn_norm || !Ly.ffn_norm) return mfail(NRQ_ERR_ARG, "model: a layer norm is not set");
+    if (!Ly.q_norm != !Ly.k_norm) return mfail(NRQ_ERR_ARG, "model: attn_q_norm and attn_k_norm come as a pair");
   }
+  // the prefill rope kernel holds every head's squares in LDS
+  if (m->L[0].q_norm && (size_t)(m->cfg.n_heads + m->cfg.n_kv_heads) * (m->cfg.head_dim + 1) * 4 > 65536)
+    return mfail(NRQ_ERR_UNSUPPORTED, "model: too many heads for the qk-norm prefill kernel");
   (void)name;
   return NRQ_OK;
 }
@@ -1516,6 +1623,7 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
     return mfail(NRQ_ERR_UNSUPPORTED, "nrq_model_create: dim or context larger than the kernels' LDS buffers");
   nrq_model* m = new nrq_model();
   m->cfg = c;
+  m->att_scale = 1.0f / sqrtf((float)c.head_dim);  // infer.rs:455-459 without attn_scale
   m->kv_dim = c.n_kv_heads * c.head_dim;
   m->att_dim = c.n_heads * c.head_dim;
   m->maxd = std::max(std::max(c.dim, m->att_dim), c.ffn_dim);
@@ -1563,7 +1671,8 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
 
 int nrq_model_set_tensor(nrq_model* m, int kind, int layer, int dtype, const void* dev_ptr) {
   if (!m || !dev_ptr) return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: null argument");
-  const bool is_norm = kind == NRQ_TENSOR_ATTN_NORM || kind == NRQ_TENSOR_FFN_NORM || kind == NRQ_TENSOR_OUTPUT_NORM;
+  const bool is_norm = kind == NRQ_TENSOR_ATTN_NORM || kind == NRQ_TENSOR_FFN_NORM || kind == NRQ_TENSOR_OUTPUT_NORM ||
+                       kind == NRQ_TENSOR_ATTN_Q_NORM || kind == NRQ_TENSOR_ATTN_K_NORM;
   if (is_norm) {
     if (dtype != NRQ_F32) return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: norms are f32");
     if (((uintptr_t)dev_ptr & 15) != 0) return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: norm not 16-byte aligned");
@@ -1572,7 +1681,7 @@ int nrq_model_set_tensor(nrq_model* m, int kind, int layer, int dtype, const voi
       return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: unknown matrix dtype");
     if (((uintptr_t)dev_ptr & 15) != 0) return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: matrix not 16-byte aligned");
   }
-  const bool layered = kind >= NRQ_TENSOR_ATTN_NORM && kind <= NRQ_TENSOR_FFN_DOWN;
+  const bool layered = kind >= NRQ_TENSOR_ATTN_NORM && kind <= NRQ_TENSOR_ATTN_K_NORM;
   if (layered && (layer < 0 || layer >= m->cfg.n_layers))
     return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: layer out of range");
   const Mat mat{dev_ptr, dtype};
@@ -1593,9 +1702,35 @@ int nrq_model_set_tensor(nrq_model* m, int kind, int layer, int dtype, const voi
     case NRQ_TENSOR_FFN_GATE: m->L[layer].m[4] = mat; break;
     case NRQ_TENSOR_FFN_UP: m->L[layer].m[5] = mat; break;
     case NRQ_TENSOR_FFN_DOWN: m->L[layer].m[6] = mat; break;
+    case NRQ_TENSOR_ATTN_Q_NORM: m->L[layer].q_norm = (const float*)dev_ptr; break;
+    case NRQ_TENSOR_ATTN_K_NORM: m->L[layer].k_norm = (const float*)dev_ptr; break;
     default: return mfail(NRQ_ERR_ARG, "nrq_model_set_tensor: unknown tensor kind");
   }
   if (m->exec) {  // tensors changed: the captured step is stale
+    hipGraphExecDestroy(m->exec);
+    hipGraphDestroy(m->graph);
+    m->exec = nullptr;
+    m->graph = nullptr;
+  }
+  return NRQ_OK;
+}
+
+int nrq_model_set_recipe(nrq_model* m, int rope_style, float embed_scale, float attn_scale, float residual_scale,
+                         float logit_scale) {
+  if (!m) return mfail(NRQ_ERR_ARG, "nrq_model_set_recipe: null handle");
+  if (rope_style != NRQ_ROPE_ADJACENT && rope_style != NRQ_ROPE_NEOX)
+    return mfail(NRQ_ERR_ARG, "nrq_model_set_recipe: unknown rope style");
+  // the ranges Model::parse accepts for the muP scalars
+  if (!std::isfinite(embed_scale) || !std::isfinite(attn_scale) || attn_scale < 0.0f ||
+      !std::isfinite(residual_scale) || residual_scale <= 0.0f || !std::isfinite(logit_scale) || logit_scale <= 0.0f)
+    return mfail(NRQ_ERR_ARG, "nrq_model_set_recipe: muP scale out of range");
+  MHIP(hipStreamSynchronize(m->stream));
+  m->rope_neox = rope_style == NRQ_ROPE_NEOX;
+  m->embed_scale = embed_scale;
+  m->att_scale = attn_scale != 0.0f ? attn_scale : 1.0f / sqrtf((float)m->cfg.head_dim);
+  m->res_scale = residual_scale;
+  m->logit_recip = 1.0f / logit_scale;
+  if (m->exec) {  // the captured step holds the old scalars
     hipGraphExecDestroy(m->exec);
     hipGraphDestroy(m->graph);
     m->exec = nullptr;

@@ -588,14 +588,7 @@ int nrq_model_load_nrm(const nrq_nrm* f, int ctx, int flags, nrq_model** out) {
   *out = nullptr;
   const nrq_nrm_meta& M = f->meta;
   if (ctx <= 0) return perr(NRQ_ERR_ARG, "nrq_model_load_nrm: ctx must be positive");
-  // The device decode runs the Llama recipe: adjacent-pair rope, no qk-norm,
-  // neutral muP scalars (a Granite file with neutral scalars is the same math).
-  if (M.arch == NRQ_ARCH_QWEN3)
-    return perr(NRQ_ERR_UNSUPPORTED, "nrq_model_load_nrm: Qwen3 (qk-norm, NEOX rope) is not in the device recipe");
-  const float neutral_attn = 1.0f / sqrtf((float)M.head_dim);
-  if (M.embed_scale != 1.0f || !(M.attn_scale == 0.0f || M.attn_scale == neutral_attn) || M.residual_scale != 1.0f ||
-      M.logit_scale != 1.0f)
-    return perr(NRQ_ERR_UNSUPPORTED, "nrq_model_load_nrm: muP scales are not in the device recipe");
+  const bool qwen = M.arch == NRQ_ARCH_QWEN3;
   const uint32_t dim = M.dim, att = M.n_heads * M.head_dim, kvd = M.n_kv_heads * M.head_dim, ffn = M.ffn_dim;
   // InferCtx::new (infer.rs:378-431): every tensor present with its shape
   auto mat = [&](int kind, int layer, uint32_t rows, uint32_t cols, const nrq_nrm_tensor_info** e) {
@@ -622,10 +615,16 @@ int nrq_model_load_nrm(const nrq_nrm* f, int ctx, int flags, nrq_model** out) {
   int rc;
   if ((rc = mat(NRQ_TENSOR_TOK_EMBED, 0, M.vocab, dim, &e))) return rc;
   binds.push_back({NRQ_TENSOR_TOK_EMBED, 0, (int)e->dtype, e->offset});
-  if (has_kind(f, 19)) return missing("unexpected attn_q_norm for this arch");
+  if (!qwen && has_kind(f, NRQ_TENSOR_ATTN_Q_NORM)) return missing("unexpected attn_q_norm for this arch");
   for (uint32_t l = 0; l < M.n_layers; l++) {
     if ((rc = vecf(NRQ_TENSOR_ATTN_NORM, l, dim, &e))) return rc;
     binds.push_back({NRQ_TENSOR_ATTN_NORM, (int)l, NRQ_F32, e->offset});
+    if (qwen) {  // per-head q/k RMSNorm weights (infer.rs:393-402)
+      for (int kind : {NRQ_TENSOR_ATTN_Q_NORM, NRQ_TENSOR_ATTN_K_NORM}) {
+        if ((rc = vecf(kind, l, M.head_dim, &e))) return rc;
+        binds.push_back({kind, (int)l, NRQ_F32, e->offset});
+      }
+    }
     const struct {
       int kind;
       uint32_t rows, cols;
@@ -701,6 +700,12 @@ int nrq_model_load_nrm(const nrq_nrm* f, int ctx, int flags, nrq_model** out) {
       return rc;
     }
   if ((rc = nrq_model_set_rope_freqs(m, freqs.data(), (int)freqs.size()))) {
+    nrq_model_destroy(m);
+    return rc;
+  }
+  // the recipe (infer.rs:447-461): Neox pairs for Qwen3, the file's muP scalars
+  if ((rc = nrq_model_set_recipe(m, qwen ? NRQ_ROPE_NEOX : NRQ_ROPE_ADJACENT, M.embed_scale, M.attn_scale,
+                                 M.residual_scale, M.logit_scale))) {
     nrq_model_destroy(m);
     return rc;
   }

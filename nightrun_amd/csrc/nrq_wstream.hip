@@ -275,6 +275,7 @@ struct WsArgs {
   float* nx_out;
   const float* nw;
   float eps;
+  float rscale;  // the pending residual is added as x + rscale * add (saxpy, vec.rs:68-72)
   // gate|up pair (nmat == 2, equal rows, multiple of 32): workgroup w computes
   // rows 32w .. 32w+31 of both (waves 0-1 gate, 2-3 up) and writes the Q8_0
   // blocks of swiglu(gate, up) (vec.rs:45-52, q8.rs:27-44) instead of y
@@ -443,7 +444,7 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
           const float4 q0 = as4[2 * j], q1 = as4[2 * j + 1];
           const float b[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
-          for (int e = 0; e < 8; e++) a[e] = a[e] + 1.0f * b[e];
+          for (int e = 0; e < 8; e++) a[e] = a[e] + A.rscale * b[e];
           if (blockIdx.x == 0) {
             ((float4*)A.nx_out)[2 * j] = make_float4(a[0], a[1], a[2], a[3]);
             ((float4*)A.nx_out)[2 * j + 1] = make_float4(a[4], a[5], a[6], a[7]);
@@ -688,6 +689,7 @@ int launch_norm_matvec_q8_0(const NormMatvecLaunch& L) {
   A.nx_out = L.x_out;
   A.nw = L.norm_w;
   A.eps = L.eps;
+  A.rscale = L.rscale;
   A.swiglu_q8 = L.swiglu_q8;
   const bool urm = ws_u_rowmajor(bpr);
   if (L.swiglu_q8)

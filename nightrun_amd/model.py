@@ -21,6 +21,8 @@ from . import _lib
 # TensorKind ids (crates/nr-model/src/format.rs:53-69)
 TOK_EMBED, OUTPUT_NORM, OUTPUT = 1, 2, 3
 ATTN_NORM, ATTN_Q, ATTN_K, ATTN_V, ATTN_O, FFN_NORM, FFN_GATE, FFN_UP, FFN_DOWN = 10, 11, 12, 13, 14, 15, 16, 17, 18
+ATTN_Q_NORM, ATTN_K_NORM = 19, 20  # TensorKind (format.rs:53-69)
+ROPE_ADJACENT, ROPE_NEOX = 0, 1
 F32 = 0
 LAYER_KINDS = {"wq": ATTN_Q, "wk": ATTN_K, "wv": ATTN_V, "wo": ATTN_O, "w_gate": FFN_GATE, "w_up": FFN_UP,
                "w_down": FFN_DOWN}
@@ -43,6 +45,10 @@ class Model:
         h = C.c_void_p()
         _lib.check(_lib.lib().nrq_model_create(C.byref(c), C.byref(h)))
         self.h = h
+        r = cfg.get("recipe")
+        if r:  # Qwen3 / Granite (infer.rs:447-461)
+            self.set_recipe(ROPE_NEOX if r.get("rope") == "neox" else ROPE_ADJACENT, r.get("embed_scale", 1.0),
+                            r.get("attn_scale", 0.0), r.get("residual_scale", 1.0), r.get("logit_scale", 1.0))
         self._keep = []  # device tensors the model points at
 
     @classmethod
@@ -86,6 +92,16 @@ class Model:
             self._bind(FFN_NORM, l, F32, lw["ffn_norm"])
             for name, kind in LAYER_KINDS.items():
                 self._bind(kind, l, lw["dtypes"][name], lw[name])
+            if "q_norm" in lw:  # Qwen3 (infer.rs:393-404)
+                self._bind(ATTN_Q_NORM, l, F32, lw["q_norm"])
+                self._bind(ATTN_K_NORM, l, F32, lw["k_norm"])
+
+    def set_recipe(self, rope_style: int, embed_scale: float = 1.0, attn_scale: float = 0.0,
+                   residual_scale: float = 1.0, logit_scale: float = 1.0) -> None:
+        """The recipe InferCtx::new takes from the file (infer.rs:447-461): rope
+        pairs, muP embedding / attention-score / residual / logit scales."""
+        _lib.check(_lib.lib().nrq_model_set_recipe(self.h, rope_style, embed_scale, attn_scale, residual_scale,
+                                                   logit_scale))
 
     @property
     def pos(self) -> int:

@@ -216,7 +216,8 @@ def tiny() -> bytearray:
 
 
 def model_tensors(cfg: dict, weights: dict, tied: bool = True, rope_factors=None):
-    """The tensor list of a Llama-recipe model in the oracle's weight dict (gen_model's layout)."""
+    """The tensor list of a model in the oracle's weight dict (gen_model's layout),
+    with Qwen3's per-head q/k norms when its layers carry them."""
     import numpy as np
 
     d, att, kvd, ffn = cfg["dim"], cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"], cfg["ffn_dim"]
@@ -231,6 +232,9 @@ def model_tensors(cfg: dict, weights: dict, tied: bool = True, rope_factors=None
         t.append((ROPE_FREQS, 0, F32, 1, cfg["head_dim"] // 2, raw(np.asarray(rope_factors, np.float32))))
     for l, lw in enumerate(weights["layers"]):
         t.append((ATTN_NORM, l, F32, 1, d, raw(lw["attn_norm"])))
+        if "q_norm" in lw:
+            t.append((ATTN_Q_NORM, l, F32, 1, cfg["head_dim"], raw(lw["q_norm"])))
+            t.append((ATTN_K_NORM, l, F32, 1, cfg["head_dim"], raw(lw["k_norm"])))
         t.append((FFN_NORM, l, F32, 1, d, raw(lw["ffn_norm"])))
         for name, (kind, rows, cols) in shapes.items():
             t.append((kind, l, lw["dtypes"][name], rows, cols, raw(lw[name])))

@@ -257,3 +257,60 @@ def test_prefill_context_exhausted_panics(gpu, oracle):
         assert m.pos == 30
     finally:
         m.close()
+
+
+# ---- the Qwen3 / Granite recipe (infer.rs:383-461): qk-norm, Neox rope, muP ----------
+
+MUP = dict(embed_scale=1.6, attn_scale=0.3, residual_scale=0.6, logit_scale=2.5)
+QWEN_HD64 = dict(TINY, rope_theta=10000.0, recipe=dict(rope="neox", **MUP))
+QWEN_HD128 = dict(dim=512, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=128, ffn_dim=512, vocab=1000,
+                  norm_eps=1e-6, rope_theta=1000000.0, recipe=dict(rope="neox"))
+GRANITE = dict(TINY, recipe=dict(rope="adjacent", embed_scale=12.0, attn_scale=0.0, residual_scale=0.22,
+                                 logit_scale=8.0))
+
+
+@pytest.mark.parametrize("cfg", [QWEN_HD64, QWEN_HD128], ids=["hd64-mup", "hd128"])
+@pytest.mark.parametrize("prefill", [False, True], ids=["decode", "prefill"])
+def test_qwen3_recipe_matches_oracle(gpu, oracle, cfg, prefill):
+    """Per-head q/k RMSNorm before Neox rope, in the decode attention kernel
+    and in the prefill rope kernel; with muP scalars on the head_dim 64 model.
+    70 prompt tokens cross a prefill chunk boundary."""
+    w = oracle.gen_model(cfg, 606, qk_norm=True)
+    prompt = np.random.default_rng(606).integers(0, cfg["vocab"], 70).astype(np.uint32)
+    run_pair(oracle, cfg, w, 128, prompt, 10, prefill=prefill)
+
+
+def test_granite_recipe_kquant_matches_oracle(gpu, oracle):
+    """Adjacent rope and muP scalars with Q4_K/Q6_K layers: the residual scale
+    goes through the standalone norm kernel (the fused norm takes Q8_0 only)."""
+    w = oracle.gen_model(GRANITE, 707)
+    shapes = oracle.layer_shapes(GRANITE)
+    for l, lw in enumerate(w["layers"]):
+        for i, name in enumerate(oracle.LAYER_MATS):
+            dt = 3 if name == "w_down" else 2
+            rows, cols = shapes[name]
+            lw[name] = oracle.gen_weights(dt, 2777 + 16 * l + i, rows, cols)
+            lw["dtypes"][name] = dt
+    prompt = np.random.default_rng(707).integers(0, GRANITE["vocab"], 40).astype(np.uint32)
+    run_pair(oracle, GRANITE, w, 96, prompt, 8)
+    run_pair(oracle, GRANITE, w, 96, prompt, 8, prefill=True)
+
+
+def test_recipe_rejects_bad_scales_and_unpaired_norms(gpu, oracle):
+    """nrq_model_set_recipe takes the ranges Model::parse accepts; a layer with
+    attn_q_norm but no attn_k_norm is refused at the first step."""
+    from nightrun_amd import NrqError
+    from nightrun_amd.model import ATTN_Q_NORM, F32, ROPE_NEOX, Model
+
+    m = Model(TINY, 32)
+    try:
+        for bad in ((7, 1.0, 0.0, 1.0, 1.0), (ROPE_NEOX, 1.0, -0.5, 1.0, 1.0), (ROPE_NEOX, 1.0, 0.0, 0.0, 1.0),
+                    (ROPE_NEOX, float("nan"), 0.0, 1.0, 1.0), (ROPE_NEOX, 1.0, 0.0, 1.0, 0.0)):
+            with pytest.raises(NrqError, match="rope style|out of range"):
+                m.set_recipe(*bad)
+        m.set_weights(oracle.gen_model(TINY, 808))
+        m._bind(ATTN_Q_NORM, 0, F32, np.ones(TINY["head_dim"], np.float32))
+        with pytest.raises(NrqError, match="pair"):
+            m.forward(1)
+    finally:
+        m.close()

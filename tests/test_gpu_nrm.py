@@ -171,6 +171,31 @@ def test_load_rope_freqs_tensor(gpu, oracle):
     decode_pair(oracle, TINY, w, bytes(blob), 64, prompt, 6, freqs=freqs)
 
 
+def test_load_qwen3_model_with_mup_scales(gpu, oracle):
+    """Qwen3 (per-head q/k RMSNorm tensors, Neox rope) with non-neutral muP
+    scalars in the header: the loader sets the recipe InferCtx::new derives
+    (infer.rs:383-461)."""
+    mup = dict(embed_scale=1.6, attn_scale=0.3, residual_scale=0.6, logit_scale=2.5)
+    cfg = dict(TINY, rope_theta=10000.0, recipe=dict(rope="neox", **mup))
+    w = oracle.gen_model(cfg, 36, qk_norm=True)
+    meta = ON.default_meta(**TINY, **mup, flags=ON.FLAG_TIED_EMBEDDINGS, arch=ON.ARCH_QWEN3)
+    meta["rope_theta"] = 10000.0
+    blob = ON.write(meta, ON.model_tensors(cfg, w, tied=True))
+    prompt = np.random.default_rng(36).integers(0, TINY["vocab"], 17).astype(np.uint32)
+    decode_pair(oracle, cfg, w, bytes(blob), 64, prompt, 8)
+
+
+def test_load_granite_model_with_mup_scales(gpu, oracle):
+    """Granite: adjacent rope, no qk-norm, muP scalars (attn_scale 0 = 1/sqrt(head_dim))."""
+    mup = dict(embed_scale=12.0, attn_scale=0.0, residual_scale=0.22, logit_scale=8.0)
+    cfg = dict(TINY, recipe=dict(rope="adjacent", **mup))
+    w = oracle.gen_model(cfg, 37)
+    meta = ON.default_meta(**TINY, **mup, flags=ON.FLAG_TIED_EMBEDDINGS, arch=ON.ARCH_GRANITE)
+    blob = ON.write(meta, ON.model_tensors(cfg, w, tied=True))
+    prompt = np.random.default_rng(37).integers(0, TINY["vocab"], 11).astype(np.uint32)
+    decode_pair(oracle, cfg, w, bytes(blob), 64, prompt, 8)
+
+
 def test_load_rejects_corrupt_data(gpu, oracle):
     from nightrun_amd import nrm
 
@@ -208,5 +233,6 @@ def test_load_reports_missing_and_misshapen_tensors(gpu, oracle):
     qn = full + [(ON.ATTN_Q_NORM, 0, ON.F32, 1, TINY["head_dim"], bytes(4 * TINY["head_dim"]))]
     with pytest.raises(nrm.ParseError, match="unexpected attn_q_norm"):
         nrm.NrmFile(bytes(ON.write(meta, qn))).load(64)
-    with pytest.raises(NrqError, match="Qwen3"):
+    with pytest.raises(nrm.ParseError, match="attn_q_norm") as e:  # Qwen3 needs its qk-norm tensors
         nrm.NrmFile(bytes(ON.write({**meta, "arch": ON.ARCH_QWEN3}, full))).load(64)
+    assert e.value.variant == "MissingTensor"
