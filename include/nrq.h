@@ -186,8 +186,9 @@ typedef struct {
 int nrq_model_create(const nrq_model_config *cfg, nrq_model **out);
 /* Binds one tensor already in HBM (matrices Q8_0/Q4_K/Q6_K in their block
  * layout; norms NRQ_F32; every tensor 16-byte aligned). The output head is tied to the
- * embedding until an NRQ_TENSOR_OUTPUT is set (infer.rs:415-419). The
- * embedding must be Q8_0. */
+ * embedding until an NRQ_TENSOR_OUTPUT is set (infer.rs:415-419). A Q4_K or
+ * Q6_K embedding needs dim % 256 == 0; its rows are dequantized as
+ * QMat::dequant_row does (infer.rs:36-56). */
 int nrq_model_set_tensor(nrq_model *m, int kind, int layer, int dtype, const void *dev_ptr);
 /* Replaces the rope table (n = head_dim / 2 host floats), as InferCtx::new
  * fills it from Llama-3 scaling or a RopeFreqs tensor (infer.rs:433-447).

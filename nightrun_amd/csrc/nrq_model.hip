@@ -154,10 +154,55 @@ enum { CTL_TOKEN = 0, CTL_POS = 1, CTL_STEP = 2, CTL_WORDS = 4 };
 
 // ---- kernels ------------------------------------------------------------------------
 
+// QMat::dequant_row (infer.rs:36-56), element i of row `row` (cols values):
+//  Q8_0 (q8.rs:47-55): f32(q) * d;
+//  Q4_K (kquant.rs:95-116): element 64c + k takes the low nibble of qs[32c + k]
+//    with scale/min pair 2c when k < 32, else the high nibble of qs[32c + k - 32]
+//    with pair 2c + 1: (d * sc) * q - dmin * m;
+//  Q6_K (kquant.rs:118-142): in half h, element 32p + l takes plane p of
+//    (ql, qh) at l: (d * sc[8h + l/16 + 2p]) * (q - 32).
+__device__ inline float dequant_elem(const uint8_t* __restrict__ E, int dt, size_t row, int cols, int i) {
+  if (dt == NRQ_Q4_K || dt == NRQ_Q6_K) {
+    const size_t b = row * (size_t)(cols / 256) + (size_t)(i >> 8);
+    const int e = i & 255;
+    if (dt == NRQ_Q4_K) {
+      const uint8_t* blk = E + b * 144;
+      const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+      const float dmin = f16_bits_to_f32((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+      const uint8_t* sc = blk + 4;
+      const int c = e >> 6, k = e & 63, j = 2 * c + (k >> 5);
+      uint32_t s, m;
+      if (j < 4) {
+        s = sc[j] & 63;
+        m = sc[j + 4] & 63;
+      } else {
+        s = (sc[j + 4] & 0x0F) | ((sc[j - 4] >> 6) << 4);
+        m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+      }
+      const uint32_t qq = blk[16 + 32 * c + (k & 31)];
+      const uint32_t q = k < 32 ? (qq & 0x0F) : (qq >> 4);
+      const float d1 = d * (float)s, min1 = dmin * (float)m;
+      return d1 * (float)q - min1;
+    }
+    const uint8_t* blk = E + b * 210;
+    const int h = e >> 7, r = e & 127, p = r >> 5, l = r & 31;
+    const uint8_t* ql = blk + 64 * h;
+    const uint32_t qh = blk[128 + 32 * h + l];
+    const uint32_t lo = (p & 1) ? ql[l + 32] : ql[l];
+    const int q = (int)(((p & 2) ? (lo >> 4) : (lo & 0x0F)) | (((qh >> (2 * p)) & 3) << 4)) - 32;
+    const float d = f16_bits_to_f32((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+    const float sc = (float)(int8_t)blk[192 + 8 * h + (l >> 4) + 2 * p];
+    return d * sc * (float)q;
+  }
+  const uint8_t* blk = E + (row * (size_t)(cols / 32) + (size_t)(i >> 5)) * kQ8_0Bytes;
+  const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+  return (float)(int8_t)blk[2 + (i & 31)] * d;
+}
+
 // QMat::dequant_row for Q8_0 (infer.rs:37-42, q8.rs:47-55): x[i] = f32(q) * d
 // Workgroup 0 also writes (cos, sin) of pos * freqs[i] for the step: rope::apply
 // takes sincosf(pos * freq_i) for every head and layer alike (rope.rs:49-65).
-__global__ void embed_q8_0_kernel(const uint8_t* __restrict__ E, const int* __restrict__ ctl, int dim,
+__global__ void embed_kernel(const uint8_t* __restrict__ E, int dt, const int* __restrict__ ctl, int dim,
                                   float* __restrict__ x, const float* __restrict__ freqs, int half,
                                   float* __restrict__ rope_cs, float escale) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -168,16 +213,13 @@ __global__ void embed_q8_0_kernel(const uint8_t* __restrict__ E, const int* __re
     rope_cs[2 * threadIdx.x + 1] = sn;
   }
   if (i >= dim) return;
-  const size_t tok = (size_t)(uint32_t)ctl[CTL_TOKEN];
-  const uint8_t* blk = E + (tok * (dim / 32) + i / 32) * kQ8_0Bytes;
-  const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-  const float v = (float)(int8_t)blk[2 + (i & 31)] * d;
+  const float v = dequant_elem(E, dt, (size_t)(uint32_t)ctl[CTL_TOKEN], dim, i);
   x[i] = escale != 1.0f ? v * escale : v;  // muP embedding scale (infer.rs:519-521)
 }
 
 // Prefill: the embedding rows of B tokens (x[i][:]) and each token's (cos, sin)
 // table at position base + i (base = ctl[CTL_POS]); grid (dim / 256, B).
-__global__ void embed_rows_q8_0_kernel(const uint8_t* __restrict__ E, const int* __restrict__ tokens,
+__global__ void embed_rows_kernel(const uint8_t* __restrict__ E, int dt, const int* __restrict__ tokens,
                                        const int* __restrict__ ctl, int dim, float* __restrict__ x,
                                        const float* __restrict__ freqs, int half, float* __restrict__ rope_cs,
                                        float escale) {
@@ -190,10 +232,7 @@ __global__ void embed_rows_q8_0_kernel(const uint8_t* __restrict__ E, const int*
     rope_cs[(size_t)row * 2 * half + 2 * threadIdx.x + 1] = sn;
   }
   if (i >= dim) return;
-  const size_t tok = (size_t)(uint32_t)tokens[row];
-  const uint8_t* blk = E + (tok * (dim / 32) + i / 32) * kQ8_0Bytes;
-  const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-  const float v = (float)(int8_t)blk[2 + (i & 31)] * d;
+  const float v = dequant_elem(E, dt, (size_t)(uint32_t)tokens[row], dim, i);
   x[(size_t)row * dim + i] = escale != 1.0f ? v * escale : v;  // muP embedding scale (infer.rs:608-615)
 }
 
@@ -1319,8 +1358,8 @@ int scale_logits(nrq_model* m) {
 int enqueue_step(nrq_model* m) {
   const auto& c = m->cfg;
   const int d = c.dim, kvd = m->kv_dim, att = m->att_dim, ffn = c.ffn_dim;
-  hipLaunchKernelGGL(nrq::embed_q8_0_kernel, dim3((d + 255) / 256), dim3(256), 0, m->stream,
-                     (const uint8_t*)m->embed.w, m->ctl, d, m->x, m->freqs, c.head_dim / 2, m->rope_cs,
+  hipLaunchKernelGGL(nrq::embed_kernel, dim3((d + 255) / 256), dim3(256), 0, m->stream,
+                     (const uint8_t*)m->embed.w, m->embed.dt, m->ctl, d, m->x, m->freqs, c.head_dim / 2, m->rope_cs,
                      m->embed_scale);
   if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: embed launch failed");
   const float scale = m->att_scale;
@@ -1512,8 +1551,9 @@ bool any_q8(const Mat* const* ws, int n) {
 int enqueue_prefill(nrq_model* m, int B) {
   const auto& c = m->cfg;
   const int d = c.dim, kvd = m->kv_dim, att = m->att_dim, ffn = c.ffn_dim;
-  hipLaunchKernelGGL(nrq::embed_rows_q8_0_kernel, dim3((d + 255) / 256, B), dim3(256), 0, m->stream,
-                     (const uint8_t*)m->embed.w, m->btok, m->ctl, d, m->bx, m->freqs, c.head_dim / 2, m->brope,
+  hipLaunchKernelGGL(nrq::embed_rows_kernel, dim3((d + 255) / 256, B), dim3(256), 0, m->stream,
+                     (const uint8_t*)m->embed.w, m->embed.dt, m->btok, m->ctl, d, m->bx, m->freqs, c.head_dim / 2,
+                     m->brope,
                      m->embed_scale);
   if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: embed launch failed");
   const float scale = m->att_scale;
@@ -1687,7 +1727,8 @@ int nrq_model_set_tensor(nrq_model* m, int kind, int layer, int dtype, const voi
   const Mat mat{dev_ptr, dtype};
   switch (kind) {
     case NRQ_TENSOR_TOK_EMBED:
-      if (dtype != NRQ_Q8_0) return mfail(NRQ_ERR_UNSUPPORTED, "nrq_model_set_tensor: embedding must be Q8_0");
+      if (dtype != NRQ_Q8_0 && m->cfg.dim % 256)
+        return mfail(NRQ_ERR_SHAPE, "nrq_model_set_tensor: a K-quant embedding needs dim % 256 == 0");
       m->embed = mat;
       if (!m->output.w) m->output = mat;  // tied head until an output tensor is set
       break;

@@ -314,3 +314,16 @@ def test_recipe_rejects_bad_scales_and_unpaired_norms(gpu, oracle):
             m.forward(1)
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("edt", [2, 3], ids=["q4k", "q6k"])
+def test_kquant_embedding_matches_oracle(gpu, oracle, edt):
+    """A Q4_K or Q6_K token embedding (QMat::dequant_row, infer.rs:36-56,
+    kquant.rs:95-142), tied to the head: every element of the dequantized row
+    feeds the first norm, so decode and prefill logits pin the element maps."""
+    w = oracle.gen_model(TINY, 909 + edt)
+    w["embed"] = oracle.gen_weights(edt, 9090 + edt, TINY["vocab"], TINY["dim"])
+    w["embed_dtype"] = edt
+    prompt = np.random.default_rng(edt).integers(0, TINY["vocab"], 30).astype(np.uint32)
+    run_pair(oracle, TINY, w, 64, prompt, 6)
+    run_pair(oracle, TINY, w, 64, prompt, 6, prefill=True)
