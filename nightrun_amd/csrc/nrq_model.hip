@@ -1047,20 +1047,49 @@ __device__ inline unsigned long long wave_sorted64(const uint32_t (&k)[E], const
   return sc[lane];
 }
 
-// The 64 largest of two sorted lists (lane l holds each one's l-th largest),
-// sorted: max(a_l, b_{63-l}) is bitonic and holds the 64 largest of the union;
-// a bitonic merge orders it.
-__device__ inline unsigned long long merge64(unsigned long long a, unsigned long long b) {
+// The value of lane l ^ J, by VALU cross-lane moves: DPP within a 16-lane row
+// (quad_perm for J = 1, 2; row_shl / row_shr by 4 for J = 4; row_ror:8 for
+// J = 8), v_permlane16_swap / v_permlane32_swap across rows (J = 16, 32).
+template <int J>
+__device__ inline uint32_t lane_xor(uint32_t v) {
   const int lane = threadIdx.x & 63;
-  const unsigned long long rb = __shfl(b, 63 - lane);
-  unsigned long long c = a > rb ? a : rb;
-#pragma unroll
-  for (int j = 32; j > 0; j >>= 1) {
-    const unsigned long long o = __shfl_xor(c, j);
-    const bool keep_max = (lane & j) == 0;
-    c = keep_max ? (c > o ? c : o) : (c < o ? c : o);
+  if constexpr (J == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return lane < 32 ? r[1] : r[0];
+  } else if constexpr (J == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else if constexpr (J == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x128, 0xf, 0xf, false);  // row_ror:8
+  } else if constexpr (J == 4) {
+    const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x104, 0xf, 0xf, false);  // row_shl:4
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    return (lane & 4) ? dn : up;
+  } else if constexpr (J == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+  } else {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
   }
-  return c;
+}
+
+template <int J>
+__device__ inline unsigned long long bitonic_stage(unsigned long long c) {
+  const uint32_t lo = lane_xor<J>((uint32_t)c), hi = lane_xor<J>((uint32_t)(c >> 32));
+  const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+  return ((threadIdx.x & J) == 0) ? (c > o ? c : o) : (c < o ? c : o);
+}
+
+// The 64 largest of two sorted lists, sorted: lane l holds a's l-th largest
+// and b's (63-l)-th (b read in reverse lane order). max(a_l, b_{63-l}) is
+// bitonic and holds the 64 largest of the union; a bitonic merge orders it.
+__device__ inline unsigned long long merge64(unsigned long long a, unsigned long long b_rev) {
+  unsigned long long c = a > b_rev ? a : b_rev;
+  c = bitonic_stage<32>(c);
+  c = bitonic_stage<16>(c);
+  c = bitonic_stage<8>(c);
+  c = bitonic_stage<4>(c);
+  c = bitonic_stage<2>(c);
+  return bitonic_stage<1>(c);
 }
 
 // First half of Sampler::sample (sample.rs:38-61) for temperature > 0: each
@@ -1087,7 +1116,7 @@ __global__ __launch_bounds__(kSelPartWaves * 64) void top64_part_kernel(const fl
 #pragma unroll
   for (int h = kSelPartWaves / 2; h >= 1; h >>= 1) {
     if (w < h) {
-      c = merge64(c, sc[w + h][lane]);
+      c = merge64(c, sc[w + h][63 - lane]);
       sc[w][lane] = c;
     }
     __syncthreads();
@@ -1114,14 +1143,16 @@ __global__ __launch_bounds__(kSelWaves * 64) void top64_sample_kernel(
     int max_out, uint32_t* __restrict__ token) {
   __shared__ unsigned long long sc[kSelWaves][kTopK];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  // list q, or an empty one past the last (clamped loads, four in flight)
-  auto list = [&](int q) {
-    const unsigned long long c = part[(size_t)min(q, nparts - 1) * kTopK + lane];
+  // list q (lane order l, or reversed), or an empty one past the last
+  // (clamped loads, four in flight)
+  auto list = [&](int q, int l) {
+    const unsigned long long c = part[(size_t)min(q, nparts - 1) * kTopK + l];
     return q < nparts ? c : 0ull;
   };
-  unsigned long long c = list(w);
+  unsigned long long c = list(w, lane);
   for (int q = w + kSelWaves; q < nparts; q += 3 * kSelWaves) {
-    const unsigned long long l1 = list(q), l2 = list(q + kSelWaves), l3 = list(q + 2 * kSelWaves);
+    const int rl = 63 - lane;
+    const unsigned long long l1 = list(q, rl), l2 = list(q + kSelWaves, rl), l3 = list(q + 2 * kSelWaves, rl);
     c = merge64(c, l1);
     if (q + kSelWaves < nparts) c = merge64(c, l2);
     if (q + 2 * kSelWaves < nparts) c = merge64(c, l3);
@@ -1131,7 +1162,7 @@ __global__ __launch_bounds__(kSelWaves * 64) void top64_sample_kernel(
 #pragma unroll
   for (int h = kSelWaves / 2; h >= 1; h >>= 1) {
     if (w < h) {
-      c = merge64(c, sc[w + h][lane]);
+      c = merge64(c, sc[w + h][63 - lane]);
       sc[w][lane] = c;
     }
     __syncthreads();
