@@ -128,3 +128,27 @@ def test_device_sampler_ties_at_the_top(gpu, oracle):
                 got = sample(dev, T, top_p, st)
                 assert got == want, (ci, T, top_p, d, got, want)
                 assert int(st.cpu().numpy().view(np.uint64)[0]) == ref.rng.value
+
+
+@pytest.mark.parametrize("n", [1, 2, 63, 64, 65, 2047, 2048, 2049, 4097])
+def test_device_sampler_slice_boundaries(gpu, oracle, n):
+    """Vocabulary sizes around the selection kernels' units: one logit, fewer
+    or more than the 64 candidates, a first-kernel slice of 2048 logits plus
+    or minus one (partial workgroups, empty waves, one-list merges)."""
+    import torch
+
+    from nightrun_amd.model import sample
+
+    logits = np.random.default_rng(n).normal(0, 1.5, n).astype(np.float32)
+    if not boundary_untied(logits):
+        pytest.skip("64th and 65th largest tie")
+    dev = torch.from_numpy(logits).cuda()
+    for T, top_p in [(0.7, 0.9), (1.5, 1.0)]:
+        seed = 7 * n + 1
+        ref = oracle.Sampler(T, top_p, seed)
+        st = torch.tensor([np.uint64(seed | 1).view(np.int64)], dtype=torch.int64, device="cuda")
+        for d in range(6):
+            want = ref.sample(logits)
+            got = sample(dev, T, top_p, st)
+            assert got == want, (n, T, top_p, d, got, want)
+            assert int(st.cpu().numpy().view(np.uint64)[0]) == ref.rng.value
