@@ -62,6 +62,12 @@ QWEN3_4B_LAYER = [("wq", 2, 4096, 2560), ("wk", 2, 1024, 2560), ("wv", 2, 1024, 
                   ("w_gate", 2, 9728, 2560), ("w_up", 2, 9728, 2560), ("w_down", 3, 2560, 9728)]
 LLAMA_1B = dict(dim=2048, n_layers=16, n_heads=32, n_kv_heads=8, head_dim=64, ffn_dim=8192, vocab=128256,
                 norm_eps=1e-5, rope_theta=500000.0)
+# Qwen3-4B (36 layers, hidden 2560, 32 query / 8 KV heads of 128, ffn 9728, tied
+# 151936 head), with the formats of a Q4_K_M file: Q4_K q/k/o/gate/up, Q6_K v,
+# down and embedding
+QWEN3_4B = dict(dim=2560, n_layers=36, n_heads=32, n_kv_heads=8, head_dim=128, ffn_dim=9728, vocab=151936,
+                norm_eps=1e-6, rope_theta=1000000.0)
+QWEN3_DTYPES = {"wq": 2, "wk": 2, "wv": 3, "wo": 2, "w_gate": 2, "w_up": 2, "w_down": 3}
 
 
 def synth_weights(dtype, rows, cols, seed):
@@ -215,20 +221,25 @@ def measure_prefill(reps=3):
             "algorithmic_bytes_per_layer": tot_bytes}
 
 
-def synth_model(cfg, seed):
-    """Llama-family random-init weights with the numpy generator: all Q8_0,
-    norms 1.0, head tied to the embedding."""
+def synth_model(cfg, seed, dtypes=None, embed_dtype=1, qk_norm=False):
+    """Llama-family random-init weights with the numpy generator: all Q8_0
+    unless `dtypes` names a format per matrix, norms 1.0 (Qwen3's per-head q/k
+    norms too, with qk_norm), head tied to the embedding."""
     d, hd = cfg["dim"], cfg["head_dim"]
     att, kv, ffn = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd, cfg["ffn_dim"]
     shapes = {"wq": (att, d), "wk": (kv, d), "wv": (kv, d), "wo": (d, att), "w_gate": (ffn, d), "w_up": (ffn, d),
               "w_down": (d, ffn)}
-    w = {"embed": synth_weights(1, cfg["vocab"], d, seed), "embed_dtype": 1, "out_norm": np.ones(d, np.float32),
-         "layers": []}
+    w = {"embed": synth_weights(embed_dtype, cfg["vocab"], d, seed), "embed_dtype": embed_dtype,
+         "out_norm": np.ones(d, np.float32), "layers": []}
     for l in range(cfg["n_layers"]):
         lw = {"attn_norm": np.ones(d, np.float32), "ffn_norm": np.ones(d, np.float32), "dtypes": {}}
         for i, (name, (rows, cols)) in enumerate(shapes.items()):
-            lw[name] = synth_weights(1, rows, cols, seed + 1 + 16 * l + i)
-            lw["dtypes"][name] = 1
+            dt = dtypes[name] if dtypes else 1
+            lw[name] = synth_weights(dt, rows, cols, seed + 1 + 16 * l + i)
+            lw["dtypes"][name] = dt
+        if qk_norm:
+            lw["q_norm"] = np.ones(hd, np.float32)
+            lw["k_norm"] = np.ones(hd, np.float32)
         w["layers"].append(lw)
     return w
 
@@ -242,7 +253,7 @@ def model_bytes_per_token(cfg, kv_pos):
     return cfg["n_layers"] * per_layer + head + kv_bytes
 
 
-def nrm_blob(cfg, w):
+def nrm_blob(cfg, w, arch=1, name=b"llama-1b"):
     """The weights `w` as a .nrm v3 file in memory (crates/nr-model/src/format.rs:1-10:
     192-byte header | tokenizer blob | 32-byte table entries | data, every tensor
     64-byte aligned, meta and data CRCs), head tied to the embedding."""
@@ -257,6 +268,8 @@ def nrm_blob(cfg, w):
     ts = [(1, 0, w["embed_dtype"], cfg["vocab"], d, w["embed"]), (2, 0, 0, 1, d, w["out_norm"])]
     for l, lw in enumerate(w["layers"]):
         ts += [(10, l, 0, 1, d, lw["attn_norm"]), (15, l, 0, 1, d, lw["ffn_norm"])]
+        if "q_norm" in lw:  # Qwen3 (TensorKind AttnQNorm / AttnKNorm)
+            ts += [(19, l, 0, 1, hd, lw["q_norm"]), (20, l, 0, 1, hd, lw["k_norm"])]
         ts += [(k, l, lw["dtypes"][n], r, c, lw[n]) for n, (k, r, c) in shapes.items()]
     tok = b"\0" * 64
     table_off = 192 + len(tok)
@@ -269,10 +282,10 @@ def nrm_blob(cfg, w):
     b = np.zeros(data_off + data_size, np.uint8)
     hdr = bytearray(192)
     hdr[0:4] = b"NRUN"
-    struct.pack_into("<II8I", hdr, 4, 3, 1, d, cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"], hd, ffn,
+    struct.pack_into("<II8I", hdr, 4, 3, arch, d, cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"], hd, ffn,
                      cfg["vocab"], 131072)
     struct.pack_into("<6fI4f", hdr, 44, cfg["rope_theta"], cfg["norm_eps"], 0.0, 0.0, 0.0, 0.0, 1, 1.0, 0.0, 1.0, 1.0)
-    hdr[88:96] = b"llama-1b"
+    hdr[88:88 + len(name)] = name
     struct.pack_into("<QQQIIQQ", hdr, 136, 192, len(tok), table_off, len(ts), 0, data_off, data_size)
     table = bytearray(32 * len(ts))
     for i, (t, off) in enumerate(zip(ts, offs)):
@@ -382,6 +395,60 @@ def measure_decode(fill=1024, n=128):
                         "tok_s": round(fill / pf_dt, 1),
                         "what": "nrq_model_prefill of the random prompt from position 0 (KV 0..1023), host sync "
                                 "per chunk, logits of the last token copied back"}}
+
+
+def kquant_bytes(dt, rows, cols):
+    return rows * cols // 256 * (144 if dt == 2 else 210) if dt in (2, 3) else rows * cols // 32 * 34
+
+
+def measure_qwen3(fill=512, n=64):
+    """Qwen3-4B shape with Q4_K_M formats through a Qwen3 .nrm file (the loader
+    sets the recipe: per-head q/k RMSNorm, Neox rope): a `fill`-token prefill,
+    then n greedy steps. The reference publishes 10.6-11.9 tok/s decode and
+    20.7 tok/s batch-64 prefill for Qwen3-4B Q4_K_M on its 8-thread x86 host."""
+    import torch
+
+    from nightrun_amd import nrm
+
+    cfg = QWEN3_4B
+    w = synth_model(cfg, 0x5EED0044, dtypes=QWEN3_DTYPES, embed_dtype=3, qk_norm=True)
+    blob = nrm_blob(cfg, w, arch=2, name=b"qwen3-4b")
+    del w
+    t0 = time.perf_counter()
+    f = nrm.NrmFile(blob)
+    m = f.load(fill + n + 8, verify=False)
+    load_s = time.perf_counter() - t0
+    del blob
+    prompt = np.random.default_rng(44).integers(0, cfg["vocab"], fill).astype(np.uint32)
+    m.prefill(prompt[:64], logits=False)  # warm-up
+    m.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    lg = m.prefill(prompt)
+    pf_dt = time.perf_counter() - t0
+    m.generate(int(np.argmax(lg)), 4)  # captures the step graph
+    m.reset()
+    m.prefill(prompt, logits=False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    m.generate(int(np.argmax(lg)), n)
+    dt = time.perf_counter() - t0
+    m.close()
+    torch.cuda.empty_cache()
+    d, hd = cfg["dim"], cfg["head_dim"]
+    att, kv, ffn = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd, cfg["ffn_dim"]
+    shapes = {"wq": (att, d), "wk": (kv, d), "wv": (kv, d), "wo": (d, att), "w_gate": (ffn, d), "w_up": (ffn, d),
+              "w_down": (d, ffn)}
+    per_tok = cfg["n_layers"] * sum(kquant_bytes(QWEN3_DTYPES[k], r, c) for k, (r, c) in shapes.items())
+    per_tok += kquant_bytes(3, cfg["vocab"], d) + cfg["n_layers"] * (fill + n // 2) * kv * 2 * 2
+    return {"workload": "Qwen3-4B architecture, Q4_K_M formats (Q4_K q/k/o/gate/up, Q6_K v/down/embedding, tied "
+                        "151936 head), random init, Qwen3 recipe (qk-norm, Neox rope) from the .nrm header; "
+                        f"prefill of {fill} tokens, then greedy at positions {fill}..{fill + n - 1}",
+            "tok_s": round(n / dt, 1), "ms_per_token": round(dt / n * 1e3, 4), "bytes_per_token": int(per_tok),
+            "gbs": round(per_tok * n / dt / 1e9, 1), "prefill_tok_s": round(fill / pf_dt, 1),
+            "load_seconds": round(load_s, 3),
+            "reference_host": {"decode_tok_s": "10.6-11.9", "prefill_batch64_tok_s": 20.7,
+                               "source": "docs/benchmarks.md:63-64, docs/baseline-x86.md:144"}}
 
 
 def host_cores():
@@ -529,6 +596,12 @@ def main():
         others[name] = {k: round(v, 3) if isinstance(v, float) else v for k, v in o.items()}
     prefill = None if args.no_prefill else measure_prefill()
     decode = None if args.no_decode else measure_decode()
+    qwen3 = None
+    if not args.no_decode:
+        try:
+            qwen3 = measure_qwen3()
+        except Exception as e:  # reported, never fatal to the bench line
+            qwen3 = {"error": f"{type(e).__name__}: {e}"}
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline_matvec(args.config, args.cpu_seconds)
@@ -571,6 +644,7 @@ def main():
         "other_configs": others,
         "prefill": prefill,
         "decode": decode,
+        "decode_qwen3": qwen3,
     }
     print(json.dumps(out))
 
