@@ -545,6 +545,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--also", default="cfg1,cfg3", help="other matvec configs reported beside (comma list)")
+    ap.add_argument("--qwen3-only", action="store_true", help="only the Qwen3-4B decode/prefill leg (profiling)")
     ap.add_argument("--prefill-only", type=int, default=0, metavar="TOKENS",
                     help="only time nrq_model_prefill of TOKENS tokens on the Llama-3.2-1B-shape model")
     ap.add_argument("--crc-only", type=int, default=0, metavar="BYTES",
@@ -554,6 +555,12 @@ def main():
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration << 20)
+        return
+    if args.qwen3_only:
+        import nightrun_amd
+
+        nightrun_amd.init(0)
+        print(json.dumps({"decode_qwen3": measure_qwen3()}))
         return
     if args.prefill_only:
         import torch
