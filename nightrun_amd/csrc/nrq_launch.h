@@ -54,6 +54,10 @@ int launch_decode_scalar(int dtype, const MatvecLaunch& L);
 int launch_stream_scalar(int dtype, const MatvecLaunch& L);
 // Scalar-order decode, one lane per block, per-wave LDS streaming (nrq_wstream.hip).
 int launch_wstream_scalar(int dtype, const MatvecLaunch& L);
+// scalar-order matvecs of up to three matrices of one format sharing the
+// activation x (bpr blocks per row), one launch
+int launch_wstream_group(int dtype, const void* const* w, float* const* y, const int* rows, int n, const void* x,
+                         int bpr, void* stream);
 // Rmsnorm of x (after x += add when add != null; the sum is written to x_out)
 // and its Q8_0 quantization, fused into one launch of up to three Q8_0 matvecs
 // over that activation (nrq_wstream.hip). n = cols, a multiple of 256 up to

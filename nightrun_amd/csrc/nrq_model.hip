@@ -1330,7 +1330,7 @@ int norm_quant(nrq_model* m, float* xr, const float* add, const float* w, int dt
 int matvec_group(nrq_model* m, const Mat* const* ws, float* const* ys, const int* rows, int n, int cols) {
   const int first = ws[0]->dt == NRQ_Q8_0 ? 0 : 1;
   bool other_ready = false;
-  for (int i = 0; i < n; i++) {
+  for (int i = 0; i < n;) {
     const int fmt = ws[i]->dt == NRQ_Q8_0 ? 0 : 1;
     const uint8_t* xq = m->xq;
     if (fmt != first) {
@@ -1341,8 +1341,25 @@ int matvec_group(nrq_model* m, const Mat* const* ws, float* const* ys, const int
       }
       xq = m->xq2;
     }
-    int rc = matvec(m, *ws[i], xq, ys[i], rows[i], cols);
-    if (rc) return rc;
+    // a run of matrices of one dtype goes out as one launch (q|k, gate|up)
+    int j = i + 1;
+    while (j < n && ws[j]->dt == ws[i]->dt) j++;
+    if (j - i > 1) {
+      const void* w[3];
+      float* y[3];
+      int r[3];
+      for (int t = i; t < j; t++) {
+        w[t - i] = ws[t]->w;
+        y[t - i] = ys[t];
+        r[t - i] = rows[t];
+      }
+      if (nrq::launch_wstream_group(ws[i]->dt, w, y, r, j - i, xq, cols / qk_of(ws[i]->dt), m->stream))
+        return mfail(NRQ_ERR_DEVICE, "model: grouped matvec launch failed");
+    } else {
+      int rc = matvec(m, *ws[i], xq, ys[i], rows[i], cols);
+      if (rc) return rc;
+    }
+    i = j;
   }
   return NRQ_OK;
 }

@@ -699,6 +699,44 @@ int launch_norm_matvec_q8_0(const NormMatvecLaunch& L) {
              : launch_ws_t<kQ8_0, 4, 2, kWsNorm>(A, bpr, rpw, L.stream);
 }
 
+// Up to three matrices of one format over one activation in one launch
+// (q|k, gate|up in a K-quant layer): workgroups are laid out matrix after
+// matrix, each row computed as launch_ws computes it.
+template <int FMT>
+static int launch_ws_group(const void* const* w, float* const* y, const int* rows, int n, const void* x, int bpr,
+                           void* stream) {
+  const int rpw = ws_rows_per_wave<FMT>(bpr, 0);
+  WsArgs A{};
+  for (int i = 0; i < n; i++) {
+    A.w[i] = (const uint8_t*)w[i];
+    A.y[i] = y[i];
+    A.rows[i] = rows[i];
+  }
+  A.nmat = n;
+  A.x = (const uint8_t*)x;
+  int rc;
+  if (ws_u_rowmajor(bpr)) {
+    rc = launch_ws_t<FMT, 4, 2, kWsRowMajorU>(A, bpr, rpw, stream);
+    if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, kWsRowMajorU>(A, bpr, rpw, stream);
+  } else {
+    rc = FMT == kQ4K ? launch_ws_t<FMT, 8, 2, 0>(A, bpr, rpw, stream) : NRQ_LAUNCH_TOO_WIDE;
+    if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 4, 2, 0>(A, bpr, rpw, stream);
+    if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, 0>(A, bpr, rpw, stream);
+  }
+  return rc;
+}
+
+int launch_wstream_group(int dtype, const void* const* w, float* const* y, const int* rows, int n, const void* x,
+                         int bpr, void* stream) {
+  if (n < 1 || n > 3 || bpr <= 0) return NRQ_LAUNCH_BAD_ARG;
+  for (int i = 0; i < n; i++)
+    if (rows[i] <= 0) return NRQ_LAUNCH_BAD_ARG;
+  if (dtype == kQ8_0) return launch_ws_group<kQ8_0>(w, y, rows, n, x, bpr, stream);
+  if (dtype == kQ4K) return launch_ws_group<kQ4K>(w, y, rows, n, x, bpr, stream);
+  if (dtype == kQ6K) return launch_ws_group<kQ6K>(w, y, rows, n, x, bpr, stream);
+  return NRQ_LAUNCH_BAD_ARG;
+}
+
 int launch_wstream_scalar(int dtype, const MatvecLaunch& L) {
   if (L.rows <= 0 || L.bpr <= 0) return 0;
   if (dtype == kQ8_0) return launch_ws<kQ8_0>(L);
