@@ -6,8 +6,9 @@
 Headline (`value`): the decode matvec of the Q4_K 8192 x 3072 matrix
 (Llama-3.2-3B FFN shape) against a runtime-quantized Q8_K activation. A step
 is one matvec launch over weights already resident in HBM; the K timed steps
-run back to back as one captured HIP graph and rotate over more than 512 MiB
-of weight copies, so the 256 MiB MALL cannot serve them. `value` is
+run back to back as one captured HIP graph. Weights come from distinct copies
+(as many as the K steps, up to 2 x the 256 MiB MALL), and a 1 GiB device copy
+runs before every replay, so no timed read can hit the MALL. `value` is
 algorithmic bytes x K / the graph's wall time (HIP events on the launch
 stream); `roofline.achieved` is algorithmic bytes / the mean time per launch
 inside that graph.
@@ -22,9 +23,10 @@ Beside it, in the same JSON line:
                  section's CRC-32 is timed on the device (verify_crc); the
                  1024-token prompt goes through the batched prefill
                  (prefill tok/s beside it)
-  cpu_baseline   the CPU oracle's AVX2 restatement of the matvec, and its
-                 scalar-order restatement of the full decode step, timed on a
-                 bounded sample on the host cores
+  cpu_baseline   the CPU oracle's AVX2 and scalar restatements of the matvec,
+                 each on 1 thread and on the box's host-core share (median of
+                 >= 21 full matvecs), and its scalar-order restatement of the
+                 full decode step at the GPU leg's KV positions
 """
 from __future__ import annotations
 
@@ -99,10 +101,31 @@ def algorithmic_bytes(dtype, rows, cols, batch=1):
     return rows * bpr * WBYTES[dtype] + batch * bpr * XBYTES[dtype] + batch * rows * 4
 
 
-def graph_time(stream, launch, k):
+class MallFlush:
+    """A 1 GiB device-to-device copy (reads 512 MiB, writes 512 MiB: four times
+    the 256 MiB MALL), run untimed before a measured region so that none of the
+    weights it reads can still be cached there."""
+
+    BYTES = 512 << 20
+
+    def __init__(self):
+        import torch
+
+        self.src = torch.ones(self.BYTES, dtype=torch.uint8, device="cuda")
+        self.dst = torch.empty_like(self.src)
+
+    def __call__(self, stream):
+        import torch
+
+        with torch.cuda.stream(stream):
+            self.dst.copy_(self.src)
+
+
+def graph_time(stream, launch, k, flush=None):
     """Captures k launches (launch(i)) into one HIP graph, replays it once
-    untimed, then times one replay with HIP events on `stream`. Returns
-    (seconds per replay, seconds per launch)."""
+    untimed, then times one replay with HIP events on `stream`; `flush(stream)`
+    runs before each replay, outside the timed region. Returns (seconds per
+    replay, seconds per launch)."""
     import torch
 
     g = torch.cuda.CUDAGraph()
@@ -111,8 +134,12 @@ def graph_time(stream, launch, k):
         for i in range(k):
             launch(i)
         g.capture_end()
+    if flush:
+        flush(stream)
     with torch.cuda.stream(stream):  # replay() launches on the current stream
         g.replay()
+    if flush:
+        flush(stream)
     stream.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
@@ -135,7 +162,10 @@ def measure_matvec(name, steps, warmup, order):
     nightrun_amd.init(0)
     w = synth_weights(dtype, rows, cols, seed)
     xf = np.random.default_rng(seed + 1).normal(0, 1, cols).astype(np.float32)
-    copies = max(2, -(-(2 * MALL_BYTES) // w.nbytes))
+    # distinct copies for the K steps, up to 2 x MALL of them: within a replay a
+    # copy is read again only after 2 x MALL of other weights
+    copies = max(2, min(steps, -(-(2 * MALL_BYTES) // w.nbytes)))
+    flush = MallFlush()
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         w0 = torch.from_numpy(w).cuda()
@@ -150,10 +180,11 @@ def measure_matvec(name, steps, warmup, order):
     def step(i):
         device.matvec(dtype, order, y, ws[i % copies], xq, rows, cols, stream=stream)
 
+    flush(stream)
     for i in range(warmup):
         step(i)
     stream.synchronize()
-    wall, per = graph_time(stream, step, steps)
+    wall, per = graph_time(stream, step, steps, flush)
     nbytes = algorithmic_bytes(dtype, rows, cols)
     # the activation quantizer, reported beside
     q0, q1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -162,10 +193,12 @@ def measure_matvec(name, steps, warmup, order):
         (device.quantize_q8_0 if dtype == 1 else device.quantize_q8k)(xd, xq, stream=stream)
     q1.record(stream)
     stream.synchronize()
-    out = {"bytes": nbytes, "copies": copies, "wall_s": wall, "ms_per_step": wall / steps * 1e3,
+    out = {"bytes": nbytes, "copies": copies, "rotated_weight_bytes": copies * int(w.nbytes),
+           "timed_distinct_weight_bytes": min(steps, copies) * int(w.nbytes), "wall_s": wall,
+           "ms_per_step": wall / steps * 1e3,
            "value_gbs": nbytes * steps / wall / 1e9, "kernel_us": per * 1e6, "kernel_gbs": nbytes / per / 1e9,
            "quant_us": q0.elapsed_time(q1) / 20 * 1e3}
-    del ws, w0
+    del ws, w0, flush
     torch.cuda.empty_cache()
     return out
 
@@ -182,7 +215,7 @@ def measure_prefill(reps=3):
     nightrun_amd.init(0)
     stream = torch.cuda.Stream()
     mats, tot_bytes, tot_ops = [], 0, 0.0
-    copies = 4  # 4 x 73 MB per layer > MALL
+    copies = 4  # the layers of one replay read distinct weight copies
     with torch.cuda.stream(stream):
         for j, (name, dt, rows, cols) in enumerate(QWEN3_4B_LAYER):
             w = torch.from_numpy(synth_weights(dt, rows, cols, 0x5EED0004 + j)).cuda()
@@ -208,10 +241,12 @@ def measure_prefill(reps=3):
             device.matmul_group(dt, [mats[j][5] for j in g], [mats[j][3][i % copies] for j in g],
                                 [mats[j][1] for j in g], xq, cols, 64, stream=stream)
 
+    flush = MallFlush()
+    flush(stream)
     layer(0)
     stream.synchronize()
-    wall, per = graph_time(stream, layer, reps)
-    del mats
+    wall, per = graph_time(stream, layer, reps, flush)
+    del mats, flush
     torch.cuda.empty_cache()
     return {"workload": "Qwen3-4B layer at M=64: Q/K/V/O/gate/up Q4_K, down Q6_K (hidden 2560, attention 4096, "
                         "KV 1024, ffn 9728), per-row Q8_K activations",
@@ -452,13 +487,48 @@ def measure_qwen3(fill=512, n=64):
 
 
 def host_cores():
+    """Threads for the CPU baselines: every CPU this process may run on, up to
+    the 16-core host share a one-GPU box gives a job (the pool is not sized past
+    what the job owns, whatever the machine reports)."""
     return min(16, len(os.sched_getaffinity(0)))
 
 
+def cpu_info():
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "machine_cpus": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "pool_threads": host_cores()}
+
+
+def _median_rate(fn, nbytes, reps, seconds):
+    """Median GB/s of fn() over at least `reps` calls (more while under `seconds`)."""
+    fn()  # warm-up (pool threads, page faults)
+    ts = []
+    t_end = time.perf_counter() + seconds
+    while len(ts) < reps or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    med = ts[len(ts) // 2]
+    return nbytes / med / 1e9, len(ts), med
+
+
 def cpu_baseline_matvec(name, seconds):
-    """The oracle's AVX2 restatement (the reference's timed x86 host path)
-    with a parallel.rs-style row pool, on full matvecs of the same workload,
-    weights rotated beyond the LLC."""
+    """The oracle's AVX2 and scalar restatements (the reference's x86 fast path
+    and its scalar kernels, kernels.rs / kquant.rs) on full matvecs of the same
+    workload, each on 1 thread and on the host-core share with a
+    parallel.rs-style row pool (chunk rule parallel.rs:97, calling thread
+    included), weights rotated over copies beyond the LLC; median of >= 21
+    calls. `value` is the AVX2 order on all pool threads (the reference's own
+    timed host path)."""
     import oracle as O
 
     dtype, rows, cols, seed, _ = CONFIGS[name]
@@ -467,40 +537,51 @@ def cpu_baseline_matvec(name, seconds):
     copies = max(1, min(8, -(-(256 << 20) // w.nbytes)))
     ws = [w] + [w.copy() for _ in range(copies - 1)]
     x = O.quantize_act(dtype, O.Rng(seed ^ 0xABCDEF).normal(cols))
-    O.matvec(dtype, O.ORDER_AVX2, ws[0], x, rows, cols, threads)  # warm the pool
-    n = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        O.matvec(dtype, O.ORDER_AVX2, ws[n % copies], x, rows, cols, threads)
-        n += 1
-    dt = time.perf_counter() - t0
-    return {"value": round(algorithmic_bytes(dtype, rows, cols) * n / dt / 1e9, 3), "unit": "GB/s",
-            "cores": threads, "kind": "port",
-            "sample": f"{n} full {name} matvecs (AVX2 order, {threads} threads, {copies} rotating weight copies) "
-                      f"in {dt:.1f} s"}
+    nbytes = algorithmic_bytes(dtype, rows, cols)
+    runs = {}
+    per = max(1.0, seconds / 4)
+    for order, oname in ((O.ORDER_AVX2, "avx2"), (O.ORDER_SCALAR, "scalar")):
+        for nt in (1, threads):
+            k = [0]
+
+            def call():
+                O.matvec(dtype, order, ws[k[0] % copies], x, rows, cols, nt)
+                k[0] += 1
+
+            gbs, n, med = _median_rate(call, nbytes, 21, per)
+            runs[f"{oname}_{nt}t"] = {"gbs": round(gbs, 3), "median_ms": round(med * 1e3, 3), "calls": n,
+                                      "threads": nt}
+    top = runs[f"avx2_{threads}t"]
+    return {"value": top["gbs"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"median of {top['calls']} full {name} matvecs (AVX2 order, {threads} threads, {copies} "
+                      f"rotating weight copies); every order x thread count in `runs`",
+            "runs": runs, **cpu_info()}
 
 
-def cpu_baseline_decode(seconds):
+def cpu_baseline_decode(seconds, fill=1024):
     """The oracle's restatement of InferCtx::forward (scalar-order kernels,
-    parallel.rs-style pool) on the same architecture: one 64-token prefill
-    chunk, then greedy decode steps for about `seconds`."""
+    parallel.rs-style pool) on the same architecture, greedy, at the GPU leg's
+    KV positions: the model is moved to position `fill` without computing the
+    cache rows before it (their cost does not depend on their values), then
+    decodes for about `seconds` (at most 128 steps)."""
     import oracle as O
 
     threads = host_cores()
     cfg = dict(O.LLAMA_1B)
     w = O.gen_model(cfg, 0x5EED0005)
-    m = O.Model(cfg, w, ctx=256, threads=threads)
-    logits = m.prefill(np.random.default_rng(5).integers(0, cfg["vocab"], 64).astype(np.uint32))
-    tok = O.argmax(logits)
+    m = O.Model(cfg, w, ctx=fill + 136, threads=threads)
+    m.seek(fill)
+    tok = O.argmax(m.forward(1))  # warm-up step at position fill
     n = 0
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds and m.pos < 256:
+    while time.perf_counter() - t0 < seconds and n < 128:
         tok = O.argmax(m.forward(tok))
         n += 1
     dt = time.perf_counter() - t0
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} greedy decode steps at KV positions 64..{63 + n} of the Llama-3.2-1B-shape Q8_0 model "
-                      f"(scalar-order kernels, {threads} threads) in {dt:.1f} s"}
+            "sample": f"{n} greedy decode steps at KV positions {fill + 1}..{fill + n} of the Llama-3.2-1B-shape Q8_0 "
+                      f"model (scalar-order kernels, {threads} threads) in {dt:.1f} s; cache rows before {fill} "
+                      f"not computed (same cost per step)"}
 
 
 def cpu_baseline_crc(seconds):

@@ -145,12 +145,18 @@ int nrq_dev_mathf(int fn, const float *x, float *y, size_t n, void *stream);
 /* Waits for all work on `stream` (NULL = library stream). */
 int nrq_sync(void *stream);
 
-/* ---- Llama-family decode on one GPU ----------------------------------------------
- * The forward pass of crates/nr-model/src/infer.rs (InferCtx) for the Llama
- * recipe (no qk-norm, adjacent-pair RoPE without frequency scaling, neutral
- * embed/residual/logit scales), every tensor resident in HBM, bit-identical to
- * the reference's scalar kernels, with greedy sampling (sample.rs:32-35). The
- * KV cache holds f16 bits, as the reference's does (infer.rs:297-299). */
+/* ---- decode and prefill of a whole model on one GPU ---------------------------------
+ * The forward pass of crates/nr-model/src/infer.rs (InferCtx) for the three
+ * recipes it runs (infer.rs:447-461): Llama (adjacent-pair RoPE), Qwen3
+ * (per-head q/k RMSNorm, NeoX pairs) and Granite (muP embed / attention /
+ * residual / logit scales), with Llama-3 rope scaling or RopeFreqs factors
+ * through nrq_model_set_rope_freqs. Layer matrices may be Q8_0, Q4_K or Q6_K
+ * in any mix; the embedding (and an untied head) Q8_0, Q4_K or Q6_K. Every
+ * tensor is resident in HBM; greedy (sample.rs:32-35) or top-p sampling
+ * (sample.rs:36-96). The KV cache holds f16 bits, as the reference's does
+ * (infer.rs:297-299).
+ * The model always computes in the reference's scalar order, bit-identical to
+ * dot_*_scalar (and so to the NEON path); nrq_set_order does not apply to it. */
 
 #define NRQ_F32 0 /* dtype of f32 tensors (norm weights) */
 
@@ -299,13 +305,17 @@ uint32_t nrq_crc32(uint32_t crc, const void *data, size_t n);
  * buffer and must not run concurrently. */
 int nrq_dev_crc32(const void *data, size_t n, uint32_t crc, uint32_t *out, void *stream);
 
-/* InferCtx::new (infer.rs:352-447) over a parsed file: checks that every
- * tensor of the Llama recipe is present with its shape (MissingTensor errors as
- * the reference reports them), uploads the data section once, optionally
- * verifies it on the device (NRQ_NRM_VERIFY_DATA), binds the tensors (the head
- * tied to the embedding under FLAG_TIED_EMBEDDINGS) and sets the rope table.
- * The model owns the device copy. Qwen3 files and non-neutral muP scales are
- * NRQ_ERR_UNSUPPORTED (the device decode runs the Llama recipe). */
+/* InferCtx::new (infer.rs:352-461) over a parsed file of any arch (Llama3,
+ * Qwen3, Granite): checks that every tensor the recipe needs is present with
+ * its shape, in the reference's order (MissingTensor errors as it reports
+ * them, Qwen3's attn_q_norm / attn_k_norm included, and "unexpected
+ * attn_q_norm for this arch" for the other families), uploads the data section
+ * once, optionally verifies it on the device (NRQ_NRM_VERIFY_DATA), binds the
+ * tensors (the head tied to the embedding under FLAG_TIED_EMBEDDINGS), sets the
+ * rope table (RopeFreqs factors or the header's Llama-3 scaling) and the recipe
+ * (NeoX pairs for Qwen3, the header's muP scales). The model owns the device
+ * copy. Widths are checked in 64 bits; a model whose widths do not fit an int
+ * is NRQ_ERR_UNSUPPORTED. */
 int nrq_model_load_nrm(const nrq_nrm *f, int ctx, int flags, nrq_model **out);
 
 #ifdef __cplusplus

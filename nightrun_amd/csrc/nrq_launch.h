@@ -24,8 +24,6 @@ struct MatvecLaunch {
   int bpr;
   int tile_rows;  // 0 = library choice, else rows per tile
   void* stream;   // hipStream_t
-  int variant = 0;  // scalar order: 0 default, 1 one-shot LDS tiles, 2 direct-to-register,
-                    // 3 workgroup-pipelined LDS streaming, 4 per-wave LDS streaming
 };
 
 struct MatmulLaunch {
@@ -36,8 +34,6 @@ struct MatmulLaunch {
   int bpr;
   int batch;
   void* stream;
-  int variant = 0;  // scalar order: 0 int8-MFMA kernels (32 x 32 tiles for Q4_K/Q6_K), 1 one
-                    // decode launch per token, 2 the 16 x 16 int8-MFMA kernel for every format
 };
 
 struct QuantLaunch {
@@ -47,11 +43,9 @@ struct QuantLaunch {
   void* stream;
 };
 
+// Scalar order: the streaming kernel (nrq_wstream.hip); AVX2 order: the
+// one-shot LDS tile kernel (nrq_matvec.hip).
 int launch_matvec(int dtype, int order, const MatvecLaunch& L);
-// Scalar-order decode kernels: weights HBM -> registers (nrq_decode.hip) and
-// persistent double-buffered LDS streaming (nrq_stream.hip).
-int launch_decode_scalar(int dtype, const MatvecLaunch& L);
-int launch_stream_scalar(int dtype, const MatvecLaunch& L);
 // Scalar-order decode, one lane per block, per-wave LDS streaming (nrq_wstream.hip).
 int launch_wstream_scalar(int dtype, const MatvecLaunch& L);
 // scalar-order matvecs of up to three matrices of one format sharing the
@@ -81,7 +75,8 @@ struct NormMatvecLaunch {
 };
 int launch_norm_matvec_q8_0(const NormMatvecLaunch& L);
 int launch_matmul(int dtype, int order, const MatmulLaunch& L);
-// Scalar-order batched matmul on int8 MFMA (nrq_mmq.hip).
+// Scalar-order batched matmul on int8 MFMA: the 32 x 32 tiles of nrq_mmt.hip,
+// or for Q8_0 below 1024 rows the 16 x 16 tiles of nrq_mmq.hip.
 int launch_mmq(int dtype, const MatmulLaunch& L);
 // Prefill on 32-row x 32-token wave tiles (nrq_mmt.hip); mmt_fits: the kernel
 // handles the format and shape.

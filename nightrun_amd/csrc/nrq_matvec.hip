@@ -1,25 +1,20 @@
-// Decode matvec kernels for gfx950: y[r] = dot(W[r, :], x) over Q8_0 / Q4_K /
-// Q6_K weights read in place from HBM, against a pre-quantized activation
-// (Q8_0 or Q8_K). Restates the reference's row loops
+// Decode matvec in the reference's AVX2 f32 order for gfx950: y[r] =
+// dot(W[r, :], x) over Q8_0 / Q4_K / Q6_K weights read in place from HBM,
+// against a pre-quantized activation (Q8_0 or Q8_K). Restates the row loops
 //   kernels.rs:36-70 (matvec_q8), kquant.rs:536-564 (matvec_q4k / matvec_q6k)
-// with the per-row dot reproduced bit for bit in one of two f32 orders:
-//   ORDER_SCALAR : dot_q8_scalar (kernels.rs:72-82), dot_q4k_scalar
-//                  (kquant.rs:192-218), dot_q6k_scalar (kquant.rs:220-250)
-//   ORDER_AVX2   : dot_q8_avx2 (kernels.rs:263-286), dot_q4k_avx2
-//                  (kquant.rs:260-305), dot_q6k_avx2 (kquant.rs:454-510)
+// with the per-row dot of dot_q8_avx2 (kernels.rs:263-286), dot_q4k_avx2
+// (kquant.rs:260-305) and dot_q6k_avx2 (kquant.rs:454-510) bit for bit. (The
+// scalar order's decode kernel is nrq_wstream.hip.)
 //
 // One workgroup owns `tr` consecutive rows. Those rows are one contiguous
 // byte range of W; it is streamed HBM -> VGPR -> LDS with 16-byte loads
-// (every lane's load is issued before any is consumed), then:
-//   scalar order : phase 1 computes, per (row, block), the block's f32
-//                  contribution exactly as the reference forms it (integer
-//                  sub-dots with v_dot4, then the reference's f32 steps);
-//                  phase 2 adds those contributions in block order, one lane
-//                  per row (the reference's `sumf +=` chain).
-//   AVX2 order   : lane (row, k) owns the k-th i32/f32 lane of the reference's
-//                  __m256 accumulators (bytes 4k..4k+3 of every 32-byte
-//                  vector), runs the fmadd chain over blocks, then the 8
-//                  lanes reduce in hsum256's order ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7)).
+// (every lane's load is issued before any is consumed). Lane (row, k) then
+// owns the k-th i32/f32 lane of the reference's __m256 accumulators (bytes
+// 4k..4k+3 of every 32-byte vector), runs the fmadd chain over blocks, and the
+// 8 lanes reduce in hsum256's order ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7)).
+//
+// The same staging and integer code also gives the exact per-(row, block)
+// integer sums of the scalar kernels (block_sums_kernel, a diagnostic entry).
 #include "nrq_device.h"
 #include "nrq_launch.h"
 
@@ -132,18 +127,14 @@ __device__ void repack_x(const uint8_t* raw, uint32_t xskew, int bpr, uint8_t* l
   }
 }
 
-// LDS layout of one workgroup: [repacked x | weight tile | aux], where aux
-// first holds the raw activation and later (scalar order) the per-(row,
-// block) contributions u[b * tr + r].
+// LDS layout of one workgroup: [repacked x | weight tile | raw activation].
 template <int FMT>
 struct TileGeom {
   int xrep, wtile, aux;
-  __host__ __device__ TileGeom(int bpr, int tr, bool with_u) {
+  __host__ __device__ TileGeom(int bpr, int tr) {
     xrep = (Fmt<FMT>::x_lds_bytes(bpr) + 15) & ~15;
     wtile = (int)(((size_t)tr * bpr * Fmt<FMT>::BS + 15 + 32 + 15) & ~(size_t)15);
-    int u = with_u ? ((tr * bpr * 4 + 15) & ~15) : 0;
-    int raw = x_raw_bytes<FMT>(bpr);
-    aux = u > raw ? u : raw;
+    aux = x_raw_bytes<FMT>(bpr);
   }
   __host__ __device__ size_t total() const { return (size_t)xrep + wtile + aux; }
 };
@@ -174,7 +165,7 @@ __device__ __forceinline__ uint32_t stage_all(const uint8_t* __restrict__ W, con
   return (uint32_t)(t0 - a0);
 }
 
-// ---- scalar order: per-(row, block) contributions -------------------------------
+// ---- exact integer sums of one block (the scalar kernels' sub-dots) ---------------
 
 // kernels.rs:75-78: acc = sum over the 32 quants of w*x (i32, exact)
 __device__ __forceinline__ int block_q8_0_ints(const uint8_t* lds_w, uint32_t o, const uint32_t* xq, int b) {
@@ -188,15 +179,6 @@ __device__ __forceinline__ int block_q8_0_ints(const uint8_t* lds_w, uint32_t o,
 #pragma unroll
   for (int t = 0; t < 8; t++) acc = sdot4(__builtin_amdgcn_alignbyte(D[t + 1], D[t], sh), xq[b * 8 + t], acc);
   return acc;
-}
-
-// kernels.rs:79: contribution = (f32(acc) * dw) * dx
-__device__ __forceinline__ float block_q8_0_scalar(const uint8_t* lds_w, uint32_t o, const uint32_t* xq,
-                                                   const float* xd, int b) {
-  int acc = block_q8_0_ints(lds_w, o, xq, b);
-  float dw = f16_bits_to_f32(lds_u16(lds_w, o));
-  float t1 = (float)acc * dw;
-  return t1 * xd[b];
 }
 
 // kquant.rs:200-214: sub_j = sum over sub-block j's 32 quants of q4*q8 (i32),
@@ -235,24 +217,6 @@ __device__ __forceinline__ void block_q4k_ints(const uint8_t* lds_w, uint32_t o,
   r.dd = hdr.x;
 }
 
-// kquant.rs:195-215: sum_q += f32(sc)*f32(sub) in j order, contribution =
-// d_all*sum_q - dmin_all*f32(sum_m).
-// f32(sc)*f32(sub) == f32(sc*sub): |sc*sub| <= 63*61440 < 2^24, exact.
-__device__ __forceinline__ float block_q4k_scalar(const uint8_t* lds_w, uint32_t o, const uint32_t* xq,
-                                                  const float* xd, const int32_t* xbs, int b) {
-  Q4KInts r;
-  block_q4k_ints(lds_w, o, xq, xbs, b, r);
-  float sum_q = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; j++) sum_q = sum_q + (float)(r.sc[j] * r.sub[j]);
-  float xdb = xd[b];
-  float d_all = f16_bits_to_f32(r.dd & 0xffffu) * xdb;
-  float dmin_all = f16_bits_to_f32(r.dd >> 16) * xdb;
-  float a = d_all * sum_q;
-  float m = dmin_all * (float)r.sum_m;
-  return a - m;
-}
-
 // Reads the 210-byte Q6_K block at even LDS offset o as 53 realigned dwords.
 __device__ __forceinline__ void load_q6k_block(const uint8_t* lds_w, uint32_t o, uint32_t v[53]) {
   const uint32_t* w32 = (const uint32_t*)lds_w;
@@ -289,25 +253,6 @@ __device__ __forceinline__ void block_q6k_ints(const uint32_t v[53], const uint3
       }
     }
   }
-}
-
-// kquant.rs:243-247: sum += f32(sc[g])*f32(gs[g]) in g order across both
-// halves, contribution = d_all * sum.
-// f32(sc)*f32(gs) == f32(sc*gs): |sc*gs| <= 128*65536 < 2^24, exact.
-__device__ __forceinline__ float block_q6k_scalar(const uint8_t* lds_w, uint32_t o, const uint32_t* xq,
-                                                  const float* xd, const int32_t* xc, int b) {
-  uint32_t v[53];
-  load_q6k_block(lds_w, o, v);
-  int gs[16];
-  block_q6k_ints(v, xq, xc, b, gs);
-  float sum = 0.0f;
-#pragma unroll
-  for (int g = 0; g < 16; g++) {
-    int s = (int)(int8_t)((v[48 + (g >> 2)] >> (8 * (g & 3))) & 0xffu);
-    sum = sum + (float)(s * gs[g]);
-  }
-  float d_all = f16_bits_to_f32(v[52] & 0xffffu) * xd[b];
-  return d_all * sum;
 }
 
 // ---- AVX2 order: lane (row, k) of the __m256 accumulators --------------------------
@@ -405,15 +350,15 @@ constexpr int kMatvecMaxC = 12;  // 16-byte weight loads per lane: a 48 KiB tile
 constexpr int kMatvecMaxX = 8;   // activation dwords per lane issued with the tile
 constexpr size_t kLdsLimit = 65536;
 
-template <int FMT, int ORDER, int NT, int MAXC, int MAXX>
-__global__ __launch_bounds__(NT) void matvec_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ X,
-                                                    float* __restrict__ Y, int rows, int bpr, int tr) {
+template <int FMT, int NT, int MAXC, int MAXX>
+__global__ __launch_bounds__(NT) void matvec_avx2_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ X,
+                                                         float* __restrict__ Y, int rows, int bpr, int tr) {
   using F = Fmt<FMT>;
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
   const int row0 = blockIdx.x * tr;
   const int nr = min(tr, rows - row0);
-  const TileGeom<FMT> G(bpr, tr, ORDER == kOrderScalar);
+  const TileGeom<FMT> G(bpr, tr);
   const uint32_t skew = stage_all<FMT, NT, MAXC, MAXX>(W, X, bpr, row0, nr, G, smem);
   const uint8_t* lds_x = smem;
   const uint8_t* lds_w = smem + G.xrep;
@@ -421,41 +366,19 @@ __global__ __launch_bounds__(NT) void matvec_kernel(const uint8_t* __restrict__ 
   const float* xd = (const float*)(lds_x + (FMT == kQ8_0 ? bpr * 32 : bpr * 256));
   const int32_t* xe = (const int32_t*)(lds_x + bpr * 260);
 
-  if constexpr (ORDER == kOrderScalar) {
-    float* u = (float*)(smem + G.xrep + G.wtile);  // u[b * tr + r]
-    const int items = nr * bpr;
-    for (int i = tid; i < items; i += NT) {
-      int r = i / bpr;
-      int b = i - r * bpr;
-      uint32_t o = skew + (uint32_t)i * F::BS;
-      float c;
-      if constexpr (FMT == kQ8_0) c = block_q8_0_scalar(lds_w, o, xq, xd, b);
-      else if constexpr (FMT == kQ4K) c = block_q4k_scalar(lds_w, o, xq, xd, xe, b);
-      else c = block_q6k_scalar(lds_w, o, xq, xd, xe, b);
-      u[b * tr + r] = c;
-    }
-    __syncthreads();
-    // The reference's `sumf += contribution` chain, in block order.
-    for (int r = tid; r < nr; r += NT) {
-      float sacc = 0.0f;
-      for (int b = 0; b < bpr; b++) sacc = sacc + u[b * tr + r];
-      Y[row0 + r] = sacc;
-    }
-  } else {
-    const int rowbytes = bpr * F::BS;
-    for (int li = tid; li < nr * 8; li += NT) {
-      int r = li >> 3, k = li & 7;
-      uint32_t o_row = skew + (uint32_t)(r * rowbytes);
-      float acc, acc_min = 0.0f;
-      if constexpr (FMT == kQ8_0) acc = lane_q8_0_avx2(lds_w, o_row, bpr, k, xq, xd);
-      else if constexpr (FMT == kQ4K) acc = lane_q4k_avx2(lds_w, o_row, bpr, k, xq, xd, xe, &acc_min);
-      else acc = lane_q6k_avx2(lds_w, o_row, bpr, k, xq, xd, xe);
-      // hsum256: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7))
-      float h = acc + __shfl_xor(acc, 4);
-      h = h + __shfl_xor(h, 2);
-      h = h + __shfl_xor(h, 1);
-      if (k == 0) Y[row0 + r] = h - acc_min;
-    }
+  const int rowbytes = bpr * F::BS;
+  for (int li = tid; li < nr * 8; li += NT) {
+    int r = li >> 3, k = li & 7;
+    uint32_t o_row = skew + (uint32_t)(r * rowbytes);
+    float acc, acc_min = 0.0f;
+    if constexpr (FMT == kQ8_0) acc = lane_q8_0_avx2(lds_w, o_row, bpr, k, xq, xd);
+    else if constexpr (FMT == kQ4K) acc = lane_q4k_avx2(lds_w, o_row, bpr, k, xq, xd, xe, &acc_min);
+    else acc = lane_q6k_avx2(lds_w, o_row, bpr, k, xq, xd, xe);
+    // hsum256: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7))
+    float h = acc + __shfl_xor(acc, 4);
+    h = h + __shfl_xor(h, 2);
+    h = h + __shfl_xor(h, 1);
+    if (k == 0) Y[row0 + r] = h - acc_min;
   }
 }
 
@@ -469,7 +392,7 @@ __global__ __launch_bounds__(NT) void block_sums_kernel(const uint8_t* __restric
   const int tid = threadIdx.x;
   const int row0 = blockIdx.x * tr;
   const int nr = min(tr, rows - row0);
-  const TileGeom<FMT> G(bpr, tr, false);
+  const TileGeom<FMT> G(bpr, tr);
   const uint32_t skew = stage_all<FMT, NT, MAXC, MAXX>(W, X, bpr, row0, nr, G, smem);
   const uint8_t* lds_w = smem + G.xrep;
   const uint32_t* xq = (const uint32_t*)smem;
@@ -500,28 +423,27 @@ __global__ __launch_bounds__(NT) void block_sums_kernel(const uint8_t* __restric
 // ---- host-side launch ------------------------------------------------------------
 
 // Rows per workgroup: as many as fit a 48 KiB weight tile and the 64 KiB LDS
-// budget (AVX2 order: at most NT/8, one lane per (row, k)).
+// budget; `lanes8`: at most NT/8, one lane per (row, k) of the AVX2 order.
 template <int FMT>
-static int pick_tile_rows(int rows, int bpr, bool scalar, int cap) {
+static int pick_tile_rows(int rows, int bpr, bool lanes8, int cap) {
   const size_t rowbytes = (size_t)bpr * Fmt<FMT>::BS;
   const size_t max_tile = (size_t)kMatvecNT * kMatvecMaxC * 16 - 32;
   int tr = (int)(max_tile / rowbytes);
-  if (!scalar && tr > kMatvecNT / 8) tr = kMatvecNT / 8;
+  if (lanes8 && tr > kMatvecNT / 8) tr = kMatvecNT / 8;
   if (cap > 0 && cap < tr) tr = cap;
   if (tr > rows) tr = rows;
-  while (tr > 0 && TileGeom<FMT>(bpr, tr, scalar).total() > kLdsLimit) tr--;
+  while (tr > 0 && TileGeom<FMT>(bpr, tr).total() > kLdsLimit) tr--;
   return tr;
 }
 
-template <int FMT, int ORDER>
-static int launch_matvec_t(const MatvecLaunch& L) {
-  const bool scalar = ORDER == kOrderScalar;
-  const int tr = pick_tile_rows<FMT>(L.rows, L.bpr, scalar, L.tile_rows);
+template <int FMT>
+static int launch_matvec_avx2(const MatvecLaunch& L) {
+  const int tr = pick_tile_rows<FMT>(L.rows, L.bpr, true, L.tile_rows);
   if (tr <= 0) return NRQ_LAUNCH_TOO_WIDE;
   const int grid = (L.rows + tr - 1) / tr;
-  const size_t lds = TileGeom<FMT>(L.bpr, tr, scalar).total();
-  hipLaunchKernelGGL((matvec_kernel<FMT, ORDER, kMatvecNT, kMatvecMaxC, kMatvecMaxX>), dim3(grid), dim3(kMatvecNT),
-                     lds, (hipStream_t)L.stream, (const uint8_t*)L.w, (const uint8_t*)L.x, L.y, L.rows, L.bpr, tr);
+  const size_t lds = TileGeom<FMT>(L.bpr, tr).total();
+  hipLaunchKernelGGL((matvec_avx2_kernel<FMT, kMatvecNT, kMatvecMaxC, kMatvecMaxX>), dim3(grid), dim3(kMatvecNT), lds,
+                     (hipStream_t)L.stream, (const uint8_t*)L.w, (const uint8_t*)L.x, L.y, L.rows, L.bpr, tr);
   return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
 }
 
@@ -530,7 +452,7 @@ static int launch_block_sums_t(const void* w, const void* x, int32_t* out, int r
   const int tr = pick_tile_rows<FMT>(rows, bpr, false, 0);
   if (tr <= 0) return NRQ_LAUNCH_TOO_WIDE;
   const int grid = (rows + tr - 1) / tr;
-  const size_t lds = TileGeom<FMT>(bpr, tr, false).total();
+  const size_t lds = TileGeom<FMT>(bpr, tr).total();
   hipLaunchKernelGGL((block_sums_kernel<FMT, kMatvecNT, kMatvecMaxC, kMatvecMaxX>), dim3(grid), dim3(kMatvecNT), lds,
                      (hipStream_t)stream, (const uint8_t*)w, (const uint8_t*)x, out, rows, bpr, tr);
   return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
@@ -546,18 +468,10 @@ int launch_block_sums(int dtype, const void* w, const void* x, int32_t* out, int
 
 int launch_matvec(int dtype, int order, const MatvecLaunch& L) {
   if (L.rows <= 0 || L.bpr <= 0) return 0;
-  if (order == kOrderScalar && (L.variant == 0 || L.variant == 4)) return launch_wstream_scalar(dtype, L);
-  if (order == kOrderScalar && L.variant == 3) return launch_stream_scalar(dtype, L);
-  if (order == kOrderScalar && L.variant == 2) return launch_decode_scalar(dtype, L);
-  if (order == kOrderScalar) {
-    if (dtype == kQ8_0) return launch_matvec_t<kQ8_0, kOrderScalar>(L);
-    if (dtype == kQ4K) return launch_matvec_t<kQ4K, kOrderScalar>(L);
-    if (dtype == kQ6K) return launch_matvec_t<kQ6K, kOrderScalar>(L);
-  } else {
-    if (dtype == kQ8_0) return launch_matvec_t<kQ8_0, kOrderAvx2>(L);
-    if (dtype == kQ4K) return launch_matvec_t<kQ4K, kOrderAvx2>(L);
-    if (dtype == kQ6K) return launch_matvec_t<kQ6K, kOrderAvx2>(L);
-  }
+  if (order == kOrderScalar) return launch_wstream_scalar(dtype, L);
+  if (dtype == kQ8_0) return launch_matvec_avx2<kQ8_0>(L);
+  if (dtype == kQ4K) return launch_matvec_avx2<kQ4K>(L);
+  if (dtype == kQ6K) return launch_matvec_avx2<kQ6K>(L);
   return NRQ_LAUNCH_BAD_ARG;
 }
 

@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -153,6 +154,15 @@ __device__ __forceinline__ void quant_q8_0_lane(float v, int lane32, uint8_t* __
 enum { CTL_TOKEN = 0, CTL_POS = 1, CTL_STEP = 2, CTL_WORDS = 4 };
 
 // ---- kernels ------------------------------------------------------------------------
+
+// ctl[i0] = v0 and, when i1 >= 0, ctl[i1] = v1. Host values reach the control
+// words as kernel arguments, so no host buffer has to outlive the enqueueing call.
+__global__ void ctl_set_kernel(int* __restrict__ ctl, int i0, int v0, int i1, int v1) {
+  if (threadIdx.x == 0) {
+    ctl[i0] = v0;
+    if (i1 >= 0) ctl[i1] = v1;
+  }
+}
 
 // QMat::dequant_row (infer.rs:36-56), element i of row `row` (cols values):
 //  Q8_0 (q8.rs:47-55): f32(q) * d;
@@ -1353,8 +1363,15 @@ int matvec_group(nrq_model* m, const Mat* const* ws, float* const* ys, const int
         y[t - i] = ys[t];
         r[t - i] = rows[t];
       }
-      if (nrq::launch_wstream_group(ws[i]->dt, w, y, r, j - i, xq, cols / qk_of(ws[i]->dt), m->stream))
+      const int g = nrq::launch_wstream_group(ws[i]->dt, w, y, r, j - i, xq, cols / qk_of(ws[i]->dt), m->stream);
+      if (g == nrq::NRQ_LAUNCH_TOO_WIDE) {  // one launch per matrix, as the ungrouped step runs them
+        for (int t = i; t < j; t++) {
+          int rc = matvec(m, *ws[t], xq, ys[t], rows[t], cols);
+          if (rc) return rc;
+        }
+      } else if (g) {
         return mfail(NRQ_ERR_DEVICE, "model: grouped matvec launch failed");
+      }
     } else {
       int rc = matvec(m, *ws[i], xq, ys[i], rows[i], cols);
       if (rc) return rc;
@@ -1392,6 +1409,11 @@ int fused_norm_group(nrq_model* m, float** xr, float** xo, const float* add, con
   if (rc) return mfail(NRQ_ERR_DEVICE, "model: norm + matvec launch failed");
   if (add) std::swap(*xr, *xo);
   return NRQ_OK;
+}
+
+int set_ctl(nrq_model* m, int i0, int v0, int i1 = -1, int v1 = 0) {
+  hipLaunchKernelGGL(nrq::ctl_set_kernel, dim3(1), dim3(64), 0, m->stream, m->ctl, i0, v0, i1, v1);
+  return hipGetLastError() == hipSuccess ? NRQ_OK : mfail(NRQ_ERR_DEVICE, "model: control word launch failed");
 }
 
 // muP logit scale (infer.rs:589-591): logits *= 1/logit_scale when it is not 1
@@ -1704,8 +1726,11 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
   if (c.dim <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 || c.ffn_dim <= 0 ||
       c.vocab <= 0 || c.ctx <= 0)
     return mfail(NRQ_ERR_SHAPE, "nrq_model_create: non-positive dimension");
+  // products in 64 bits: the buffers below are indexed with int
+  if ((long long)c.n_heads * c.head_dim > INT_MAX || (long long)c.n_kv_heads * c.head_dim > INT_MAX)
+    return mfail(NRQ_ERR_UNSUPPORTED, "nrq_model_create: attention width does not fit an int");
   if (c.n_heads % c.n_kv_heads || c.head_dim % 32 || c.head_dim > 128 || c.dim % 256 || c.ffn_dim % 256 ||
-      (c.n_heads * c.head_dim) % 256)
+      ((long long)c.n_heads * c.head_dim) % 256)
     return mfail(NRQ_ERR_UNSUPPORTED, "nrq_model_create: head or width layout not supported");
   if (c.dim > nrq::kNormMax || c.ctx > nrq::kAttMaxCtx)
     return mfail(NRQ_ERR_UNSUPPORTED, "nrq_model_create: dim or context larger than the kernels' LDS buffers");
@@ -1905,8 +1930,7 @@ int nrq_model_forward(nrq_model* m, uint32_t token, float* logits_host) {
   // infer.rs:513: assert!(pos < d.ctx, "context window exhausted")
   if (m->host_pos >= m->cfg.ctx) return mfail(NRQ_ERR_SHAPE, "assertion failed: pos < d.ctx: context window exhausted");
   if (token >= (uint32_t)m->cfg.vocab) return mfail(NRQ_ERR_ARG, "nrq_model_forward: token out of vocabulary");
-  const int tok = (int)token;
-  MHIP(hipMemcpyAsync(m->ctl + nrq::CTL_TOKEN, &tok, 4, hipMemcpyHostToDevice, m->stream));
+  if ((rc = set_ctl(m, nrq::CTL_TOKEN, (int)token))) return rc;
   uint32_t* keep = m->out_tokens;
   m->out_tokens = nullptr;
   rc = enqueue_step(m);
@@ -1935,12 +1959,13 @@ int nrq_model_prefill(nrq_model* m, const uint32_t* tokens, int n, float* logits
     const int B = std::min(kMaxBatch, n - i0);
     const int base = m->host_pos;
     MHIP(hipMemcpyAsync(m->btok, tokens + i0, (size_t)B * 4, hipMemcpyHostToDevice, m->stream));
-    MHIP(hipMemcpyAsync(m->ctl + nrq::CTL_POS, &base, 4, hipMemcpyHostToDevice, m->stream));
-    if ((rc = enqueue_prefill(m, B))) return rc;
-    const int next = base + B;
-    MHIP(hipMemcpyAsync(m->ctl + nrq::CTL_POS, &next, 4, hipMemcpyHostToDevice, m->stream));
-    MHIP(hipStreamSynchronize(m->stream));  // the host values copied above stay valid until here
-    m->host_pos = next;
+    if ((rc = set_ctl(m, nrq::CTL_POS, base)) || (rc = enqueue_prefill(m, B)) ||
+        (rc = set_ctl(m, nrq::CTL_POS, base + B))) {
+      hipStreamSynchronize(m->stream);  // the token copy reads the caller's array
+      return rc;
+    }
+    MHIP(hipStreamSynchronize(m->stream));
+    m->host_pos = base + B;
   }
   if (logits_host)
     MHIP(hipMemcpyAsync(logits_host, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost, m->stream));
@@ -1968,10 +1993,7 @@ int nrq_model_generate(nrq_model* m, uint32_t token, int n, uint32_t* out_tokens
       m->graph = nullptr;
     }
   }
-  const int tok = (int)token;
-  MHIP(hipMemcpyAsync(m->ctl + nrq::CTL_TOKEN, &tok, 4, hipMemcpyHostToDevice, m->stream));
-  const int zero = 0;
-  MHIP(hipMemcpyAsync(m->ctl + nrq::CTL_STEP, &zero, 4, hipMemcpyHostToDevice, m->stream));
+  if ((rc = set_ctl(m, nrq::CTL_TOKEN, (int)token, nrq::CTL_STEP, 0))) return rc;
   if (!m->exec) {
     MHIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
     rc = enqueue_step(m);
@@ -1990,11 +2012,15 @@ int nrq_model_generate(nrq_model* m, uint32_t token, int n, uint32_t* out_tokens
     m->graph = g;
     m->exec = x;
   }
-  for (int i = 0; i < n; i++) MHIP(hipGraphLaunch(m->exec, m->stream));
-  MHIP(hipMemcpyAsync(out_tokens, m->out_tokens, (size_t)n * 4, hipMemcpyDeviceToHost, m->stream));
-  if (last_logits)
-    MHIP(hipMemcpyAsync(last_logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost, m->stream));
-  MHIP(hipStreamSynchronize(m->stream));
+  // every copy into the caller's buffers completes before this returns, on error too
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < n && e == hipSuccess; i++) e = hipGraphLaunch(m->exec, m->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(out_tokens, m->out_tokens, (size_t)n * 4, hipMemcpyDeviceToHost, m->stream);
+  if (e == hipSuccess && last_logits)
+    e = hipMemcpyAsync(last_logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost, m->stream);
+  const hipError_t es = hipStreamSynchronize(m->stream);
+  MHIP(e);
+  MHIP(es);
   m->host_pos += n;
   return NRQ_OK;
 }

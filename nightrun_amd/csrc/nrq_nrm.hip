@@ -20,6 +20,7 @@
 // c0..c3 of c (n >= 4), or a carry-less multiply by a constant.
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -589,16 +590,19 @@ int nrq_model_load_nrm(const nrq_nrm* f, int ctx, int flags, nrq_model** out) {
   const nrq_nrm_meta& M = f->meta;
   if (ctx <= 0) return perr(NRQ_ERR_ARG, "nrq_model_load_nrm: ctx must be positive");
   const bool qwen = M.arch == NRQ_ARCH_QWEN3;
-  const uint32_t dim = M.dim, att = M.n_heads * M.head_dim, kvd = M.n_kv_heads * M.head_dim, ffn = M.ffn_dim;
+  // widths in 64 bits, as the reference's usize Dims (infer.rs:60-73): a header whose
+  // n_heads * head_dim wraps 32 bits then fails the shape checks below, as it does there
+  const uint64_t dim = M.dim, att = (uint64_t)M.n_heads * M.head_dim, kvd = (uint64_t)M.n_kv_heads * M.head_dim,
+                 ffn = M.ffn_dim;
   // InferCtx::new (infer.rs:378-431): every tensor present with its shape
-  auto mat = [&](int kind, int layer, uint32_t rows, uint32_t cols, const nrq_nrm_tensor_info** e) {
+  auto mat = [&](int kind, int layer, uint64_t rows, uint64_t cols, const nrq_nrm_tensor_info** e) {
     *e = find(f, kind, layer);
     if (!*e) return missing(kind_name(kind));
     if ((*e)->rows != rows || (*e)->cols != cols) return missing("bad matrix shape");
     if ((*e)->dtype == NRQ_F32) return perr(NRQ_ERR_NRM_BAD_TABLE, "BadTable");
     return NRQ_OK;
   };
-  auto vecf = [&](int kind, int layer, uint32_t len, const nrq_nrm_tensor_info** e) {
+  auto vecf = [&](int kind, int layer, uint64_t len, const nrq_nrm_tensor_info** e) {
     *e = find(f, kind, layer);
     if (!*e) return missing(kind_name(kind));
     if ((*e)->dtype != NRQ_F32)
@@ -627,7 +631,7 @@ int nrq_model_load_nrm(const nrq_nrm* f, int ctx, int flags, nrq_model** out) {
     }
     const struct {
       int kind;
-      uint32_t rows, cols;
+      uint64_t rows, cols;
     } ms[] = {{NRQ_TENSOR_ATTN_Q, att, dim}, {NRQ_TENSOR_ATTN_K, kvd, dim}, {NRQ_TENSOR_ATTN_V, kvd, dim},
               {NRQ_TENSOR_ATTN_O, dim, att}};
     for (const auto& s : ms) {
@@ -638,7 +642,7 @@ int nrq_model_load_nrm(const nrq_nrm* f, int ctx, int flags, nrq_model** out) {
     binds.push_back({NRQ_TENSOR_FFN_NORM, (int)l, NRQ_F32, e->offset});
     const struct {
       int kind;
-      uint32_t rows, cols;
+      uint64_t rows, cols;
     } fs[] = {{NRQ_TENSOR_FFN_GATE, ffn, dim}, {NRQ_TENSOR_FFN_UP, ffn, dim}, {NRQ_TENSOR_FFN_DOWN, dim, ffn}};
     for (const auto& s : fs) {
       if ((rc = mat(s.kind, l, s.rows, s.cols, &e))) return rc;
@@ -664,6 +668,11 @@ int nrq_model_load_nrm(const nrq_nrm* f, int ctx, int flags, nrq_model** out) {
     infer_freqs(M, nullptr, 0, freqs);
   }
 
+  // the device model indexes with int: every width must fit one
+  const uint64_t widths[] = {dim, M.n_layers, M.n_heads, M.n_kv_heads, M.head_dim, ffn, M.vocab, att, kvd};
+  for (uint64_t v : widths)
+    if (v == 0 || v > (uint64_t)INT_MAX)
+      return perr(NRQ_ERR_UNSUPPORTED, "nrq_model_load_nrm: a model width is zero or does not fit an int");
   nrq_model_config cfg{};
   cfg.dim = (int)dim;
   cfg.n_layers = (int)M.n_layers;

@@ -718,10 +718,12 @@ static int launch_ws_group(const void* const* w, float* const* y, const int* row
   if (ws_u_rowmajor(bpr)) {
     rc = launch_ws_t<FMT, 4, 2, kWsRowMajorU>(A, bpr, rpw, stream);
     if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, kWsRowMajorU>(A, bpr, rpw, stream);
+    if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, kWsRowMajorU>(A, bpr, 1, stream);
   } else {
     rc = FMT == kQ4K ? launch_ws_t<FMT, 8, 2, 0>(A, bpr, rpw, stream) : NRQ_LAUNCH_TOO_WIDE;
     if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 4, 2, 0>(A, bpr, rpw, stream);
     if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, 0>(A, bpr, rpw, stream);
+    if (rc == NRQ_LAUNCH_TOO_WIDE) rc = launch_ws_t<FMT, 1, 2, 0>(A, bpr, 1, stream);
   }
   return rc;
 }

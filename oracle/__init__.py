@@ -288,6 +288,7 @@ def _model_lib():
         L.nro_model_prefill_chunk.argtypes, L.nro_model_prefill_chunk.restype = [vp, C.POINTER(C.c_uint32), C.c_int], f32p
         L.nro_model_pos.argtypes, L.nro_model_pos.restype = [vp], C.c_int
         L.nro_model_reset.argtypes = [vp]
+        L.nro_model_seek.argtypes = [vp, C.c_int]
         L.nro_model_kcache.argtypes, L.nro_model_kcache.restype = [vp], C.POINTER(C.c_uint16)
         L.nro_model_vcache.argtypes, L.nro_model_vcache.restype = [vp], C.POINTER(C.c_uint16)
         L.nro_model_set_freqs.argtypes = [vp, vp]
@@ -479,6 +480,10 @@ class Model:
     @property
     def pos(self) -> int:
         return _model_lib().nro_model_pos(self.h)
+
+    def seek(self, pos: int) -> None:
+        """Timing aid: moves to `pos` without computing the cache rows before it."""
+        _model_lib().nro_model_seek(self.h, pos)
 
     def set_freqs(self, freqs: np.ndarray) -> None:
         """Replaces the rope table (head_dim/2 floats), e.g. with infer_freqs' scaled one."""

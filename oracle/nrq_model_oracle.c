@@ -411,6 +411,11 @@ void nro_model_set_qk_norm(nro_model *m, int l, const float *q_norm, const float
 
 int nro_model_pos(const nro_model *m) { return m->pos; }
 void nro_model_reset(nro_model *m) { m->pos = 0; }
+/* Timing aid for the CPU baseline: moves to position pos (< ctx) without
+ * computing the cache rows before it (they keep their contents). */
+void nro_model_seek(nro_model *m, int pos) {
+    if (pos >= 0 && pos < m->ctx) m->pos = pos;
+}
 void nro_model_set_freqs(nro_model *m, const float *freqs) {
     memcpy(m->freqs, freqs, (size_t)m->head_dim / 2 * sizeof(float));
 }

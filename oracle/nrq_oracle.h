@@ -154,6 +154,7 @@ const float *nro_model_prefill_chunk(nro_model *m, const uint32_t *tokens, int n
 void nro_model_set_freqs(nro_model *m, const float *freqs);
 int nro_model_pos(const nro_model *m);
 void nro_model_reset(nro_model *m);
+void nro_model_seek(nro_model *m, int pos); /* timing aid: skips computing the rows before pos */
 const float *nro_model_logits(const nro_model *m);
 const uint16_t *nro_model_kcache(const nro_model *m);
 const uint16_t *nro_model_vcache(const nro_model *m);

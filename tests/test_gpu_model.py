@@ -148,6 +148,35 @@ def test_tiny_model_kquant_weights(gpu, oracle):
     run_pair(oracle, TINY, w, 64, prompt, 12)
 
 
+MIXES = {
+    # a Q4_K_M file: q, k, o, gate, up Q4_K; v and down Q6_K (q|k and gate|up
+    # go out as grouped launches, v alone on the other activation format)
+    "q4k_m": {"wq": 2, "wk": 2, "wv": 3, "wo": 2, "w_gate": 2, "w_up": 2, "w_down": 3},
+    # Q6_K gate|up (the Q6_K grouped launch), Q8_0 q/k/v with a Q4_K o and down
+    "q6k_ffn": {"wq": 1, "wk": 1, "wv": 1, "wo": 2, "w_gate": 3, "w_up": 3, "w_down": 2},
+    # Q8_0 gate|up into a Q4_K down (swiglu without the fused Q8_0 epilogue)
+    "q8_into_q4k": {"wq": 2, "wk": 3, "wv": 2, "wo": 1, "w_gate": 1, "w_up": 1, "w_down": 2},
+}
+
+
+@pytest.mark.parametrize("prefill", [False, True])
+@pytest.mark.parametrize("mix", sorted(MIXES))
+def test_tiny_model_format_mixes(gpu, oracle, mix, prefill):
+    """Per-matrix format mixes the grouping logic must split correctly:
+    logits, tokens and KV cache bit-identical to the oracle in decode and in
+    the batched prefill."""
+    w = oracle.gen_model(TINY, 5151)
+    shapes = oracle.layer_shapes(TINY)
+    for l, lw in enumerate(w["layers"]):
+        for i, name in enumerate(oracle.LAYER_MATS):
+            dt = MIXES[mix][name]
+            rows, cols = shapes[name]
+            lw[name] = oracle.gen_weights(dt, 901 + 16 * l + i, rows, cols)
+            lw["dtypes"][name] = dt
+    prompt = np.random.default_rng(7).integers(0, TINY["vocab"], 70).astype(np.uint32)
+    run_pair(oracle, TINY, w, 96, prompt, 10, prefill=prefill)
+
+
 def test_context_exhausted_panics(gpu, oracle):
     """infer.rs:513: forward past the context asserts."""
     from nightrun_amd import NrPanic

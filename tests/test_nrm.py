@@ -271,3 +271,32 @@ def test_infer_freqs_scaling_branches(oracle):
     fac = np.linspace(1.0, 40.0, hd // 2).astype(np.float32)
     want = (base / fac).view(np.uint32)
     assert np.array_equal(oracle.infer_freqs(hd, theta, 32.0, 1.0, 4.0, 8192.0, factors=fac).view(np.uint32), want)
+
+
+def test_loader_widths_do_not_wrap_32_bits():
+    """InferCtx::new computes att_dim = n_heads * head_dim in usize
+    (infer.rs:60-73, 401-404). A header with n_heads = 2^25 and head_dim = 128
+    has att_dim = 2^32; a q matrix stored with 0 rows (what 2^32 wraps to in
+    32 bits) is then a shape mismatch, MissingTensor("bad matrix shape"), and
+    the loader must stop there, before any device allocation. Host-only: the
+    check runs before the model is created."""
+    import ctypes as C
+
+    from nightrun_amd import _lib, nrm
+
+    cfg = dict(dim=256, n_layers=1, n_heads=1 << 25, n_kv_heads=1 << 25, head_dim=128, ffn_dim=256, vocab=4)
+    emb = bytes(4 * 256 // 32 * 34)
+    t = [(ON.TOK_EMBED, 0, 1, 4, 256, emb), (ON.OUTPUT_NORM, 0, ON.F32, 1, 256, bytes(1024)),
+         (ON.ATTN_NORM, 0, ON.F32, 1, 256, bytes(1024)), (ON.FFN_NORM, 0, ON.F32, 1, 256, bytes(1024))]
+    # q/k/v with the wrapped row count 0 and o with the wrapped column count 0: 0-byte tensors
+    t += [(ON.ATTN_Q, 0, 1, 0, 256, b""), (ON.ATTN_K, 0, 1, 0, 256, b""), (ON.ATTN_V, 0, 1, 0, 256, b""),
+          (ON.ATTN_O, 0, 1, 256, 0, b"")]
+    t += [(k, 0, 1, r, c, bytes(r * c // 32 * 34)) for k, r, c in
+          ((ON.FFN_GATE, 256, 256), (ON.FFN_UP, 256, 256), (ON.FFN_DOWN, 256, 256))]
+    blob = bytes(ON.write(ON.default_meta(**cfg, flags=ON.FLAG_TIED_EMBEDDINGS), t))
+    f = nrm.NrmFile(blob)  # Model::parse accepts it: every entry's size is its block math
+    h = C.c_void_p()
+    rc = _lib.lib().nrq_model_load_nrm(f.h, 64, 0, C.byref(h))
+    assert rc == -15 and not h.value  # NRQ_ERR_NRM_MISSING_TENSOR, no model
+    assert "bad matrix shape" in _lib.lib().nrq_last_error().decode()
+    f.close()
