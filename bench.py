@@ -7,8 +7,8 @@ Headline (`value`): the decode matvec of the Q4_K 8192 x 3072 matrix
 (Llama-3.2-3B FFN shape) against a runtime-quantized Q8_K activation. A step
 is one matvec launch over weights already resident in HBM; the K timed steps
 run back to back as one captured HIP graph. Weights come from distinct copies
-(as many as the K steps, up to 2 x the 256 MiB MALL), and a 1 GiB device copy
-runs before every replay, so no timed read can hit the MALL. `value` is
+(as many as the K steps, up to 2 x the 256 MiB MALL), and a 1 GiB read runs
+before every replay, so no timed read can hit the MALL. `value` is
 algorithmic bytes x K / the graph's wall time (HIP events on the launch
 stream); `roofline.achieved` is algorithmic bytes / the mean time per launch
 inside that graph.
@@ -102,23 +102,23 @@ def algorithmic_bytes(dtype, rows, cols, batch=1):
 
 
 class MallFlush:
-    """A 1 GiB device-to-device copy (reads 512 MiB, writes 512 MiB: four times
-    the 256 MiB MALL), run untimed before a measured region so that none of the
-    weights it reads can still be cached there."""
+    """A read of 1 GiB (four times the 256 MiB MALL), run untimed before a
+    measured region so that none of the weights it reads can still be cached
+    there. It only reads (a sum), so it leaves no dirty lines whose write-back
+    the measured kernels would pay for."""
 
-    BYTES = 512 << 20
+    BYTES = 1 << 30
 
     def __init__(self):
         import torch
 
-        self.src = torch.ones(self.BYTES, dtype=torch.uint8, device="cuda")
-        self.dst = torch.empty_like(self.src)
+        self.buf = torch.ones(self.BYTES // 4, dtype=torch.float32, device="cuda")
 
     def __call__(self, stream):
         import torch
 
         with torch.cuda.stream(stream):
-            self.dst.copy_(self.src)
+            self.out = self.buf.sum()
 
 
 def graph_time(stream, launch, k, flush=None):
@@ -626,7 +626,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--also", default="cfg1,cfg3", help="other matvec configs reported beside (comma list)")
-    ap.add_argument("--qwen3-only", action="store_true", help="only the Qwen3-4B decode/prefill leg (profiling)")
+    ap.add_argument("--qwen3-only", action="store_true", help="only the Qwen3-4B decode/prefill leg")
+    ap.add_argument("--no-qwen3", action="store_true", help="skip the Qwen3-4B decode/prefill leg")
     ap.add_argument("--prefill-only", type=int, default=0, metavar="TOKENS",
                     help="only time nrq_model_prefill of TOKENS tokens on the Llama-3.2-1B-shape model")
     ap.add_argument("--crc-only", type=int, default=0, metavar="BYTES",
@@ -685,7 +686,7 @@ def main():
     prefill = None if args.no_prefill else measure_prefill()
     decode = None if args.no_decode else measure_decode()
     qwen3 = None
-    if not args.no_decode:
+    if not args.no_decode and not args.no_qwen3:
         try:
             qwen3 = measure_qwen3()
         except Exception as e:  # reported, never fatal to the bench line
