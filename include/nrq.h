@@ -241,6 +241,17 @@ int nrq_model_sampler_state(nrq_model *m, uint64_t *state);
  * > 0. Enqueued on `stream`. */
 int nrq_dev_sample(const float *logits, int n, float temperature, float top_p, uint64_t *rng, uint32_t *token,
                    void *stream);
+/* nrq_dev_sample without allocation. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The partial
+ * top-64 lists go to a fixed 128 KiB array per device, held until the process
+ * ends, instead of stream-ordered memory; n is at most 524288 logits (else
+ * NRQ_ERR_UNSUPPORTED). The array belongs to the current device, and `stream`
+ * (NULL = the null stream) must be on that device. Every call on a device
+ * shares the array: calls that overlap on one device (different streams or
+ * threads) race and must not run concurrently. Same results as nrq_dev_sample. */
+int nrq_dev_sample_noalloc(const float *logits, int n, float temperature, float top_p, uint64_t *rng,
+                           uint32_t *token, void *stream);
 /* Copies the f16 KV cache ([n_layers][ctx][kv_dim] each) to host buffers. */
 int nrq_model_kv_cache(nrq_model *m, void *k, void *v, size_t bytes);
 int nrq_model_destroy(nrq_model *m);

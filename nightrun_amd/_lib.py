@@ -70,6 +70,7 @@ SIGNATURES = {
     "nrq_model_set_sampler": ([_vp, C.c_float, C.c_float, C.c_uint64], _i),
     "nrq_model_sampler_state": ([_vp, C.POINTER(C.c_uint64)], _i),
     "nrq_dev_sample": ([_vp, _i, C.c_float, C.c_float, _vp, _vp, _vp], _i),
+    "nrq_dev_sample_noalloc": ([_vp, _i, C.c_float, C.c_float, _vp, _vp, _vp], _i),
     "nrq_nrm_open": ([_vp, _sz, C.POINTER(_vp)], _i),
     "nrq_nrm_get_meta": ([_vp, _vp], _i),
     "nrq_nrm_entry": ([_vp, C.c_uint32, _vp], _i),

@@ -227,6 +227,11 @@ int nrq_init(int device) {
     return fail(NRQ_ERR_DEVICE, "nrq_init: device %d is %s, libnrq is built for gfx950 only", device, prop.gcnArchName);
   HIP_TRY(hipSetDevice(device));
   HIP_TRY(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
+  if (nrq::sample_scratch_setup() != NRQ_OK) {
+    hipStreamDestroy(s.stream);
+    s.stream = nullptr;
+    return NRQ_ERR_DEVICE;
+  }
   s.device = device;
   s.init = true;
   g_err.clear();

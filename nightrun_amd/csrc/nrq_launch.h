@@ -107,5 +107,8 @@ int launch_block_sums(int dtype, const void* w, const void* x, int32_t* out, int
 void set_last_error(const char* msg);
 // The model frees `dev` (a hipMalloc'd buffer its tensors point into) when destroyed.
 void model_adopt_buffer(nrq_model* m, void* dev);
+// Looks up the current device's address of the sampler's fixed scratch
+// (nrq_model.hip), so that nrq_dev_sample_noalloc needs no lookup later.
+int sample_scratch_setup();
 
 }  // namespace nrq

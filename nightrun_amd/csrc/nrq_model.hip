@@ -23,6 +23,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
@@ -1226,6 +1227,53 @@ __global__ void mathf_kernel(int fn, const float* __restrict__ x, float* __restr
 }  // namespace
 }  // namespace nrq
 
+// ---- the sampler's fixed scratch (nrq_dev_sample_noalloc) ------------------------------
+// The partial top-64 lists of top64_part_kernel for callers that cannot
+// allocate: one array per device, 128 KiB, held until the process ends. Every
+// call on a device shares it and leaves its lists there; top64_sample_kernel
+// reads only the lists the same call's top64_part_kernel wrote, so nothing
+// needs clearing. In host code `scratch` is a host-side stand-in: only the
+// per-device address from hipGetSymbolAddress is passed to kernels.
+namespace nrq {
+constexpr int kSampleMaxLogits = 1 << 19;
+constexpr int kSampleScratchLists = kSampleMaxLogits / kSelSlice;
+}  // namespace nrq
+static __device__ __align__(256) unsigned long long scratch[nrq::kSampleScratchLists * nrq::kTopK];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kScratchDevices];  // address of `scratch` on each device, once looked up
+
+// The address of this device's `scratch` (the device must be current).
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+    nrq::set_last_error("sampler scratch: no usable current device");
+    return NRQ_ERR_DEVICE;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      nrq::set_last_error((std::string("sampler scratch: hipGetSymbolAddress: ") + hipGetErrorString(e)).c_str());
+      return NRQ_ERR_DEVICE;
+    }
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return NRQ_OK;
+}
+}  // namespace
+
+namespace nrq {
+int sample_scratch_setup() {
+  void* p = nullptr;
+  return scratch_on_current_device(&p);
+}
+}  // namespace nrq
+
 // ---- host side -----------------------------------------------------------------------
 
 namespace {
@@ -1912,6 +1960,36 @@ int nrq_dev_sample(const float* logits, int n, float temperature, float top_p, u
                        token, 1);
   }
   return hipGetLastError() == hipSuccess ? NRQ_OK : mfail(NRQ_ERR_DEVICE, "nrq_dev_sample: launch failed");
+}
+
+int nrq_dev_sample_noalloc(const float* logits, int n, float temperature, float top_p, uint64_t* rng,
+                           uint32_t* token, void* stream) {
+  if (!logits || !token || (temperature > 0.0f && !rng))
+    return mfail(NRQ_ERR_ARG, "nrq_dev_sample_noalloc: null pointer");
+  if (n <= 0) return mfail(NRQ_ERR_ARG, "nrq_dev_sample_noalloc: empty logits");
+  if (n > nrq::kSampleMaxLogits)
+    return mfail(NRQ_ERR_UNSUPPORTED, "nrq_dev_sample_noalloc: more than 524288 logits (its fixed scratch holds "
+                                      "the partial lists of at most that many)");
+  hipStream_t s = (hipStream_t)stream;
+  if (temperature <= 0.0f) {  // argmax: no scratch
+    hipLaunchKernelGGL(nrq::argmax_kernel, dim3(1), dim3(nrq::kArgNT), 0, s, logits, n, nullptr, token, 1);
+    return hipGetLastError() == hipSuccess ? NRQ_OK : mfail(NRQ_ERR_DEVICE, "nrq_dev_sample_noalloc: launch failed");
+  }
+  if (s) {  // the scratch used is the current device's: the stream must be on it
+    int sdev = -1, cur = -1;
+    if (hipStreamGetDevice(s, &sdev) != hipSuccess || hipGetDevice(&cur) != hipSuccess || sdev != cur)
+      return mfail(NRQ_ERR_ARG, "nrq_dev_sample_noalloc: the stream is not on the current device");
+  }
+  void* part = nullptr;
+  int rc = scratch_on_current_device(&part);
+  if (rc) return rc;
+  const int np = (n + nrq::kSelSlice - 1) / nrq::kSelSlice;
+  hipLaunchKernelGGL(nrq::top64_part_kernel, dim3(np), dim3(nrq::kSelPartWaves * 64), 0, s, logits, n,
+                     (unsigned long long*)part);
+  hipLaunchKernelGGL(nrq::top64_sample_kernel, dim3(1), dim3(nrq::kSelWaves * 64), 0, s,
+                     (const unsigned long long*)part, np, logits, temperature, top_p, (unsigned long long*)rng, nullptr,
+                     nullptr, 0, token);
+  return hipGetLastError() == hipSuccess ? NRQ_OK : mfail(NRQ_ERR_DEVICE, "nrq_dev_sample_noalloc: launch failed");
 }
 
 int nrq_model_reset(nrq_model* m) {
