@@ -5,8 +5,8 @@
 // so y[t][r] equals the per-token matvec bit for bit, as kquant_matmul! and
 // matmul_q8 guarantee (kquant.rs:566-639, kernels.rs:91-143).
 //
-// Tiles. A wave owns 32 weight rows x 32 tokens (v_mfma_i32_32x32x16_i8: lane l
-// holds row l % 32 and 16 tokens, so a row's scales stay in one lane and one
+// Tiles. A wave owns 32 weight rows x 32 tokens (32x32 int8 MFMA: lane l holds
+// row l % 32 and 16 tokens, so a row's scales stay in one lane and one
 // unpacked weight operand serves 16 outputs per lane). A workgroup is KS waves
 // over the same tile, splitting its blocks: in round k, wave s takes block
 // KS*k + s. With KS = 1 the reference's `sumf +=` chain runs in registers; with
@@ -14,16 +14,19 @@
 // round's barrier, the wave that owns an element adds the KS contributions in
 // block order.
 //
-// Loads. Each lane reads what its MFMA operands need straight into registers,
-// one block ahead of use (from a second register buffer, or into the current
-// one once its operands are consumed): its token's 16 activation bytes of each Q4_K
-// sub-block (one 16-byte load per sub-block) or 8 bytes of each Q6_K group,
-// and its row's weight bytes for the same K positions. Inside a Q4_K
-// sub-block, MFMA step h of lane half kg covers elements 32j + 16kg + 8h .. +8,
-// so both operands are contiguous (the sub-block's integer dot is exact in any
-// order). The token values the f32 steps need per output element (bsum pair
-// sums, d) pass through a small per-wave LDS table, from the lane that loaded
-// the token to the lanes that hold its outputs.
+// Loads, one block ahead of use (from a second register buffer, or into the
+// current one once its operands are consumed). Weights: each lane reads its
+// row's bytes for its MFMA K positions straight into registers. K-quant
+// activations: the wave reads its 32 tokens' Q8_K blocks as consecutive
+// 16-byte windows (about three whole blocks per load instruction, where one
+// 16-byte operand per lane would touch 32 tokens' lines) and writes them to
+// its LDS stage, from where each lane reads its operands: 16 bytes per Q4_K
+// sub-block, one v_mfma_i32_32x32x32_i8 step, or 8 bytes per Q6_K group, one
+// v_mfma_i32_32x32x16_i8 step. A and B take the same K positions per lane
+// half, so a step sums exactly the sub-block's (group's) products. The token
+// values the f32 steps need per output element (d) pass through a small
+// per-wave LDS table, from the lane that read the token to the lanes that
+// hold its outputs.
 //
 // f32 steps. Q4_K's sum_q += f32(sc_j) * f32(sub_j): each product is an
 // integer below 63 * 61440 < 2^22, so the first four partial sums are exact
@@ -56,6 +59,17 @@ __device__ __forceinline__ i32x16 md_mfma(uint32_t a0, uint32_t a1, uint32_t b0,
   return __builtin_amdgcn_mfma_i32_32x32x16_i8(a, b, c, 0, 0, 0);
 }
 
+// One 32-value Q4_K sub-block per step (gfx950 v_mfma_i32_32x32x32_i8): lane
+// half kg supplies the same 16 K positions of both operands, so the step sums
+// exactly the sub-block's 32 products.
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x16 md_mfma32(const u32x4& a, uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3,
+                                            i32x16 c) {
+  const i32x4v av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w};
+  const i32x4v bv = {(int)b0, (int)b1, (int)b2, (int)b3};
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ void md_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x7f | (0 << 8) | (3 << 14));  // this wave's LDS accesses are done
@@ -86,13 +100,20 @@ constexpr int kMdScalDw = 160;
 // Registers one block needs, loaded one block ahead of use.
 template <int FMT>
 struct MdLoad;
+// K-quant activation tiles move as 16-byte windows: 19 per token (qs in 16,
+// then bsums in 2, then one holding d), window i of lane l being number
+// 64i + l of the tile's 32 x 19, so that each load instruction reads about
+// three whole token blocks. The wave writes them to its LDS stage in the same
+// order (token t at 304t: qs at +0, bsums at +256, d at +288), from where
+// every lane reads its MFMA operands.
+constexpr int kMdWin = 19, kMdTokB = 16 * kMdWin, kMdStage = 32 * kMdTokB;
+constexpr int kMdXi = (32 * kMdWin + 63) / 64;  // window loads per lane (10)
+
 template <>
 struct MdLoad<kQ4K> {
-  u32x4a a[8];  // activation: sub-block j, bytes 32j + 16kg .. +16
-  u32x4a bs;    // bsums 8kg .. 8kg+7 (dwords 65 + 4kg .. +4)
-  uint32_t d;   // activation d (f32 bits)
-  u32x4 h;      // weight header: d | dmin, scales[12]
-  u32x4 q[4];   // qs bytes 32cc + 16kg .. +16
+  u32x4a x[kMdXi];  // activation windows
+  u32x4 h;          // weight header: d | dmin, scales[12]
+  u32x4 q[4];       // qs bytes 32cc + 16kg .. +16
 };
 template <>
 struct MdLoad<kQ8_0> {
@@ -105,24 +126,51 @@ struct MdLoad<kQ8_0> {
 };
 template <>
 struct MdLoad<kQ6K> {
-  u32x2a a[16];  // activation: group G, bytes 16G + 8kg .. +8
-  uint32_t d;
+  u32x4a x[kMdXi];  // activation windows, as for Q4_K
   u32x3a w[12];  // aligned 12-byte windows [hh][u][ql low planes, ql high planes, qh]
   u32x4a s;      // aligned window over scales[16] ...
   uint32_t s4;   // ... and d
 };
 
+// xb: Q8_0 — this lane's token's block; K-quants — the tile's block column
+// (its first token's block), with xo the lane's window offsets from it.
 template <int FMT>
 __device__ __forceinline__ void md_load(MdLoad<FMT>& L, const uint8_t* __restrict__ xb, const uint8_t* __restrict__ wb,
-                                        int kg);
+                                        int kg, const uint32_t* xo);
+
+__device__ __forceinline__ void md_load_windows(u32x4a (&x)[kMdXi], const uint8_t* __restrict__ xb,
+                                                const uint32_t* xo) {
+#pragma unroll
+  for (int i = 0; i < kMdXi; i++) x[i] = *(const u32x4a*)(xb + xo[i]);
+}
+
+// The lane's windows into the wave's stage (the last load's upper half-wave
+// holds repeats and is not written).
+__device__ __forceinline__ void md_stage(const u32x4a (&x)[kMdXi], uint8_t* stg, int lane) {
+#pragma unroll
+  for (int i = 0; i < kMdXi; i++) {
+    const int idx = 64 * i + lane;
+    if (i < kMdXi - 1 || idx < 32 * kMdWin) *(u32x4*)(stg + 16 * idx) = (u32x4)x[i];
+  }
+}
+
+// Byte offsets of the lane's windows from the tile's block column: token
+// min(t, last) of the tile, window c of its block.
+__device__ __forceinline__ void md_window_offsets(uint32_t* xo, int lane, int last, int bpr) {
+#pragma unroll
+  for (int i = 0; i < kMdXi; i++) {
+    int idx = 64 * i + lane;
+    if (idx >= 32 * kMdWin) idx -= 32;
+    const int t = idx / kMdWin, c = idx - t * kMdWin;
+    const uint32_t off = c < 16 ? 4u + 16u * (uint32_t)c : c == 16 ? 260u : c == 17 ? 276u : 0u;
+    xo[i] = (uint32_t)min(t, last) * (uint32_t)bpr * (uint32_t)kQ8KBytes + off;
+  }
+}
 
 template <>
 __device__ __forceinline__ void md_load<kQ4K>(MdLoad<kQ4K>& L, const uint8_t* __restrict__ xb,
-                                              const uint8_t* __restrict__ wb, int kg) {
-#pragma unroll
-  for (int j = 0; j < 8; j++) L.a[j] = *(const u32x4a*)(xb + 4 + 32 * j + 16 * kg);
-  L.bs = *(const u32x4a*)(xb + 260 + 16 * kg);
-  L.d = *(const uint32_t*)xb;
+                                              const uint8_t* __restrict__ wb, int kg, const uint32_t* xo) {
+  md_load_windows(L.x, xb, xo);
   L.h = *(const u32x4*)wb;
 #pragma unroll
   for (int cc = 0; cc < 4; cc++) L.q[cc] = *(const u32x4*)(wb + 16 + 32 * cc + 16 * kg);
@@ -147,7 +195,8 @@ __device__ __forceinline__ void md_q8_window(const uint8_t* __restrict__ blk, in
 
 template <>
 __device__ __forceinline__ void md_load<kQ8_0>(MdLoad<kQ8_0>& L, const uint8_t* __restrict__ xb,
-                                               const uint8_t* __restrict__ wb, int kg) {
+                                               const uint8_t* __restrict__ wb, int kg, const uint32_t* xo) {
+  (void)xo;
   md_q8_window(xb, kg, L.a, L.a4, L.ad, L.ao);
   md_q8_window(wb, kg, L.w, L.w4, L.wd, L.wo);
 }
@@ -155,9 +204,8 @@ __device__ __forceinline__ void md_load<kQ8_0>(MdLoad<kQ8_0>& L, const uint8_t* 
 // Q6_K loads by half: half 0 = groups 0-7 and their weights, plus d and the
 // scales (read at the block's start); half 1 = groups 8-15.
 __device__ __forceinline__ void md_load_q6k_half(MdLoad<kQ6K>& L, const uint8_t* __restrict__ xb,
-                                                 const uint8_t* __restrict__ wb, int kg, int hh) {
-#pragma unroll
-  for (int G = 8 * hh; G < 8 * hh + 8; G++) L.a[G] = *(const u32x2a*)(xb + 4 + 16 * G + 8 * kg);
+                                                 const uint8_t* __restrict__ wb, int kg, int hh, const uint32_t* xo) {
+  if (hh == 0) md_load_windows(L.x, xb, xo);
   const uint8_t* w4 = wb - ((uintptr_t)wb & 3u);  // the block is 2-byte aligned
 #pragma unroll
   for (int u = 0; u < 2; u++) {
@@ -167,7 +215,6 @@ __device__ __forceinline__ void md_load_q6k_half(MdLoad<kQ6K>& L, const uint8_t*
     L.w[6 * hh + 3 * u + 2] = *(const u32x3a*)(w4 + 128 + 32 * hh + l0);  // qh[32hh + l]
   }
   if (hh == 0) {
-    L.d = *(const uint32_t*)xb;
     L.s = *(const u32x4a*)(w4 + 192);
     L.s4 = *(const uint32_t*)(w4 + 208);
   }
@@ -175,17 +222,20 @@ __device__ __forceinline__ void md_load_q6k_half(MdLoad<kQ6K>& L, const uint8_t*
 
 template <>
 __device__ __forceinline__ void md_load<kQ6K>(MdLoad<kQ6K>& L, const uint8_t* __restrict__ xb,
-                                              const uint8_t* __restrict__ wb, int kg) {
-  md_load_q6k_half(L, xb, wb, kg, 0);
-  md_load_q6k_half(L, xb, wb, kg, 1);
+                                              const uint8_t* __restrict__ wb, int kg, const uint32_t* xo) {
+  md_load_q6k_half(L, xb, wb, kg, 0, xo);
+  md_load_q6k_half(L, xb, wb, kg, 1, xo);
 }
 
 // Q4_K block: contributions c[e] of this lane's 16 outputs (row l % 32,
 // tile tokens 8(e/4) + 4kg + e%4). `ta` is this lane's operand token.
 // prefetch() runs once L is no longer read (it loads the next block into L).
 template <typename PF>
-__device__ __forceinline__ void md_q4k(MdLoad<kQ4K>& L, uint32_t* scal, int ta, int kg, float c[16], PF prefetch) {
-  if (kg == 0) scal[128 + ta] = L.d;  // token ta's d
+__device__ __forceinline__ void md_q4k(MdLoad<kQ4K>& L, uint8_t* stg, uint32_t* scal, int ta, int kg, float c[16],
+                                       PF prefetch) {
+  md_stage(L.x, stg, ta + 32 * kg);
+  const uint8_t* at = stg + ta * kMdTokB;  // operand token ta in the stage
+  if (kg == 0) scal[128 + ta] = *(const uint32_t*)(at + 288);  // token ta's d
   const u32x4 h = L.h;
   // kquant.rs:83-92, four scales or mins per word
   const uint32_t scA = h.y & 0x3f3f3f3fu, mnA = h.z & 0x3f3f3f3fu;
@@ -196,7 +246,8 @@ __device__ __forceinline__ void md_q4k(MdLoad<kQ4K>& L, uint32_t* scal, int ta, 
   // split exactly as bsum = 128 * hi + lo (lo = low 7 bits, hi in [-16, 15]),
   // against m_{4kg}, m_{4kg}, m_{4kg+1}, ... of row l % 32.
   // (the two steps issue after the sub-block loop, whose results they would otherwise sit beside)
-  const uint32_t sb0 = L.bs[0], sb1 = L.bs[1], sb2 = L.bs[2], sb3 = L.bs[3];
+  const u32x4 bsv = *(const u32x4*)(at + 256 + 16 * kg);
+  const uint32_t sb0 = bsv.x, sb1 = bsv.y, sb2 = bsv.z, sb3 = bsv.w;
   const uint32_t mn = kg ? mnB : mnA;
   const float dw = f16_bits_to_f32(h.x & 0xffffu), dmw = f16_bits_to_f32(h.x >> 16);
   int S[16];
@@ -207,7 +258,9 @@ __device__ __forceinline__ void md_q4k(MdLoad<kQ4K>& L, uint32_t* scal, int ta, 
     const uint32_t b0 = (q.x >> sh) & 0x0f0f0f0fu, b1 = (q.y >> sh) & 0x0f0f0f0fu;
     const uint32_t b2 = (q.z >> sh) & 0x0f0f0f0fu, b3 = (q.w >> sh) & 0x0f0f0f0fu;
     const i32x16 z = {};
-    return md_mfma(L.a[j][2], L.a[j][3], b2, b3, md_mfma(md_after(L.a[j][0], dep), L.a[j][1], b0, b1, z));
+    u32x4 a = *(const u32x4*)(at + 32 * j + 16 * kg);
+    a.x = md_after(a.x, dep);
+    return md_mfma32(a, b0, b1, b2, b3, z);
   };
   float dep[16];
 #pragma unroll
@@ -303,9 +356,11 @@ __device__ __forceinline__ void md_q8(MdLoad<kQ8_0>& L, uint32_t* scal, int ta, 
 // Q6_K block, `sh` = its start's byte offset (0 or 2) past the aligned windows.
 // prefetch(half) runs once that half of L is no longer read.
 template <typename PF>
-__device__ __forceinline__ void md_q6k(MdLoad<kQ6K>& L, uint32_t sh, uint32_t* scal, int ta, int kg, float c[16],
-                                       PF prefetch) {
-  if (kg == 0) scal[128 + ta] = L.d;
+__device__ __forceinline__ void md_q6k(MdLoad<kQ6K>& L, uint32_t sh, uint8_t* stg, uint32_t* scal, int ta, int kg,
+                                       float c[16], PF prefetch) {
+  md_stage(L.x, stg, ta + 32 * kg);
+  const uint8_t* at = stg + ta * kMdTokB;  // operand token ta in the stage
+  if (kg == 0) scal[128 + ta] = *(const uint32_t*)(at + 288);
   uint32_t S[4];  // scales[16], realigned
   {
     const uint32_t sw[5] = {L.s.x, L.s.y, L.s.z, L.s.w, L.s4};
@@ -345,7 +400,8 @@ __device__ __forceinline__ void md_q6k(MdLoad<kQ6K>& L, uint32_t sh, uint32_t* s
         bq[k] = md_q6_signed(md_after(lo | hi, dep));
       }
       const i32x16 z = {};
-      return md_mfma(L.a[G][0], L.a[G][1], bq[0], bq[1], z);
+      const uint2 a = *(const uint2*)(at + 16 * G + 8 * kg);
+      return md_mfma(a.x, a.y, bq[0], bq[1], z);
     };
     i32x16 ngs = step(0, sum);
 #pragma unroll
@@ -408,11 +464,16 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* _
   const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ta = lane & 31, kg = lane >> 5;
   const int r0 = (rt - (m == 2 ? M.tile2 : m == 1 ? M.tile1 : 0)) * 32, t0 = tt * 32;
-  // rows and tokens past the end load valid memory (the last row / token) and store nothing
-  const uint8_t* xrow = X + (size_t)min(t0 + ta, batch - 1) * bpr * XS;
+  // rows and tokens past the end load valid memory (the last row / token) and store nothing;
+  // K-quants: xrow is the tile's first token's row, the lanes' windows offsets from it
+  const uint8_t* xrow = X + (size_t)min(t0 + (FMT == kQ8_0 ? ta : 0), batch - 1) * bpr * XS;
   const uint8_t* wrow = W + (size_t)min(r0 + ta, rows - 1) * bpr * BS;
+  uint32_t xo[FMT == kQ8_0 ? 1 : kMdXi];
+  if constexpr (FMT != kQ8_0) md_window_offsets(xo, lane, batch - 1 - t0, bpr);
   uint32_t* scal = lds + ks * kMdScalDw;
   float* xch = (float*)(lds + KS * kMdScalDw);  // KS > 1: [2][KS][1024], producer-lane-major
+  // K-quants: this wave's activation stage, after the exchange buffers
+  uint8_t* stg = (uint8_t*)(lds + KS * kMdScalDw + (KS > 1 ? 2 * KS * 1024 : 0)) + ks * kMdStage;
   const int nrounds = (bpr + KS - 1) / KS;
 
   float acc[KS == 1 ? 16 : OWN];
@@ -445,14 +506,15 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* _
     MdLoad<FMT> L0, L1, L2, L3;
     {
       const int b0 = min(ks, bpr - 1), b1 = min(KS + ks, bpr - 1), b2 = min(2 * KS + ks, bpr - 1);
-      md_load<FMT>(L0, xrow + (size_t)b0 * XS, wrow + (size_t)b0 * BS, kg);
-      md_load<FMT>(L1, xrow + (size_t)b1 * XS, wrow + (size_t)b1 * BS, kg);
-      md_load<FMT>(L2, xrow + (size_t)b2 * XS, wrow + (size_t)b2 * BS, kg);
+      md_load<FMT>(L0, xrow + (size_t)b0 * XS, wrow + (size_t)b0 * BS, kg, xo);
+      md_load<FMT>(L1, xrow + (size_t)b1 * XS, wrow + (size_t)b1 * BS, kg, xo);
+      md_load<FMT>(L2, xrow + (size_t)b2 * XS, wrow + (size_t)b2 * BS, kg, xo);
     }
     auto body = [&](int k, MdLoad<FMT>& cur, MdLoad<FMT>& nxt) {
       const int b = KS * k + ks;
       const int bn = min(b + 3 * KS, bpr - 1);
-      md_load<FMT>(nxt, xrow + (size_t)bn * XS, wrow + (size_t)bn * BS, kg);
+      md_load<FMT>(nxt, xrow + (size_t)bn * XS, wrow + (size_t)bn * BS, kg, xo);
+      asm volatile("" ::: "memory");  // the loads issue here, ahead of the block's compute
       if constexpr (KS > 1) {
         md_barrier();
         if (k > 0) chain_add(k - 1);
@@ -462,9 +524,9 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* _
         if constexpr (FMT == kQ8_0) {
           md_q8(cur, scal, ta, kg, c, [&]() {});
         } else if constexpr (FMT == kQ4K) {
-          md_q4k(cur, scal, ta, kg, c, [&]() {});
+          md_q4k(cur, stg, scal, ta, kg, c, [&]() {});
         } else {
-          md_q6k(cur, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), scal, ta, kg, c, [&](int) {});
+          md_q6k(cur, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), stg, scal, ta, kg, c, [&](int) {});
         }
         finish(k, c);
       }
@@ -484,12 +546,13 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* _
     MdLoad<FMT> La, Lb;
     {
       const int b0 = min(ks, bpr - 1);
-      md_load<FMT>(La, xrow + (size_t)b0 * XS, wrow + (size_t)b0 * BS, kg);
+      md_load<FMT>(La, xrow + (size_t)b0 * XS, wrow + (size_t)b0 * BS, kg, xo);
     }
     auto body = [&](int k, MdLoad<FMT>& cur, MdLoad<FMT>& nxt) {
       const int b = KS * k + ks;
       const int bn = min(b + KS, bpr - 1);
-      md_load<FMT>(nxt, xrow + (size_t)bn * XS, wrow + (size_t)bn * BS, kg);
+      md_load<FMT>(nxt, xrow + (size_t)bn * XS, wrow + (size_t)bn * BS, kg, xo);
+      asm volatile("" ::: "memory");  // the loads issue here, ahead of the block's compute
       if constexpr (KS > 1) {
         md_barrier();
         if (k > 0) chain_add(k - 1);
@@ -499,9 +562,9 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* _
         if constexpr (FMT == kQ8_0) {
           md_q8(cur, scal, ta, kg, c, [&]() {});
         } else if constexpr (FMT == kQ4K) {
-          md_q4k(cur, scal, ta, kg, c, [&]() {});
+          md_q4k(cur, stg, scal, ta, kg, c, [&]() {});
         } else {
-          md_q6k(cur, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), scal, ta, kg, c, [&](int) {});
+          md_q6k(cur, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), stg, scal, ta, kg, c, [&](int) {});
         }
         finish(k, c);
       }
@@ -518,7 +581,7 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* _
     MdLoad<FMT> L;
     {
       const int b0 = min(ks, bpr - 1);
-      md_load<FMT>(L, xrow + (size_t)b0 * XS, wrow + (size_t)b0 * BS, kg);
+      md_load<FMT>(L, xrow + (size_t)b0 * XS, wrow + (size_t)b0 * BS, kg, xo);
     }
     for (int k = 0; k < nrounds; k++) {
       const int b = KS * k + ks;
@@ -532,12 +595,12 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* _
         const uint8_t* xn = xrow + (size_t)bn * XS;
         const uint8_t* wn = wrow + (size_t)bn * BS;
         if constexpr (FMT == kQ8_0) {
-          md_q8(L, scal, ta, kg, c, [&]() { md_load<kQ8_0>(L, xn, wn, kg); });
+          md_q8(L, scal, ta, kg, c, [&]() { md_load<kQ8_0>(L, xn, wn, kg, xo); });
         } else if constexpr (FMT == kQ4K) {
-          md_q4k(L, scal, ta, kg, c, [&]() { md_load<kQ4K>(L, xn, wn, kg); });
+          md_q4k(L, stg, scal, ta, kg, c, [&]() { md_load<kQ4K>(L, xn, wn, kg, xo); });
         } else {
-          md_q6k(L, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), scal, ta, kg, c,
-                 [&](int hh) { md_load_q6k_half(L, xn, wn, kg, hh); });
+          md_q6k(L, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), stg, scal, ta, kg, c,
+                 [&](int hh) { md_load_q6k_half(L, xn, wn, kg, hh, xo); });
         }
         finish(k, c);
       }
@@ -596,7 +659,8 @@ int md_launch_t(const MatmulGroupLaunch& G) {
   const long rt_pad = (long)((nrt + 7) / 8) * 8;
   const long nwg = rt_pad * ntt;
   if (nwg > 0x7fffffffL) return NRQ_LAUNCH_BAD_ARG;
-  const size_t lds = (size_t)KS * kMdScalDw * 4 + (KS > 1 ? (size_t)2 * KS * 1024 * 4 : 0);
+  const size_t lds = (size_t)KS * kMdScalDw * 4 + (KS > 1 ? (size_t)2 * KS * 1024 * 4 : 0) +
+                     (FMT == kQ8_0 ? 0 : (size_t)KS * kMdStage);
   hipLaunchKernelGGL((mmd_kernel<FMT, KS, NB>), dim3((unsigned)nwg), dim3(64 * KS), lds, (hipStream_t)G.stream, M,
                      (const uint8_t*)G.xs, G.bpr, G.batch, ntt, nrt);
   return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
@@ -653,16 +717,17 @@ int md_group(int dtype, const MatmulGroupLaunch& G) {
 }
 
 // Register buffers of block loads. K-quants: two (a block's loads issued a
-// whole block ahead) where waves are fewest per SIMD, one split, or eight
-// splits of long Q6_K rows; else one. Q8_0: one (on the Llama-3.2-1B shapes
-// at M = 64 one buffer beat two and a ring of four by 4-20%).
+// whole block ahead) where waves are fewest per SIMD, one split; else one
+// (eight splits of the Qwen3-4B down projection: 30.4 us on one buffer, 34.1
+// on two, which spill). Q8_0: one (on the Llama-3.2-1B shapes at M = 64 one
+// buffer beat two and a ring of four by 4-20%).
 int md_buffers(int dtype, int ks) {
   const char* nb = getenv("NRQ_MMT_NB");  // tuning override: 1, 2 or 4 (4: Q8_0 only)
   if (nb && nb[0]) return atoi(nb);
   const char* env = getenv("NRQ_MMT_DB");  // tuning override: 0 (one buffer) or 1 (two)
   if (env && env[0]) return env[0] == '1' ? 2 : 1;
   if (dtype == kQ8_0) return 1;
-  return ks == 1 || (dtype == kQ6K && ks == 8) ? 2 : 1;
+  return ks == 1 ? 2 : 1;
 }
 
 }  // namespace
