@@ -409,12 +409,14 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q,
 constexpr int kAttNT = 1024;
 constexpr int kAttMaxCtx = 8192;
 constexpr int kAttProd = 8704;  // floats per product stage (head_dim x (chunk + 4) <= 8704)
+constexpr int kAttRing = 3 * 1024 * 16;  // bytes of the value ring: three chunks of at most 1024 pieces
 
 // One workgroup per query head: the attention block of infer.rs:540-572.
 //  1. Loads first (every key/value row but the current one is already in the
 //     cache): the key rows of this thread's positions (two rounds of kAttNT
-//     positions when they fit in registers) and, in the producer waves, the
-//     value rows of the first three chunks. Then rope::apply (rope.rs:49-65)
+//     positions when they fit in registers) and, from the producer waves, DMA
+//     requests of the first three chunks' value rows into an LDS ring. Then
+//     rope::apply (rope.rs:49-65)
 //     on the head's q and its KV head's k with the step's (cos, sin) table, and
 //     the KV append as f16 (infer.rs:547-551) by the first query head of each
 //     KV group. The fresh key/value are used from LDS, so the other heads of
@@ -425,8 +427,9 @@ constexpr int kAttProd = 8704;  // floats per product stage (head_dim x (chunk +
 //  4. out[i] += a_t * v_t[i] in position order (kernels.rs:163-173). Chunks of
 //     C positions: the producer waves form the products a_t * v_t[i] of the
 //     next chunk in LDS, dimension-major (row stride C + 4 floats), from value
-//     rows they requested three chunks earlier; the chain lanes (one per
-//     dimension) add the current chunk, four positions per 16-byte LDS read.
+//     rows their DMA requests brought into the ring two chunks earlier; the
+//     chain lanes (one per dimension) add the current chunk, four positions
+//     per 16-byte LDS read.
 //  5. out (f32) and, when out_q8 != null, its Q8_0 blocks for the output
 //     projection.
 // With PF (prefill), workgroup (h, i) serves token i of a chunk at position
@@ -448,6 +451,7 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   constexpr int nprod = kAttNT - 64 * cw;
   constexpr int npc = C * g8;  // 16-byte value pieces per chunk
   static_assert(npc <= 2 * nprod, "two pieces per producer thread");
+  static_assert(npc % 64 == 0 && 3 * npc * 16 <= kAttRing, "whole-wave DMAs within the value ring");
   constexpr bool kTwoRounds = HD <= 64;  // second round of key rows held in registers
   extern __shared__ __align__(16) float sm[];
   const int h = blockIdx.x, tid = threadIdx.x;
@@ -467,6 +471,8 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   float* kcur = qs + hd;
   float* vcur = kcur + hd;
   float* red = vcur + hd;
+  // value pieces of three chunks, [3][npc] x 16 bytes, written by DMA
+  uint4* vring = (uint4*)(red + 32);
   // KV cache, per layer and KV head, piece-major: [hd / 8][ctx][8 dims] f16, so
   // that lanes taking consecutive positions read consecutive 16-byte pieces
   const size_t base = ((size_t)layer * n_kv_heads + g) * hd * ctx;
@@ -484,24 +490,50 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
       for (int j = 0; j < g8; j++) r[j] = src[(size_t)j * ctx];
     }
   };
-  // value piece idx of a chunk: position idx % C (consecutive lanes, consecutive
-  // positions), dimensions 8 (idx / C) .. + 8
-  auto vload = [&](int c, uint4 r[2]) {
+  // Chunk c's value pieces go to ring slot c % 3 by DMA (global_load_lds_dwordx4,
+  // no registers held): piece idx = position idx % C (consecutive lanes,
+  // consecutive positions), dimensions 8 (idx / C) .. + 8. Producer wave p moves
+  // pieces 64p + lane and nprod + 64p + lane, those below npc; positions past
+  // the last are clamped to it (valid memory, never used) and the current
+  // position's row is taken from LDS instead. Chunk c is requested two steps
+  // before its products are formed, into the slot whose chunk was consumed
+  // before the last barrier.
+  const int pw = ptid >> 6;  // producer wave index (uniform)
+  const int vdma = (64 * pw < npc ? 1 : 0) + (nprod + 64 * pw < npc ? 1 : 0);  // this wave's DMAs per chunk
+  auto vload = [&](int c) {
+    const int slot = c % 3;
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-      const int idx = ptid + nprod * j;
+      const int wbase = 64 * pw + nprod * j;  // the wave's first piece
+      if (wbase >= npc) break;
+      const int idx = wbase + (tid & 63);
       const int tl = idx % C, i0 = 8 * (idx / C);
-      const int t = c * C + tl;
-      if (idx < npc && t < n && t != self) r[j] = *(const uint4*)(vc + kvi(t, i0));
+      const int t = min(c * C + tl, n - 1);
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(
+          (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint4*)(vring + (size_t)slot * npc + wbase));
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(dst), "v"(vc + kvi(t, i0)) : "memory");
     }
   };
-  uint4 s0[2], s1[2], s2[2];  // value rows of chunks k with k % 3 == 0, 1, 2
+  // this wave's DMAs for the older of its two outstanding chunks are done
+  auto vwait = [&]() {
+    asm volatile("" ::: "memory");
+    if (vdma == 2) __builtin_amdgcn_s_waitcnt(2 | (7 << 4) | (15 << 8));
+    else if (vdma == 1) __builtin_amdgcn_s_waitcnt(1 | (7 << 4) | (15 << 8));
+    asm volatile("" ::: "memory");
+  };
+  // the first wait, with chunks 1 and 2 still outstanding
+  auto vwait2 = [&]() {
+    asm volatile("" ::: "memory");
+    if (vdma == 2) __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (15 << 8));
+    else if (vdma == 1) __builtin_amdgcn_s_waitcnt(2 | (7 << 4) | (15 << 8));
+    asm volatile("" ::: "memory");
+  };
   load_key(tid, kr);
   if constexpr (kTwoRounds) load_key(tid + kAttNT, kr2);
   if (producer) {
-    vload(0, s0);
-    vload(1, s1);
-    vload(2, s2);
+    vload(0);
+    vload(1);
+    vload(2);
   }
   if (PF) {
     for (int i = tid; i < hd; i += kAttNT) qs[i] = q_in[(size_t)h * hd + i];
@@ -624,8 +656,9 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   __syncthreads();
   const float inv = red[16];
   for (int t = tid; t < n; t += kAttNT) att[t] = att[t] * inv;
-  auto vprod = [&](int c, const uint4 r[2]) {
+  auto vprod = [&](int c) {
     float* pb = prod + (c & 1) * kAttProd;
+    const uint4* r = vring + (size_t)(c % 3) * npc;
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int idx = ptid + nprod * j;
@@ -638,7 +671,8 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
 #pragma unroll
         for (int q = 0; q < 8; q++) vv[q] = vcur[i0 + q];
       } else {
-        const uint32_t vw[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+        const uint4 rv = r[idx];
+        const uint32_t vw[4] = {rv.x, rv.y, rv.z, rv.w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           vv[2 * q] = f16_bits_to_f32(vw[q] & 0xffffu);
@@ -649,31 +683,32 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
       for (int q = 0; q < 8; q++) pb[(i0 + q) * CP + tl] = a * vv[q];
     }
   };
-  __syncthreads();  // att[] normalized
+  if (producer) vwait2();  // chunk 0
+  __syncthreads();  // att[] normalized, chunk 0's values in the ring
   if (producer) {
-    vprod(0, s0);
-    vload(3, s0);
+    vprod(0);
+    vwait();  // chunk 1 (chunk 2 outstanding)
   }
   __syncthreads();
   float o = 0.0f;
   // chunk cc: the chain lanes add it while the producers fill chunk cc + 1 (from
-  // slot (cc + 1) % 3) and request chunk cc + 4 into that slot
-  auto step = [&](int cc, uint4 slot[2]) {
+  // slot (cc + 1) % 3) and request chunk cc + 3 into the slot of chunk cc
+  auto step = [&](int cc) {
     if (producer) {
       if (cc + 1 < nchunks) {
-        vprod(cc + 1, slot);
-        vload(cc + 4, slot);
+        vprod(cc + 1);
+        vload(cc + 3);  // into the slot of chunk cc, consumed before the last barrier
+        vwait();        // chunk cc + 2 (chunk cc + 3 outstanding), read after the barrier
       }
     } else if (tid < hd) {
       o = chain_from(prod + (cc & 1) * kAttProd + tid * CP, min(C, n - cc * C), o);
     }
     __syncthreads();
   };
-  for (int c = 0; c < nchunks; c += 3) {
-    step(c, s1);
-    if (c + 1 < nchunks) step(c + 1, s2);
-    if (c + 2 < nchunks) step(c + 2, s0);
-  }
+  for (int c = 0; c < nchunks; c++) step(c);
+  // requests past the last chunk land in unread slots; none may still be
+  // writing to LDS when the workgroup ends
+  if (producer) __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
   if (tid < hd) {
     out[(size_t)h * hd + tid] = o;
     if (out_q8) quant_q8_0_lane(o, tid & 31, out_q8 + (size_t)((h * hd + tid) >> 5) * kQ8_0Bytes);
@@ -1789,7 +1824,8 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
   m->att_dim = c.n_heads * c.head_dim;
   m->maxd = std::max(std::max(c.dim, m->att_dim), c.ffn_dim);
   m->L.resize(c.n_layers);
-  m->att_lds = ((size_t)((c.ctx + 127) & ~127) + 2 * nrq::kAttProd + 3 * (size_t)c.head_dim + 32) * 4;
+  m->att_lds = ((size_t)((c.ctx + 127) & ~127) + 2 * nrq::kAttProd + 3 * (size_t)c.head_dim + 32) * 4 +
+               nrq::kAttRing;
   auto bail = [&](hipError_t e, const char* what) {
     nrq::set_last_error((std::string(what) + ": " + hipGetErrorString(e)).c_str());
     nrq_model_destroy(m);
