@@ -412,6 +412,19 @@ def measure_decode(fill=1024, n=128):
     t0 = time.perf_counter()
     m.generate(int(np.argmax(lg)), n)
     sdt = time.perf_counter() - t0
+    # untimed: the first steps again one forward at a time, for the margin
+    # between the two largest logits (how far a numeric difference would have
+    # to move a logit to change the greedy token) and the token check
+    m.reset()
+    m.set_sampler(0.0, 1.0, 0)
+    m.prefill(prompt, logits=False)
+    gaps, same, tok = [], True, int(np.argmax(lg))
+    for i in range(min(n, 16)):
+        step_lg = m.forward(tok)
+        top2 = np.sort(step_lg)[-2:]
+        gaps.append(float(top2[1] - top2[0]))
+        tok = int(np.argmax(step_lg))
+        same = same and tok == int(out[i])
     m.close()
     torch.cuda.empty_cache()
     mid = fill + n // 2
@@ -426,6 +439,8 @@ def measure_decode(fill=1024, n=128):
             "gbs": round(model_bytes_per_token(cfg, mid) * n / dt / 1e9, 1), "tokens": int(n),
             "first_tokens": [int(t) for t in out[:4]], "load": load, "verify_crc": crc,
             "sampled_tok_s": round(n / sdt, 1),
+            "top2_logit_gap": {"steps": len(gaps), "min": round(min(gaps), 6), "median": round(float(np.median(gaps)), 6),
+                               "per_step": [round(g, 6) for g in gaps], "forward_tokens_match_generate": bool(same)},
             "prefill": {"tokens": int(fill), "chunks_of": 64, "seconds": round(pf_dt, 4),
                         "tok_s": round(fill / pf_dt, 1),
                         "what": "nrq_model_prefill of the random prompt from position 0 (KV 0..1023), host sync "
@@ -600,6 +615,11 @@ def cpu_baseline_crc(seconds):
             "sample": f"{n >> 20} MiB of random bytes in 64 MiB calls, {dt:.1f} s"}
 
 
+def progress(msg):
+    """One line per finished leg on stderr (the JSON line stays alone on stdout)."""
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
 def copy_calibration(nbytes):
     """Five device-to-device copies of `nbytes` (reads nbytes, writes nbytes):
     the reference kernel for scaling FETCH_SIZE / WRITE_SIZE counter readings."""
@@ -625,6 +645,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--decode-tokens", type=int, default=128, help="greedy tokens timed by the decode leg")
     ap.add_argument("--also", default="cfg1,cfg3", help="other matvec configs reported beside (comma list)")
     ap.add_argument("--qwen3-only", action="store_true", help="only the Qwen3-4B decode/prefill leg")
     ap.add_argument("--no-qwen3", action="store_true", help="skip the Qwen3-4B decode/prefill leg")
@@ -679,24 +700,33 @@ def main():
         sys.exit(2)
     order = 0 if args.order == "scalar" else 1
     r = measure_matvec(args.config, args.steps, args.warmup, order)
+    progress(f"{args.config} matvec {r['kernel_us']:.3f} us")
     others = {}
     for name in [s for s in args.also.split(",") if s and s != args.config]:
         o = measure_matvec(name, args.steps, args.warmup, order)
         others[name] = {k: round(v, 3) if isinstance(v, float) else v for k, v in o.items()}
+        progress(f"{name} matvec {o['kernel_us']:.3f} us")
     prefill = None if args.no_prefill else measure_prefill()
-    decode = None if args.no_decode else measure_decode()
+    if prefill is not None:
+        progress("prefill layer")
+    decode = None if args.no_decode else measure_decode(n=args.decode_tokens)
+    if decode is not None:
+        progress(f"decode {decode['tok_s']} tok/s")
     qwen3 = None
     if not args.no_decode and not args.no_qwen3:
         try:
             qwen3 = measure_qwen3()
         except Exception as e:  # reported, never fatal to the bench line
             qwen3 = {"error": f"{type(e).__name__}: {e}"}
+        progress("qwen3")
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline_matvec(args.config, args.cpu_seconds)
+        progress("cpu matvec")
         if decode is not None:
             cpu["decode"] = cpu_baseline_decode(args.cpu_seconds)
             cpu["verify_crc"] = cpu_baseline_crc(min(args.cpu_seconds, 5.0))
+            progress("cpu decode")
     dtype, rows, cols, _, desc = CONFIGS[args.config]
     out = {
         "metric": METRIC,

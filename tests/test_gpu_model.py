@@ -65,6 +65,13 @@ def test_device_expf_sincosf_bitexact(gpu, oracle):
         assert_bitwise(got[~nan], want[~nan], name)
 
 
+def top2_gap(logits):
+    """Largest minus second-largest logit: the distance a numeric difference
+    would have to move a logit to change the greedy token."""
+    t = np.sort(np.asarray(logits, np.float64))[-2:]
+    return float(t[1] - t[0])
+
+
 def run_pair(oracle, cfg, weights, ctx, prompt, n_gen, check_kv=True, prefill=False):
     """Feeds `prompt` then generates n_gen tokens greedily on both sides.
     The oracle takes the prompt in 64-token prefill chunks; the GPU one
@@ -78,11 +85,15 @@ def run_pair(oracle, cfg, weights, ctx, prompt, n_gen, check_kv=True, prefill=Fa
     ref_prompt_logits = want_logits.copy()
     tok = oracle.argmax(want_logits)
     want_tokens = []
+    gaps = []  # top-2 logit margin of each greedy choice
     for _ in range(n_gen):
         want_tokens.append(tok)
+        gaps.append(top2_gap(want_logits))
         want_logits = ref.forward(tok)
         tok = oracle.argmax(want_logits)
     want_tokens.append(tok)
+    gaps.append(top2_gap(want_logits))
+    print(f"top-2 logit gap over {len(gaps)} greedy choices: min {min(gaps):.6g}, median {np.median(gaps):.6g}")
 
     m = Model(cfg, ctx)
     try:
@@ -99,7 +110,7 @@ def run_pair(oracle, cfg, weights, ctx, prompt, n_gen, check_kv=True, prefill=Fa
         assert first == want_tokens[0], (first, want_tokens[0])
         got_tokens, last = m.generate(first, n_gen, logits=True)
         assert m.pos == len(prompt) + n_gen
-        assert [first] + list(got_tokens) == want_tokens, "greedy tokens differ"
+        assert [first] + list(got_tokens) == want_tokens, f"greedy tokens differ (min top-2 gap {min(gaps):.6g})"
         assert_bitwise(last, want_logits, "last logits")
         if check_kv:
             k, v = m.kv_cache()
