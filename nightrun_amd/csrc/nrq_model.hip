@@ -2164,6 +2164,17 @@ int nrq_model_kv_cache(nrq_model* m, void* k_host, void* v_host, size_t bytes) {
   return NRQ_OK;
 }
 
+int nrq_dev_rmsnorm(const float* x, const float* w, float* out, size_t rows, size_t n, float eps, void* stream) {
+  if (rows == 0) return NRQ_OK;
+  if (!x || !w || !out) return mfail(NRQ_ERR_ARG, "nrq_dev_rmsnorm: null pointer");
+  if (n == 0 || n % 256 || n > (size_t)nrq::kNormMax) return mfail(NRQ_ERR_SHAPE, "nrq_dev_rmsnorm: n must be a multiple of 256, at most 8192");
+  if (rows > (size_t)INT_MAX) return mfail(NRQ_ERR_SHAPE, "nrq_dev_rmsnorm: too many rows");
+  // norm_kernel updates x in place only when it adds a residual; here it reads x
+  hipLaunchKernelGGL(nrq::norm_kernel, dim3((unsigned)rows), dim3(nrq::kNormNT), 0, (hipStream_t)stream,
+                     const_cast<float*>(x), nullptr, w, (int)n, eps, 1.0f, out, nullptr);
+  return hipGetLastError() == hipSuccess ? NRQ_OK : mfail(NRQ_ERR_DEVICE, "nrq_dev_rmsnorm: launch failed");
+}
+
 int nrq_dev_mathf(int fn, const float* x, float* y, size_t n, void* stream) {
   if (fn < 0 || fn > 2) return mfail(NRQ_ERR_ARG, "nrq_dev_mathf: unknown function");
   if (n == 0) return NRQ_OK;
