@@ -425,6 +425,7 @@ def measure_decode(fill=1024, n=128):
         gaps.append(float(top2[1] - top2[0]))
         tok = int(np.argmax(step_lg))
         same = same and tok == int(out[i])
+    stages = step_stages(m, tok)
     m.close()
     torch.cuda.empty_cache()
     mid = fill + n // 2
@@ -439,12 +440,23 @@ def measure_decode(fill=1024, n=128):
             "gbs": round(model_bytes_per_token(cfg, mid) * n / dt / 1e9, 1), "tokens": int(n),
             "first_tokens": [int(t) for t in out[:4]], "load": load, "verify_crc": crc,
             "sampled_tok_s": round(n / sdt, 1),
+            "step_stages_us": {"what": f"eager steps at KV {fill + min(n, 16)}.., HIP events after each stage, "
+                                       "medians of 8 (the graph replay above runs the same kernels)", **stages},
             "top2_logit_gap": {"steps": len(gaps), "min": round(min(gaps), 6), "median": round(float(np.median(gaps)), 6),
                                "per_step": [round(g, 6) for g in gaps], "forward_tokens_match_generate": bool(same)},
             "prefill": {"tokens": int(fill), "chunks_of": 64, "seconds": round(pf_dt, 4),
                         "tok_s": round(fill / pf_dt, 1),
                         "what": "nrq_model_prefill of the random prompt from position 0 (KV 0..1023), host sync "
                                 "per chunk, logits of the last token copied back"}}
+
+
+def step_stages(m, token, steps=8):
+    """Median microseconds per stage of `steps` eagerly launched decode steps,
+    each stage bracketed by HIP events on the model's stream."""
+    rows = [m.step_profile(token) for _ in range(steps)]
+    out = {k: round(float(np.median([r[k] for r in rows])), 2) for k in rows[0]}
+    out["sum"] = round(sum(v for k, v in out.items()), 2)
+    return out
 
 
 def kquant_bytes(dt, rows, cols):
@@ -481,8 +493,9 @@ def measure_qwen3(fill=512, n=64):
     m.prefill(prompt, logits=False)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    m.generate(int(np.argmax(lg)), n)
+    out = m.generate(int(np.argmax(lg)), n)
     dt = time.perf_counter() - t0
+    stages = step_stages(m, int(out[-1]))
     m.close()
     torch.cuda.empty_cache()
     d, hd = cfg["dim"], cfg["head_dim"]
@@ -497,6 +510,8 @@ def measure_qwen3(fill=512, n=64):
             "tok_s": round(n / dt, 1), "ms_per_token": round(dt / n * 1e3, 4), "bytes_per_token": int(per_tok),
             "gbs": round(per_tok * n / dt / 1e9, 1), "prefill_tok_s": round(fill / pf_dt, 1),
             "load_seconds": round(load_s, 3),
+            "step_stages_us": {"what": f"eager steps at KV {fill + n}.., HIP events after each stage, medians of 8",
+                               **stages},
             "reference_host": {"decode_tok_s": "10.6-11.9", "prefill_batch64_tok_s": 20.7,
                                "source": "docs/benchmarks.md:63-64, docs/baseline-x86.md:144"}}
 

@@ -233,6 +233,13 @@ int nrq_model_prefill(nrq_model *m, const uint32_t *tokens, int n, float *logits
  * out_tokens gets the n sampled ids; last_logits (optional) the last step's
  * logits. */
 int nrq_model_generate(nrq_model *m, uint32_t token, int n, uint32_t *out_tokens, float *last_logits);
+/* One decode step of `token` (as nrq_model_forward, no logits copied back),
+ * launched eagerly with a HIP event after each stage; stage_us[0..8] get the
+ * microseconds per stage summed over the layers: embed, norm + q|k|v,
+ * attention, o, norm + gate|up (+ swiglu), down, final norm, head, argmax or
+ * sampler. No reference counterpart: the step's own timing, beside the graph
+ * replays of nrq_model_generate. */
+int nrq_model_step_profile(nrq_model *m, uint32_t token, float *stage_us, int n_stages);
 /* Sampler::new (sample.rs:15-21) for nrq_model_generate: temperature <= 0 is
  * greedy (argmax, the default); otherwise each step draws from the 64 largest
  * logits at `temperature`, cut to the shortest prefix whose probability

@@ -63,6 +63,7 @@ SIGNATURES = {
     "nrq_model_pos": ([_vp], _i),
     "nrq_model_forward": ([_vp, C.c_uint32, _vp], _i),
     "nrq_model_generate": ([_vp, C.c_uint32, _i, _vp, _vp], _i),
+    "nrq_model_step_profile": ([_vp, C.c_uint32, _vp, _i], _i),
     "nrq_model_kv_cache": ([_vp, _vp, _vp, _sz], _i),
     "nrq_model_destroy": ([_vp], _i),
     "nrq_model_set_rope_freqs": ([_vp, _vp, _i], _i),
@@ -106,6 +107,11 @@ def lib():
         if not os.path.exists(LIB_PATH):
             raise FileNotFoundError(
                 f"{LIB_PATH} is missing: build it with `python -m nightrun_amd.build` (no CPU fallback exists)")
+        # torch first: it ships its own HIP runtime, and libnrq (whose
+        # libamdhip64.so.7 then resolves to that copy) must share it; loaded
+        # the other way round, torch finds no GPU
+        import torch  # noqa: F401
+
         L = C.CDLL(LIB_PATH)
         for name, (args, res) in SIGNATURES.items():
             fn = getattr(L, name)

@@ -125,6 +125,11 @@ __device__ __forceinline__ int rust_f32_to_i32(float f) {
   return (int)f;
 }
 
+// kquant.rs:145-153
+__device__ __forceinline__ int nearest_int(float v) {
+  return v >= 0.0f ? rust_f32_to_i32(v + 0.5f) : rust_f32_to_i32(v - 0.5f);
+}
+
 // q8::quantize (q8.rs:27-44) of one 32-value block held one value per lane of
 // a 32-lane group: amax over the group, d = f16(amax / 127), round half away
 // from zero, clamp to [-127, 127]. Returns this lane's quant and the f16 bits of d.

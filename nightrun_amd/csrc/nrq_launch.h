@@ -71,9 +71,13 @@ struct NormMatvecLaunch {
   // optional, for a gate|up pair: the Q8_0 blocks of swiglu(gate, up) are
   // written here (y is then not written); rows a multiple of 32
   uint8_t* swiglu_q8;
+  // optional, K-quant weights: the activation's Q8_K blocks are also stored here
+  uint8_t* xq_out;
   void* stream;
 };
-int launch_norm_matvec_q8_0(const NormMatvecLaunch& L);
+// Residual + rmsnorm + activation quantization fused into the matvec prologue,
+// for 1-3 matrices of one dtype (Q8_0, Q4_K or Q6_K)
+int launch_norm_matvec(int dtype, const NormMatvecLaunch& L);
 int launch_matmul(int dtype, int order, const MatmulLaunch& L);
 // Scalar-order batched matmul on int8 MFMA: the 32 x 32 tiles of nrq_mmt.hip,
 // or for Q8_0 below 1024 rows the 16 x 16 tiles of nrq_mmq.hip.

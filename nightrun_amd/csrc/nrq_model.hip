@@ -1347,6 +1347,10 @@ int qk_of(int dt) { return dt == NRQ_Q8_0 ? 32 : 256; }
 
 struct nrq_model {
   nrq_model_config cfg{};
+  // HIP events recorded after each stage of a timed eager step (nrq_model_step_profile)
+  std::vector<hipEvent_t> tev;
+  std::vector<int> tstage;
+  bool timing = false;
   int kv_dim = 0, att_dim = 0, maxd = 0;
   hipStream_t stream = nullptr;
   Mat embed, output;
@@ -1469,8 +1473,16 @@ int matvec_group(nrq_model* m, const Mat* const* ws, float* const* ys, const int
 // *xo and the two buffers swap. Returns 1 when the shapes do not allow it.
 int fused_norm_group(nrq_model* m, float** xr, float** xo, const float* add, const float* normw,
                      const Mat* const* ws, float* const* ys, const int* rows, int n, uint8_t* swiglu_q8 = nullptr) {
+  // Q8_0 groups, or K-quant groups (Q4_K / Q6_K, no swiglu epilogue): the
+  // leading run of one dtype takes the fused launch, which for K-quants also
+  // stores the Q8_K activation that the rest of the group reads
+  const int dt = ws[0]->dt;
+  const bool kq = dt != NRQ_Q8_0;
   for (int i = 0; i < n; i++)
-    if (ws[i]->dt != NRQ_Q8_0) return 1;
+    if ((ws[i]->dt == NRQ_Q8_0) == kq) return 1;
+  if (kq && swiglu_q8) return 1;
+  int j = 1;
+  while (j < n && ws[j]->dt == dt) j++;
   nrq::NormMatvecLaunch L{};
   L.x = *xr;
   L.add = add;
@@ -1479,18 +1491,20 @@ int fused_norm_group(nrq_model* m, float** xr, float** xo, const float* add, con
   L.n = m->cfg.dim;
   L.eps = m->cfg.norm_eps;
   L.rscale = m->res_scale;
-  L.nmat = n;
-  for (int i = 0; i < n; i++) {
+  L.nmat = j;
+  for (int i = 0; i < j; i++) {
     L.w[i] = ws[i]->w;
     L.y[i] = ys[i];
     L.rows[i] = rows[i];
   }
   L.swiglu_q8 = swiglu_q8;
+  L.xq_out = kq ? m->xq : nullptr;
   L.stream = m->stream;
-  const int rc = nrq::launch_norm_matvec_q8_0(L);
+  const int rc = nrq::launch_norm_matvec(dt, L);
   if (rc == nrq::NRQ_LAUNCH_TOO_WIDE) return 1;
   if (rc) return mfail(NRQ_ERR_DEVICE, "model: norm + matvec launch failed");
   if (add) std::swap(*xr, *xo);
+  if (j < n) return matvec_group(m, ws + j, ys + j, rows + j, n - j, m->cfg.dim);
   return NRQ_OK;
 }
 
@@ -1507,6 +1521,27 @@ int scale_logits(nrq_model* m) {
   return hipGetLastError() == hipSuccess ? NRQ_OK : mfail(NRQ_ERR_DEVICE, "model: logit scale launch failed");
 }
 
+// Holds the stream for `ticks` of the 100 MHz real-time clock (one wave, a
+// bounded wait), so that the host enqueues a whole timed step before the GPU
+// reaches its first kernel.
+__global__ void hold_kernel(long long ticks) {
+  const long long t0 = wall_clock64();
+  while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+}
+
+// Stages of a decode step, as nrq_model_step_profile reports them.
+enum { kStEmbed, kStQkv, kStAttention, kStO, kStGateUp, kStDown, kStFinalNorm, kStHead, kStPick, kStCount };
+
+// In a timed step: an event after the stage just enqueued.
+static void step_mark(nrq_model* m, int stage) {
+  if (!m->timing) return;
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return;
+  hipEventRecord(e, m->stream);
+  m->tev.push_back(e);
+  m->tstage.push_back(stage);
+}
+
 // One decode step, enqueued on m->stream (infer.rs:510-595 + argmax).
 int enqueue_step(nrq_model* m) {
   const auto& c = m->cfg;
@@ -1515,6 +1550,7 @@ int enqueue_step(nrq_model* m) {
                      (const uint8_t*)m->embed.w, m->embed.dt, m->ctl, d, m->x, m->freqs, c.head_dim / 2, m->rope_cs,
                      m->embed_scale);
   if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: embed launch failed");
+  step_mark(m, kStEmbed);
   const float scale = m->att_scale;
   const float* pending = nullptr;  // residual not yet added into *xr
   float* xr = m->x;                // the residual stream
@@ -1533,6 +1569,7 @@ int enqueue_step(nrq_model* m) {
         rc = matvec_group(m, ws, ys, rows, 3, d);
       }
       if (rc) return rc;
+      step_mark(m, kStQkv);
     }
     {
       const bool q8 = Ly.m[3].dt == NRQ_Q8_0;
@@ -1545,8 +1582,10 @@ int enqueue_step(nrq_model* m) {
                          q8 ? m->xq : nullptr, Ly.q_norm, Ly.k_norm, c.norm_eps, m->rope_neox);
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: attention launch failed");
       if (!q8 && (rc = quantize_for(m, Ly.m[3].dt, m->attn, att, m->xq))) return rc;
+      step_mark(m, kStAttention);
     }
     if ((rc = matvec(m, Ly.m[3], m->xq, m->xb2, d, att))) return rc;
+    step_mark(m, kStO);
     {
       const Mat* ws[2] = {&Ly.m[4], &Ly.m[5]};
       float* ys[2] = {m->gate, m->up};
@@ -1570,12 +1609,16 @@ int enqueue_step(nrq_model* m) {
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: swiglu launch failed");
       if (!q8 && (rc = quantize_for(m, Ly.m[6].dt, m->gate, ffn, m->xq))) return rc;
     }
+    step_mark(m, kStGateUp);
     if ((rc = matvec(m, Ly.m[6], m->xq, m->xb2, d, ffn))) return rc;
+    step_mark(m, kStDown);
     pending = m->xb2;
   }
   if ((rc = norm_quant(m, xr, pending, m->out_norm, m->output.dt))) return rc;
+  step_mark(m, kStFinalNorm);
   if ((rc = matvec(m, m->output, m->xq, m->logits, c.vocab, d))) return rc;
   if ((rc = scale_logits(m))) return rc;
+  step_mark(m, kStHead);
   if (m->samp_t > 0.0f) {
     const int np = (c.vocab + nrq::kSelSlice - 1) / nrq::kSelSlice;
     hipLaunchKernelGGL(nrq::top64_part_kernel, dim3(np), dim3(nrq::kSelPartWaves * 64), 0, m->stream, m->logits,
@@ -1584,11 +1627,13 @@ int enqueue_step(nrq_model* m) {
                        m->logits,
                        m->samp_t, m->samp_p, m->rng, m->ctl, m->out_tokens, m->max_out, nullptr);
     if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: sampler launch failed");
+    step_mark(m, kStPick);
     return NRQ_OK;
   }
   hipLaunchKernelGGL(nrq::argmax_kernel, dim3(1), dim3(nrq::kArgNT), 0, m->stream, m->logits, c.vocab, m->ctl,
                      m->out_tokens, m->max_out);
   if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: argmax launch failed");
+  step_mark(m, kStPick);
   return NRQ_OK;
 }
 
@@ -2053,6 +2098,43 @@ int nrq_model_forward(nrq_model* m, uint32_t token, float* logits_host) {
   if (logits_host)
     MHIP(hipMemcpyAsync(logits_host, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost, m->stream));
   MHIP(hipStreamSynchronize(m->stream));
+  m->host_pos += 1;
+  return NRQ_OK;
+}
+
+int nrq_model_step_profile(nrq_model* m, uint32_t token, float* stage_us, int n_stages) {
+  int rc = check_ready(m, "nrq_model_step_profile");
+  if (rc) return rc;
+  if (!stage_us || n_stages < kStCount) return mfail(NRQ_ERR_ARG, "nrq_model_step_profile: needs 9 stage slots");
+  if (m->host_pos >= m->cfg.ctx) return mfail(NRQ_ERR_SHAPE, "assertion failed: pos < d.ctx: context window exhausted");
+  if (token >= (uint32_t)m->cfg.vocab) return mfail(NRQ_ERR_ARG, "nrq_model_step_profile: token out of vocabulary");
+  if ((rc = set_ctl(m, nrq::CTL_TOKEN, (int)token))) return rc;
+  MHIP(hipStreamSynchronize(m->stream));
+  hipEvent_t e0 = nullptr;
+  MHIP(hipEventCreate(&e0));
+  // 3 ms of hold (the host enqueues a step in well under that), then the step
+  hipLaunchKernelGGL(hold_kernel, dim3(1), dim3(64), 0, m->stream, 300000LL);
+  hipEventRecord(e0, m->stream);
+  uint32_t* keep = m->out_tokens;
+  m->out_tokens = nullptr;
+  m->timing = true;
+  rc = enqueue_step(m);
+  m->timing = false;
+  m->out_tokens = keep;
+  const hipError_t es = hipStreamSynchronize(m->stream);
+  for (int i = 0; i < n_stages; i++) stage_us[i] = 0.0f;
+  hipEvent_t prev = e0;
+  for (size_t i = 0; i < m->tev.size() && es == hipSuccess && rc == 0; i++) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, prev, m->tev[i]) == hipSuccess) stage_us[m->tstage[i]] += ms * 1e3f;
+    prev = m->tev[i];
+  }
+  for (hipEvent_t e : m->tev) hipEventDestroy(e);
+  m->tev.clear();
+  m->tstage.clear();
+  hipEventDestroy(e0);
+  if (rc) return rc;
+  MHIP(es);
   m->host_pos += 1;
   return NRQ_OK;
 }

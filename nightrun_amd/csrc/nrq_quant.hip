@@ -38,11 +38,6 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restr
   }
 }
 
-// kquant.rs:145-153
-__device__ __forceinline__ int nearest_int(float v) {
-  return v >= 0.0f ? rust_f32_to_i32(v + 0.5f) : rust_f32_to_i32(v - 0.5f);
-}
-
 // One 256-thread workgroup per Q8_K block.
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ src, uint8_t* __restrict__ dst) {
   __shared__ float s_abs[4];

@@ -280,6 +280,9 @@ struct WsArgs {
   // rows 32w .. 32w+31 of both (waves 0-1 gate, 2-3 up) and writes the Q8_0
   // blocks of swiglu(gate, up) (vec.rs:45-52, q8.rs:27-44) instead of y
   uint8_t* swiglu_q8;
+  // fused norm, K-quant weights: workgroup 0 also stores the activation's Q8_K
+  // blocks here (or null), for the next matvec over the same activation
+  uint8_t* xq_out;
 };
 
 // Block contributions of a wave's rows wait in LDS for the per-row sum. Long
@@ -316,6 +319,74 @@ struct WSGeom {
 // 1.0), fused into a Q8_0 matvec's prologue: LDS holds x, add and the norm
 // weight (DMA, issued before the weight tiles), then the squares; the result
 // is quantized to Q8_0 (q8.rs:27-44) straight into the activation layout.
+// One Q8_K block (kquant.rs:157-187) from 32 lanes of a half-wave, lane r
+// holding values 8r .. 8r+7 of the block: the first index of the largest |v|
+// (a strict `>` scan; NaN never wins), iscale = -128 / v[that index],
+// q = min(nearest_int(iscale * v), 127), d = 1 / iscale, an all-zero block
+// when the largest |v| is not > 0. Written into the kernel's activation layout
+// (Q4_K: qs, 16-value sums as i16 pairs, d; Q6_K: qs, -32 * 16-value sums, d)
+// and, when gout != null, as the standard 292-byte block.
+template <int FMT>
+__device__ __forceinline__ void ws_q8k_half(const float o[8], int r, uint32_t* xb, uint8_t* gout) {
+  float a = -1.0f;
+  int idx = 8 * r;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    float ae = fabsf(o[e]);
+    if (ae != ae) ae = -1.0f;
+    if (ae > a) {
+      a = ae;
+      idx = 8 * r + e;
+    }
+  }
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) {
+    const float oa = __shfl_xor(a, m, 32);
+    const int oi = __shfl_xor(idx, m, 32);
+    if (oa > a || (oa == a && oi < idx)) {
+      a = oa;
+      idx = oi;
+    }
+  }
+  float mine = o[0];
+#pragma unroll
+  for (int e = 1; e < 8; e++) mine = (idx & 7) == e ? o[e] : mine;
+  const float mx = __shfl(mine, idx >> 3, 32);
+  const bool zero = !(a > 0.0f);
+  const float iscale = -128.0f / mx;
+  int q[8];
+  int p = 0;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const int t = nearest_int(iscale * o[e]);
+    q[e] = zero ? 0 : (t > 127 ? 127 : t);
+    p += q[e];
+  }
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    lo |= (uint32_t)(q[e] & 0xff) << (8 * e);
+    hi |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
+  }
+  const int ps = p + __shfl_xor(p, 1, 32);          // the 16-value sum of lanes r & ~1, r | 1
+  const int ps2 = __shfl_down(ps, 2, 32);           // the next pair's sum
+  const uint32_t d_bits = zero ? 0u : __float_as_uint(1.0f / iscale);
+  ((uint2*)xb)[r] = make_uint2(lo, hi);
+  if constexpr (FMT == kQ4K) {
+    if ((r & 3) == 0) xb[64 + (r >> 2)] = ((uint32_t)ps & 0xffffu) | ((uint32_t)ps2 << 16);
+    if (r == 0) xb[72] = d_bits;
+  } else {
+    if ((r & 1) == 0) xb[64 + (r >> 1)] = (uint32_t)(-32 * ps);
+    if (r == 0) xb[80] = d_bits;
+  }
+  if (gout) {
+    *(uint32_t*)(gout + 4 + 8 * r) = lo;  // 4-byte aligned: blocks are 292 bytes
+    *(uint32_t*)(gout + 8 + 8 * r) = hi;
+    if ((r & 1) == 0) *(int16_t*)(gout + 260 + r) = (int16_t)ps;
+    if (r == 0) *(uint32_t*)gout = d_bits;
+  }
+}
+
 constexpr int kFusedNormMax = 4096;
 constexpr int kFusedNormPT = kFusedNormMax / 256;
 
@@ -329,7 +400,8 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
   using F = WS<FMT>;
   constexpr int NI = F::NI, BS = F::BS, TBK = 64 * F::BPL, STAGE = NI * 1024, NT = 64 * NW;
   static_assert(NS >= 1 && NS <= 4, "the vmcnt waits cover up to 4 stages");
-  static_assert(!NORM || (FMT == kQ8_0 && NW == 4), "the fused norm feeds Q8_0 weights, 256 lanes");
+  static_assert(!NORM || NW == 4, "the fused norm runs on 256 lanes");
+  static_assert(!SWI || FMT == kQ8_0, "the swiglu pair writes Q8_0 blocks");
   static_assert(!SWI || NORM, "the swiglu pair is a fused-norm variant");
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
@@ -374,7 +446,7 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
 
   // The activation (or the norm's inputs) first, so an in-order vmcnt wait below covers it.
   float* nxs = (float*)(smem + G.total);  // fused norm: x | add | weight | squares, n floats each
-  const int n = bpr * 32;
+  const int n = bpr * (FMT == kQ8_0 ? 32 : 256);
   if constexpr (NORM) {
     const int nk = n / 256;  // 1 KiB DMAs per array
     const float* src[3] = {A.nx, A.nadd, A.nw};
@@ -473,11 +545,17 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
         float o[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) o[e] = v[8 * k + e] * scale * w[e];
-        uint32_t lo, hi, d_bits;
-        q8_0_quad8(o, &lo, &hi, &d_bits);
-        uint32_t* xb = xl + (j >> 2) * WS<kQ8_0>::XS;
-        ((uint2*)xb)[j & 3] = make_uint2(lo, hi);
-        if ((j & 3) == 0) xb[8] = __float_as_uint(f16_bits_to_f32(d_bits));
+        if constexpr (FMT == kQ8_0) {
+          uint32_t lo, hi, d_bits;
+          q8_0_quad8(o, &lo, &hi, &d_bits);
+          uint32_t* xb = xl + (j >> 2) * WS<kQ8_0>::XS;
+          ((uint2*)xb)[j & 3] = make_uint2(lo, hi);
+          if ((j & 3) == 0) xb[8] = __float_as_uint(f16_bits_to_f32(d_bits));
+        } else {
+          // a Q8_K block is 32 runs, one aligned half-wave (nrun is a multiple of 32)
+          ws_q8k_half<FMT>(o, j & 31, xl + (j >> 5) * WS<FMT>::XS,
+                           (A.xq_out && blockIdx.x == 0) ? A.xq_out + (size_t)(j >> 5) * kQ8KBytes : nullptr);
+        }
       }
     }
     ws_lds_barrier();
@@ -591,7 +669,7 @@ static int launch_ws_t(WsArgs A, int bpr, int rpw, void* stream) {
   const int nstages = (int)(tiles_per_wave < NS ? tiles_per_wave : NS);
   const WSGeom<FMT> G(bpr, rpw, nstages, NW, URM);
   // fused norm: x, add, weight, squares (n floats each) and the scale
-  const size_t lds = G.total + (NORM ? (size_t)4 * bpr * 32 * 4 + 16 : 0);
+  const size_t lds = G.total + (NORM ? (size_t)4 * bpr * (FMT == kQ8_0 ? 32 : 256) * 4 + 16 : 0);
   if (lds > 160 * 1024) return NRQ_LAUNCH_TOO_WIDE;
   if (grid == 0) return 0;
   hipLaunchKernelGGL((wstream_matvec<FMT, NW, NS, MODE>), dim3(grid), dim3(64 * NW), lds, (hipStream_t)stream, A, bpr,
@@ -661,13 +739,18 @@ static int ws_num_cus() {
   return n;
 }
 
-int launch_norm_matvec_q8_0(const NormMatvecLaunch& L) {
+int launch_norm_matvec(int dtype, const NormMatvecLaunch& L) {
+  if (dtype != kQ8_0 && dtype != kQ4K && dtype != kQ6K) return NRQ_LAUNCH_TOO_WIDE;
+  const int qk = dtype == kQ8_0 ? 32 : 256;
   if (L.nmat < 1 || L.nmat > 3 || L.n <= 0 || L.n % 256 || L.n > kFusedNormMax) return NRQ_LAUNCH_TOO_WIDE;
-  const int bpr = L.n / 32;
+  if (L.swiglu_q8 && dtype != kQ8_0) return NRQ_LAUNCH_TOO_WIDE;
+  const int bpr = L.n / qk;
   // Every workgroup runs the norm's sequential sum once, and its LDS allows one
   // workgroup per CU, so the launch is sized to one workgroup per CU: rows per
   // wave grow (in steps that keep the tiles full) until the grid fits.
-  const int rpw0 = ws_rows_per_wave<kQ8_0>(bpr, 0);
+  const int rpw0 = dtype == kQ8_0 ? ws_rows_per_wave<kQ8_0>(bpr, 0)
+                   : dtype == kQ4K ? ws_rows_per_wave<kQ4K>(bpr, 0)
+                                   : ws_rows_per_wave<kQ6K>(bpr, 0);
   long total = 0;
   for (int i = 0; i < L.nmat; i++) total += L.rows[i];
   const long slots = 4L * ws_num_cus();
@@ -691,7 +774,14 @@ int launch_norm_matvec_q8_0(const NormMatvecLaunch& L) {
   A.eps = L.eps;
   A.rscale = L.rscale;
   A.swiglu_q8 = L.swiglu_q8;
+  A.xq_out = L.xq_out;
   const bool urm = ws_u_rowmajor(bpr);
+  if (dtype == kQ4K)
+    return urm ? launch_ws_t<kQ4K, 4, 2, kWsNorm | kWsRowMajorU>(A, bpr, rpw, L.stream)
+               : launch_ws_t<kQ4K, 4, 2, kWsNorm>(A, bpr, rpw, L.stream);
+  if (dtype == kQ6K)
+    return urm ? launch_ws_t<kQ6K, 4, 2, kWsNorm | kWsRowMajorU>(A, bpr, rpw, L.stream)
+               : launch_ws_t<kQ6K, 4, 2, kWsNorm>(A, bpr, rpw, L.stream);
   if (L.swiglu_q8)
     return urm ? launch_ws_t<kQ8_0, 4, 2, kWsNorm | kWsSwiglu | kWsRowMajorU>(A, bpr, rpw, L.stream)
                : launch_ws_t<kQ8_0, 4, 2, kWsNorm | kWsSwiglu>(A, bpr, rpw, L.stream);

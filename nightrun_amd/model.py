@@ -139,6 +139,17 @@ class Model:
                                                  last.ctypes.data if logits else None))
         return (toks, last) if logits else toks
 
+    STEP_STAGES = ("embed", "norm_qkv", "attention", "o", "norm_gate_up_swiglu", "down", "final_norm", "head",
+                   "argmax_or_sampler")
+
+    def step_profile(self, token: int) -> dict:
+        """One eager decode step of `token` with a HIP event after each stage
+        (nrq_model_step_profile): microseconds per stage, summed over layers.
+        Advances the position like forward()."""
+        us = np.zeros(len(self.STEP_STAGES), np.float32)
+        _lib.check(_lib.lib().nrq_model_step_profile(self.h, int(token), us.ctypes.data, us.size))
+        return dict(zip(self.STEP_STAGES, (float(v) for v in us)))
+
     def kv_cache(self):
         n = self.cfg["n_layers"] * self.ctx * self.cfg["n_kv_heads"] * self.cfg["head_dim"]
         k = np.empty(n, np.uint16)

@@ -128,6 +128,35 @@ def test_tiny_model_forward_and_generate(gpu, oracle):
     run_pair(oracle, TINY, w, 128, prompt, 20)
 
 
+def test_step_profile_is_a_forward_step(gpu, oracle):
+    """nrq_model_step_profile runs the same step as nrq_model_forward (the
+    next step's logits are bitwise the same either way) and reports a positive
+    time for every stage but the unused ones."""
+    from nightrun_amd.model import Model
+
+    w = oracle.gen_model(TINY, 77)
+    prompt = np.random.default_rng(3).integers(0, TINY["vocab"], 9).astype(np.uint32)
+    out = []
+    for profiled in (False, True):
+        m = Model(TINY, 64)
+        try:
+            m.set_weights(w)
+            m.prefill(prompt, logits=False)
+            if profiled:
+                st = m.step_profile(5)
+                assert set(st) == set(Model.STEP_STAGES)
+                for k in ("embed", "norm_qkv", "attention", "o", "norm_gate_up_swiglu", "down", "head",
+                          "argmax_or_sampler"):
+                    assert st[k] > 0.0, (k, st)
+            else:
+                m.forward(5, logits=False)
+            assert m.pos == 10
+            out.append(m.forward(7))
+        finally:
+            m.close()
+    assert_bitwise(out[1], out[0], "logits after a profiled step")
+
+
 def test_tiny_model_logits_every_step(gpu, oracle):
     """Logits of every forward step equal the oracle's (not only the argmax)."""
     from nightrun_amd.model import Model
