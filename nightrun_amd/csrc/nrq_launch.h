@@ -41,6 +41,7 @@ struct QuantLaunch {
   void* dst;         // device blocks
   long long n;       // elements (multiple of the block size)
   void* stream;
+  const float* up = nullptr;  // Q8_K only: quantize swiglu(src, up), written back over src
 };
 
 // Scalar order: the streaming kernel (nrq_wstream.hip); AVX2 order: the
@@ -78,6 +79,8 @@ struct NormMatvecLaunch {
 // Residual + rmsnorm + activation quantization fused into the matvec prologue,
 // for 1-3 matrices of one dtype (Q8_0, Q4_K or Q6_K)
 int launch_norm_matvec(int dtype, const NormMatvecLaunch& L);
+// An f32 activation quantized to Q8_K in the prologue of one Q4_K / Q6_K matvec
+int launch_quant_matvec(int dtype, const float* x, int n, const void* w, float* y, int rows, void* stream);
 int launch_matmul(int dtype, int order, const MatmulLaunch& L);
 // Scalar-order batched matmul on int8 MFMA: the 32 x 32 tiles of nrq_mmt.hip,
 // or for Q8_0 below 1024 rows the 16 x 16 tiles of nrq_mmq.hip.

@@ -1581,10 +1581,16 @@ int enqueue_step(nrq_model* m) {
                          m->rope_cs, m->ctl, c.n_heads, c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->attn,
                          q8 ? m->xq : nullptr, Ly.q_norm, Ly.k_norm, c.norm_eps, m->rope_neox);
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: attention launch failed");
-      if (!q8 && (rc = quantize_for(m, Ly.m[3].dt, m->attn, att, m->xq))) return rc;
       step_mark(m, kStAttention);
+      // a K-quant o projection quantizes the attention output in its prologue
+      const int fq = q8 ? nrq::NRQ_LAUNCH_TOO_WIDE
+                        : nrq::launch_quant_matvec(Ly.m[3].dt, m->attn, att, Ly.m[3].w, m->xb2, d, m->stream);
+      if (fq && fq != nrq::NRQ_LAUNCH_TOO_WIDE) return mfail(NRQ_ERR_DEVICE, "model: quantize + matvec launch failed");
+      if (fq) {
+        if (!q8 && (rc = quantize_for(m, Ly.m[3].dt, m->attn, att, m->xq))) return rc;
+        if ((rc = matvec(m, Ly.m[3], m->xq, m->xb2, d, att))) return rc;
+      }
     }
-    if ((rc = matvec(m, Ly.m[3], m->xq, m->xb2, d, att))) return rc;
     step_mark(m, kStO);
     {
       const Mat* ws[2] = {&Ly.m[4], &Ly.m[5]};
@@ -1604,10 +1610,15 @@ int enqueue_step(nrq_model* m) {
     }
     if (!swiglu_done) {
       const bool q8 = Ly.m[6].dt == NRQ_Q8_0;
-      hipLaunchKernelGGL(nrq::swiglu_kernel, dim3((ffn + 255) / 256), dim3(256), 0, m->stream, m->gate, m->up, ffn,
-                         q8 ? m->xq : nullptr);
-      if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: swiglu launch failed");
-      if (!q8 && (rc = quantize_for(m, Ly.m[6].dt, m->gate, ffn, m->xq))) return rc;
+      if (q8) {
+        hipLaunchKernelGGL(nrq::swiglu_kernel, dim3((ffn + 255) / 256), dim3(256), 0, m->stream, m->gate, m->up, ffn,
+                           m->xq);
+        if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: swiglu launch failed");
+      } else {  // swiglu inside the Q8_K quantizer, one launch
+        nrq::QuantLaunch Q{m->gate, m->xq, (long long)ffn, m->stream};
+        Q.up = m->up;
+        if (nrq::launch_quantize_q8k(Q)) return mfail(NRQ_ERR_DEVICE, "model: swiglu + quantize launch failed");
+      }
     }
     step_mark(m, kStGateUp);
     if ((rc = matvec(m, Ly.m[6], m->xq, m->xb2, d, ffn))) return rc;

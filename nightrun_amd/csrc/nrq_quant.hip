@@ -38,14 +38,23 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restr
   }
 }
 
-// One 256-thread workgroup per Q8_K block.
-__global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ src, uint8_t* __restrict__ dst) {
+// One 256-thread workgroup per Q8_K block. With `up`, the values quantized
+// are swiglu(src, up) = src / (1 + expf(-src)) * up (vec.rs:45-52), also
+// written back over src.
+__global__ __launch_bounds__(256) void quantize_q8k_kernel(float* __restrict__ src, uint8_t* __restrict__ dst,
+                                                           const float* __restrict__ up) {
   __shared__ float s_abs[4];
   __shared__ int s_idx[4];
   __shared__ int s_q[256];
+  __shared__ float s_v[256];
   const long long b = blockIdx.x;
   const int i = threadIdx.x;
-  const float v = src[b * 256 + i];
+  float v = src[b * 256 + i];
+  if (up) {
+    v = v / (1.0f + dev_expf(-v)) * up[b * 256 + i];
+    src[b * 256 + i] = v;
+  }
+  s_v[i] = v;
   // The first index holding the largest |v| (strict `>` scan, NaN never wins).
   float a = fabsf(v);
   if (a != a) a = -1.0f;
@@ -80,7 +89,7 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
     if (i < 32) blk[260 + i] = 0;
     return;
   }
-  const float max = src[b * 256 + bi];
+  const float max = s_v[bi];  // s_v was written before the barrier above
   const float iscale = -128.0f / max;
   int q = nearest_int(iscale * v);
   q = q > 127 ? 127 : q;
@@ -131,8 +140,8 @@ int launch_quantize_q8k(const QuantLaunch& L) {
   if (L.n <= 0) return 0;
   if (L.n % 256) return NRQ_LAUNCH_BAD_ARG;
   long long nb = L.n / 256;
-  hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)L.stream, L.src,
-                     (uint8_t*)L.dst);
+  hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)L.stream,
+                     const_cast<float*>(L.src), (uint8_t*)L.dst, L.up);
   return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
 }
 

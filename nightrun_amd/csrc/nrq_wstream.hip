@@ -293,7 +293,7 @@ __host__ __device__ inline bool ws_u_rowmajor(int bpr) { return bpr >= 48; }
 // Kernel variants, chosen at launch so that each instantiation carries only
 // its own code: the fused rmsnorm prologue, the swiglu pair epilogue, and the
 // row-major contribution layout.
-enum { kWsNorm = 1, kWsSwiglu = 2, kWsRowMajorU = 4 };
+enum { kWsNorm = 1, kWsSwiglu = 2, kWsRowMajorU = 4, kWsQuant = 8 };
 __host__ __device__ inline int ws_u_stride(int bpr) { return ((bpr + 3) & ~3) + 4; }
 
 template <int FMT>
@@ -397,7 +397,9 @@ __device__ __forceinline__ void ws_dma16_g(const void* g, uint32_t m0) {
 template <int FMT, int NW, int NS, int MODE>
 __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int rpw, int nstages) {
   constexpr bool NORM = (MODE & kWsNorm) != 0, SWI = (MODE & kWsSwiglu) != 0, URM = (MODE & kWsRowMajorU) != 0;
+  constexpr bool QNT = (MODE & kWsQuant) != 0;
   using F = WS<FMT>;
+  static_assert(!QNT || (!NORM && FMT != kQ8_0), "the quantize prologue makes Q8_K blocks from an f32 activation");
   constexpr int NI = F::NI, BS = F::BS, TBK = 64 * F::BPL, STAGE = NI * 1024, NT = 64 * NW;
   static_assert(NS >= 1 && NS <= 4, "the vmcnt waits cover up to 4 stages");
   static_assert(!NORM || NW == 4, "the fused norm runs on 256 lanes");
@@ -447,7 +449,10 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
   // The activation (or the norm's inputs) first, so an in-order vmcnt wait below covers it.
   float* nxs = (float*)(smem + G.total);  // fused norm: x | add | weight | squares, n floats each
   const int n = bpr * (FMT == kQ8_0 ? 32 : 256);
-  if constexpr (NORM) {
+  if constexpr (QNT) {  // the f32 activation, quantized after the barrier below
+    const uint32_t dst = ws_lds_addr(nxs);
+    for (int k = wave; k < n / 256; k += NW) ws_dma16_g(A.nx + 256 * k + 4 * lane, dst + (uint32_t)k * 1024u);
+  } else if constexpr (NORM) {
     const int nk = n / 256;  // 1 KiB DMAs per array
     const float* src[3] = {A.nx, A.nadd, A.nw};
 #pragma unroll
@@ -559,6 +564,15 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
       }
     }
     ws_lds_barrier();
+  } else if constexpr (QNT) {
+    // Q8_K blocks of the activation (kquant.rs:157-187), a half-wave per block
+    const float4* xs4 = (const float4*)nxs;
+    for (int j = tid; j < (n >> 3); j += NT) {
+      const float4 p0 = xs4[2 * j], p1 = xs4[2 * j + 1];
+      const float o[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+      ws_q8k_half<FMT>(o, j & 31, xl + (j >> 5) * WS<FMT>::XS, nullptr);
+    }
+    ws_lds_barrier();
   } else if constexpr (FMT != kQ4K) {
     ws_repack<FMT>((const uint32_t*)xraw, (uint32_t)((uintptr_t)A.x & 15), bpr, xl, tid, NT);
     ws_lds_barrier();
@@ -653,6 +667,7 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
 template <int FMT, int NW, int NS, int MODE>
 static int launch_ws_t(WsArgs A, int bpr, int rpw, void* stream) {
   constexpr bool NORM = (MODE & kWsNorm) != 0, SWI = (MODE & kWsSwiglu) != 0, URM = (MODE & kWsRowMajorU) != 0;
+  constexpr bool QNT = (MODE & kWsQuant) != 0;
   constexpr int TBK = 64 * WS<FMT>::BPL;
   int grid = 0;
   if constexpr (SWI) {
@@ -669,7 +684,8 @@ static int launch_ws_t(WsArgs A, int bpr, int rpw, void* stream) {
   const int nstages = (int)(tiles_per_wave < NS ? tiles_per_wave : NS);
   const WSGeom<FMT> G(bpr, rpw, nstages, NW, URM);
   // fused norm: x, add, weight, squares (n floats each) and the scale
-  const size_t lds = G.total + (NORM ? (size_t)4 * bpr * (FMT == kQ8_0 ? 32 : 256) * 4 + 16 : 0);
+  const size_t lds = G.total + (NORM ? (size_t)4 * bpr * (FMT == kQ8_0 ? 32 : 256) * 4 + 16 : 0) +
+                     (QNT ? (size_t)bpr * 256 * 4 : 0);
   if (lds > 160 * 1024) return NRQ_LAUNCH_TOO_WIDE;
   if (grid == 0) return 0;
   hipLaunchKernelGGL((wstream_matvec<FMT, NW, NS, MODE>), dim3(grid), dim3(64 * NW), lds, (hipStream_t)stream, A, bpr,
@@ -754,8 +770,20 @@ int launch_norm_matvec(int dtype, const NormMatvecLaunch& L) {
   long total = 0;
   for (int i = 0; i < L.nmat; i++) total += L.rows[i];
   const long slots = 4L * ws_num_cus();
-  int rpw = rpw0;
-  while (rpw + rpw0 <= 64 && (total + rpw - 1) / rpw + 3L * L.nmat > slots) rpw += rpw0;
+  // the fewest rows per wave whose workgroups (four waves, per matrix) fit one
+  // per CU and whose blocks fill 85% of their tiles
+  const int tbk = dtype == kQ8_0 ? 64 * WS<kQ8_0>::BPL : 64;
+  int rpw = 0;
+  for (int r = rpw0; r <= 64 && !rpw; r++) {
+    long wgs = 0;
+    for (int i = 0; i < L.nmat; i++) wgs += ((L.rows[i] + r - 1) / r + 3) / 4;
+    const long tiles = ((long)r * bpr + tbk - 1) / tbk;
+    if (4 * wgs <= slots && (double)r * bpr >= 0.85 * (double)(tiles * tbk)) rpw = r;
+  }
+  if (!rpw) {
+    rpw = rpw0;
+    while (rpw + rpw0 <= 64 && (total + rpw - 1) / rpw + 3L * L.nmat > slots) rpw += rpw0;
+  }
   if (L.swiglu_q8) {  // 16 rows per wave: a workgroup owns 32 rows of gate and of up
     if (L.nmat != 2 || L.rows[0] != L.rows[1] || L.rows[0] % 32) return NRQ_LAUNCH_TOO_WIDE;
     rpw = 16;
@@ -776,9 +804,15 @@ int launch_norm_matvec(int dtype, const NormMatvecLaunch& L) {
   A.swiglu_q8 = L.swiglu_q8;
   A.xq_out = L.xq_out;
   const bool urm = ws_u_rowmajor(bpr);
-  if (dtype == kQ4K)
-    return urm ? launch_ws_t<kQ4K, 4, 2, kWsNorm | kWsRowMajorU>(A, bpr, rpw, L.stream)
+  if (dtype == kQ4K) {
+    // three stages where the LDS has room: a wave's tiles in flight during the norm
+    int rc = urm ? launch_ws_t<kQ4K, 4, 3, kWsNorm | kWsRowMajorU>(A, bpr, rpw, L.stream)
+                 : launch_ws_t<kQ4K, 4, 3, kWsNorm>(A, bpr, rpw, L.stream);
+    if (rc == NRQ_LAUNCH_TOO_WIDE)
+      rc = urm ? launch_ws_t<kQ4K, 4, 2, kWsNorm | kWsRowMajorU>(A, bpr, rpw, L.stream)
                : launch_ws_t<kQ4K, 4, 2, kWsNorm>(A, bpr, rpw, L.stream);
+    return rc;
+  }
   if (dtype == kQ6K)
     return urm ? launch_ws_t<kQ6K, 4, 2, kWsNorm | kWsRowMajorU>(A, bpr, rpw, L.stream)
                : launch_ws_t<kQ6K, 4, 2, kWsNorm>(A, bpr, rpw, L.stream);
@@ -787,6 +821,26 @@ int launch_norm_matvec(int dtype, const NormMatvecLaunch& L) {
                : launch_ws_t<kQ8_0, 4, 2, kWsNorm | kWsSwiglu>(A, bpr, rpw, L.stream);
   return urm ? launch_ws_t<kQ8_0, 4, 2, kWsNorm | kWsRowMajorU>(A, bpr, rpw, L.stream)
              : launch_ws_t<kQ8_0, 4, 2, kWsNorm>(A, bpr, rpw, L.stream);
+}
+
+int launch_quant_matvec(int dtype, const float* x, int n, const void* w, float* y, int rows, void* stream) {
+  if ((dtype != kQ4K && dtype != kQ6K) || n <= 0 || n % 256 || rows <= 0) return NRQ_LAUNCH_TOO_WIDE;
+  const int bpr = n / 256;
+  WsArgs A{};
+  A.w[0] = (const uint8_t*)w;
+  A.y[0] = y;
+  A.rows[0] = rows;
+  A.nmat = 1;
+  A.nx = x;
+  const bool urm = ws_u_rowmajor(bpr);
+  if (dtype == kQ4K) {
+    const int rpw = ws_rows_per_wave<kQ4K>(bpr, 0);
+    return urm ? launch_ws_t<kQ4K, 4, 2, kWsQuant | kWsRowMajorU>(A, bpr, rpw, stream)
+               : launch_ws_t<kQ4K, 4, 2, kWsQuant>(A, bpr, rpw, stream);
+  }
+  const int rpw = ws_rows_per_wave<kQ6K>(bpr, 0);
+  return urm ? launch_ws_t<kQ6K, 4, 2, kWsQuant | kWsRowMajorU>(A, bpr, rpw, stream)
+             : launch_ws_t<kQ6K, 4, 2, kWsQuant>(A, bpr, rpw, stream);
 }
 
 // Up to three matrices of one format over one activation in one launch
