@@ -152,6 +152,38 @@ def graph_time(stream, launch, k, flush=None):
     return s, s / k
 
 
+def measure_read(nbytes, steps):
+    """The plain streaming-read rate at `nbytes` per launch (nrq_dev_stream_read),
+    timed like the matvecs: K launches in one graph over rotating copies after a
+    MALL flush. The ceiling a bandwidth-bound matvec of that size can reach."""
+    import torch
+
+    import nightrun_amd
+    from nightrun_amd import _lib
+
+    nightrun_amd.init(0)
+    n16 = -(-nbytes // 16)
+    copies = max(2, min(steps, -(-(2 * MALL_BYTES) // (16 * n16))))
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        bufs = [torch.ones(n16 * 4, dtype=torch.int32, device="cuda") for _ in range(copies)]
+        out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream.synchronize()
+    flush = MallFlush()
+
+    def step(i):
+        _lib.check(_lib.lib().nrq_dev_stream_read(bufs[i % copies].data_ptr(), 16 * n16, out.data_ptr(),
+                                                  stream.cuda_stream))
+
+    for i in range(3):
+        step(i)
+    wall, per = graph_time(stream, step, steps, flush)
+    del bufs
+    torch.cuda.empty_cache()
+    return {"bytes": 16 * n16, "us": round(per * 1e6, 3), "gbs": round(16 * n16 / per / 1e9, 1),
+            "frac_of_peak": round(16 * n16 / per / 1e9 / HBM_PEAK_GBS, 4), "copies": copies}
+
+
 def measure_matvec(name, steps, warmup, order):
     import torch
 
@@ -721,6 +753,9 @@ def main():
         o = measure_matvec(name, args.steps, args.warmup, order)
         others[name] = {k: round(v, 3) if isinstance(v, float) else v for k, v in o.items()}
         progress(f"{name} matvec {o['kernel_us']:.3f} us")
+    ceil = {name: measure_read(algorithmic_bytes(CONFIGS[name][0], CONFIGS[name][1], CONFIGS[name][2]), args.steps)
+            for name in [args.config] + [s for s in args.also.split(",") if s and s != args.config]}
+    progress("read ceiling")
     prefill = None if args.no_prefill else measure_prefill()
     if prefill is not None:
         progress("prefill layer")
@@ -773,9 +808,11 @@ def main():
             "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": MEASURED_TRAFFIC.get((args.config, args.order)),
             "kernel_us": round(r["kernel_us"], 3),
+            "read_ceiling": {**ceil[args.config], "kernel_frac_of_read": round(r["kernel_gbs"] / ceil[args.config]["gbs"], 4),
+                             "what": "a plain streaming read of the same bytes per launch, timed the same way"},
         },
         "cpu_baseline": cpu,
-        "other_configs": others,
+        "other_configs": {k: {**v, "read_ceiling": ceil.get(k)} for k, v in others.items()},
         "prefill": prefill,
         "decode": decode,
         "decode_qwen3": qwen3,

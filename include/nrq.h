@@ -149,6 +149,11 @@ int nrq_dev_mathf(int fn, const float *x, float *y, size_t n, void *stream);
 int nrq_dev_rmsnorm(const float *x, const float *w, float *out, size_t rows, size_t n, float eps, void *stream);
 /* Waits for all work on `stream` (NULL = library stream). */
 int nrq_sync(void *stream);
+/* A plain streaming read of `bytes` (16-byte aligned units) of device memory,
+ * xor-folded (out is written only on a 2^-32 chance): no reference
+ * counterpart; the read rate the matvecs are measured against on the same
+ * GPU. */
+int nrq_dev_stream_read(const void *data, size_t bytes, uint32_t *out, void *stream);
 
 /* ---- decode and prefill of a whole model on one GPU ---------------------------------
  * The forward pass of crates/nr-model/src/infer.rs (InferCtx) for the three

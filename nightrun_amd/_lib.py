@@ -55,6 +55,7 @@ SIGNATURES = {
     "nrq_dev_quantize_q8k": ([_vp, _sz, _vp, _vp], _i),
     "nrq_dev_block_sums": ([_i, _vp, _vp, _vp, _sz, _sz, _vp], _i),
     "nrq_sync": ([_vp], _i),
+    "nrq_dev_stream_read": ([_vp, _sz, _vp, _vp], _i),
     "nrq_dev_mathf": ([_i, _vp, _vp, _sz, _vp], _i),
     "nrq_dev_rmsnorm": ([_vp, _vp, _vp, _sz, _sz, C.c_float, _vp], _i),
     "nrq_model_create": ([_vp, C.POINTER(_vp)], _i),

@@ -460,4 +460,12 @@ int nrq_sync(void* stream) {
   return NRQ_OK;
 }
 
+int nrq_dev_stream_read(const void* data, size_t bytes, uint32_t* out, void* stream) {
+  if (!S().init) return fail(NRQ_ERR_NOT_INIT, "nrq_dev_stream_read: nrq_init was not called");
+  if (!out || (bytes && !data)) return fail(NRQ_ERR_ARG, "nrq_dev_stream_read: null pointer");
+  if (((uintptr_t)data & 15) || (bytes & 15)) return fail(NRQ_ERR_ARG, "nrq_dev_stream_read: needs 16-byte units");
+  return launch_rc(nrq::launch_stream_read(data, (long long)bytes, out, stream_or_default(stream)),
+                   "nrq_dev_stream_read");
+}
+
 }  // extern "C"

@@ -106,6 +106,7 @@ int launch_mmt_group(int dtype, const MatmulGroupLaunch& G);
 int launch_quantize_q8_0(const QuantLaunch& L);
 // y[0..n) = +0.0 (a kernel, not hipMemsetAsync, so it is safe under graph capture)
 int launch_fill_zero(float* y, long long n, void* stream);
+int launch_stream_read(const void* p, long long bytes, uint32_t* out, void* stream);
 int launch_quantize_q8k(const QuantLaunch& L);
 // Q4_K/Q6_K/Q8_0 per-(row, block) exact integer sums (test/diagnostic path).
 int launch_block_sums(int dtype, const void* w, const void* x, int32_t* out, int rows, int bpr, void* stream);
