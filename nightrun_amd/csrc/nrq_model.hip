@@ -407,6 +407,10 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q,
 }
 
 constexpr int kAttNT = 1024;
+// Threads of attention_kernel: 1024, or 768 for 96- and 128-wide heads, whose
+// key rows (16 pieces of 16 bytes per position) need the 168 registers per
+// lane that twelve waves leave (sixteen waves leave 128, and spill)
+__host__ __device__ constexpr int att_threads(int hd) { return hd >= 96 ? 768 : kAttNT; }
 constexpr int kAttMaxCtx = 8192;
 constexpr int kAttProd = 8704;  // floats per product stage (head_dim x (chunk + 4) <= 8704)
 constexpr int kAttRing = 3 * 1024 * 16;  // bytes of the value ring: three chunks of at most 1024 pieces
@@ -437,8 +441,8 @@ constexpr int kAttRing = 3 * 1024 * 16;  // bytes of the value ring: three chunk
 // value row, its own included, is read from the cache (the chunk's rows were
 // all appended before this launch); out and out_q8 are row i of [B][...].
 // LDS: att[ctx] | prod[2][kAttProd] | q[hd] | kcur[hd] | vcur[hd] | red[32]
-template <int HD, bool PF = false>
-__global__ __launch_bounds__(kAttNT) void attention_kernel(
+template <int HD, bool PF = false, int NT = att_threads(HD)>
+__global__ __launch_bounds__(NT) void attention_kernel(
     const float* __restrict__ q_in, const float* __restrict__ k_in, const float* __restrict__ v_in,
     const float* __restrict__ rope_cs, const int* __restrict__ ctl, int n_heads, int n_kv_heads, int ctx, int layer,
     float scale, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, float* __restrict__ out,
@@ -448,7 +452,7 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   constexpr int CP = C + 4;
   static_assert(HD * CP <= kAttProd, "product chunk exceeds its LDS stage");
   constexpr int cw = (HD + 63) / 64;  // chain waves
-  constexpr int nprod = kAttNT - 64 * cw;
+  constexpr int nprod = NT - 64 * cw;
   constexpr int npc = C * g8;  // 16-byte value pieces per chunk
   static_assert(npc <= 2 * nprod, "two pieces per producer thread");
   static_assert(npc % 64 == 0 && 3 * npc * 16 <= kAttRing, "whole-wave DMAs within the value ring");
@@ -529,19 +533,19 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
     asm volatile("" ::: "memory");
   };
   load_key(tid, kr);
-  if constexpr (kTwoRounds) load_key(tid + kAttNT, kr2);
+  if constexpr (kTwoRounds) load_key(tid + NT, kr2);
   if (producer) {
     vload(0);
     vload(1);
     vload(2);
   }
   if (PF) {
-    for (int i = tid; i < hd; i += kAttNT) qs[i] = q_in[(size_t)h * hd + i];
+    for (int i = tid; i < hd; i += NT) qs[i] = q_in[(size_t)h * hd + i];
   } else if (qn || neox) {
     // Qwen3: the head's q and its KV head's k RMS-normalized (vec.rs:17-28,
     // infer.rs:533-541; squares in the product stage, free until the scores),
     // then rope with pair j = (j, j + hd/2) when neox; in LDS, in place.
-    for (int i = tid; i < hd; i += kAttNT) {
+    for (int i = tid; i < hd; i += NT) {
       qs[i] = q_in[(size_t)h * hd + i];
       kcur[i] = k_in[(size_t)g * hd + i];
     }
@@ -549,7 +553,7 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
     if (qn) {
       float* sqq = prod;
       float* sqk = prod + hd;
-      for (int i = tid; i < hd; i += kAttNT) {
+      for (int i = tid; i < hd; i += NT) {
         sqq[i] = qs[i] * qs[i];
         sqk[i] = kcur[i] * kcur[i];
       }
@@ -558,13 +562,13 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
       if (tid == 64) red[1] = 1.0f / sqrtf(chain_sum(sqk, hd) / (float)hd + eps);
       __syncthreads();
       const float sq_ = red[0], sk_ = red[1];
-      for (int i = tid; i < hd; i += kAttNT) {
+      for (int i = tid; i < hd; i += NT) {
         qs[i] = qs[i] * (sq_ * qn[i]);
         kcur[i] = kcur[i] * (sk_ * kn[i]);
       }
       __syncthreads();
     }
-    for (int i = tid; i < half; i += kAttNT) {
+    for (int i = tid; i < half; i += NT) {
       const int ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
       const float cs = rope_cs[2 * i], sn = rope_cs[2 * i + 1];
       const float qa = qs[ia], qb = qs[ib];
@@ -579,13 +583,13 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
         kc[kvi(pos, ib)] = (uint16_t)k1;
       }
     }
-    for (int i = tid; i < hd; i += kAttNT) {
+    for (int i = tid; i < hd; i += NT) {
       const uint32_t vb = f32_to_f16_bits(v_in[(size_t)g * hd + i]);
       vcur[i] = f16_bits_to_f32(vb);
       if (writer) vc[kvi(pos, i)] = (uint16_t)vb;
     }
   } else {
-  for (int i = tid; i < half; i += kAttNT) {
+  for (int i = tid; i < half; i += NT) {
     const float cs = rope_cs[2 * i], sn = rope_cs[2 * i + 1];
     const float qa = q_in[(size_t)h * hd + 2 * i], qb = q_in[(size_t)h * hd + 2 * i + 1];
     qs[2 * i] = qa * cs - qb * sn;
@@ -599,14 +603,14 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
       kc[kvi(pos, 2 * i + 1)] = (uint16_t)k1;
     }
   }
-  for (int i = tid; i < hd; i += kAttNT) {
+  for (int i = tid; i < hd; i += NT) {
     const uint32_t vb = f32_to_f16_bits(v_in[(size_t)g * hd + i]);
     vcur[i] = f16_bits_to_f32(vb);
     if (writer) vc[kvi(pos, i)] = (uint16_t)vb;
   }
   }
   __syncthreads();
-  // Scores: thread tid takes positions tid, tid + kAttNT, ...
+  // Scores: thread tid takes positions tid, tid + NT, ...
   float mx = -INFINITY;
   auto score = [&](int t, const uint4* r) {
     float s = 0.0f;
@@ -628,12 +632,12 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
     mx = fmaxf(mx, a);
   };
   if (tid < n) score(tid, kr);
-  int t1 = tid + kAttNT;
+  int t1 = tid + NT;
   if constexpr (kTwoRounds) {
     if (t1 < n) score(t1, kr2);
-    t1 += kAttNT;
+    t1 += NT;
   }
-  for (; t1 < n; t1 += kAttNT) {
+  for (; t1 < n; t1 += NT) {
     load_key(t1, kr);
     score(t1, kr);
   }
@@ -643,11 +647,11 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
   mx = red[0];
-  for (int w = 1; w < kAttNT / 64; w++) mx = fmaxf(mx, red[w]);
+  for (int w = 1; w < NT / 64; w++) mx = fmaxf(mx, red[w]);
   // exps, then zeros up to a multiple of 128: adding +0 leaves the
   // (non-negative) sum unchanged, and the whole sum takes the DPP path
   const int n128 = (n + 127) & ~127;
-  for (int t = tid; t < n128; t += kAttNT) att[t] = t < n ? dev_expf(att[t] - mx) : 0.0f;
+  for (int t = tid; t < n128; t += NT) att[t] = t < n ? dev_expf(att[t] - mx) : 0.0f;
   __syncthreads();
   if (tid < 64) {
     const float tot = wave_chain_from(att, n128, 0.0f);
@@ -655,7 +659,7 @@ __global__ __launch_bounds__(kAttNT) void attention_kernel(
   }
   __syncthreads();
   const float inv = red[16];
-  for (int t = tid; t < n; t += kAttNT) att[t] = att[t] * inv;
+  for (int t = tid; t < n; t += NT) att[t] = att[t] * inv;
   auto vprod = [&](int c) {
     float* pb = prod + (c & 1) * kAttProd;
     const uint4* r = vring + (size_t)(c % 3) * npc;
@@ -1577,7 +1581,7 @@ int enqueue_step(nrq_model* m) {
                    : c.head_dim == 64 ? nrq::attention_kernel<64>
                    : c.head_dim == 96 ? nrq::attention_kernel<96>
                                       : nrq::attention_kernel<128>;
-      hipLaunchKernelGGL(kern, dim3(c.n_heads), dim3(nrq::kAttNT), m->att_lds, m->stream, m->q, m->k, m->v,
+      hipLaunchKernelGGL(kern, dim3(c.n_heads), dim3(nrq::att_threads(c.head_dim)), m->att_lds, m->stream, m->q, m->k, m->v,
                          m->rope_cs, m->ctl, c.n_heads, c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->attn,
                          q8 ? m->xq : nullptr, Ly.q_norm, Ly.k_norm, c.norm_eps, m->rope_neox);
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: attention launch failed");
@@ -1797,7 +1801,8 @@ int enqueue_prefill(nrq_model* m, int B) {
                      : c.head_dim == 64 ? nrq::attention_kernel<64, true>
                      : c.head_dim == 96 ? nrq::attention_kernel<96, true>
                                         : nrq::attention_kernel<128, true>;
-        hipLaunchKernelGGL(kern, dim3(c.n_heads, B), dim3(nrq::kAttNT), m->att_lds, m->stream, m->bq, m->bk, m->bv,
+        hipLaunchKernelGGL(kern, dim3(c.n_heads, B), dim3(nrq::att_threads(c.head_dim)), m->att_lds, m->stream, m->bq,
+                           m->bk, m->bv,
                            m->brope, m->ctl, c.n_heads, c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->battn,
                            q8 ? m->bxq : nullptr, nullptr, nullptr, 0.0f, 0);
       }
