@@ -313,6 +313,169 @@ __device__ inline float wave_chain_from(const float* __restrict__ a, int n, floa
 #undef NRQ_DPP_ADD16
 #undef NRQ_DPP_ADD
 
+// Inclusive prefix sum over the wave's 64 lanes (all active): row shifts
+// within each 16-lane row, then the row totals through row_bcast:15/31.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x) {
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+  return x;
+}
+
+// Inclusive prefix sum of f32 over the wave (any association: a prediction only).
+__device__ __forceinline__ float wave_incl_scan_f32(float x) {
+  x = x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, false));
+  x = x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, false));
+  x = x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, false));
+  x = x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, false));
+  x = x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));
+  x = x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xc, 0xf, false));
+  return x;
+}
+
+__device__ __forceinline__ int f32_exp(float x) { return (int)((__float_as_uint(x) >> 23) & 0xffu) - 127; }
+
+// One pass of wave_chain_nonneg over a[0 .. m), m <= 64 * RL: s <- s + a[0] +
+// ... + a[m-1] exactly as the sequential f32
+// chain gives it. Returns false (s unchanged) when the pass cannot vouch for its
+// result; the caller then runs the plain chain over the same terms.
+//
+// While the running sum s is a normal float in one binade [2^E, 2^(E+1)), it is
+// a multiple of the binade's unit u = 2^(E-23), and so is every rounded s + a.
+// Round-to-nearest-even of s + a then equals s + (a rounded to a multiple of u)
+// as long as the exact s + a stays below 2^(E+1), except when a is an odd half
+// of u away from a multiple (a tie, whose direction depends on s). So with
+// S = s / u, an integer in [2^23, 2^24], a run of terms in one binade is S plus
+// an integer prefix sum of the terms' roundings, exact in 32-bit integers.
+//
+// Lane l takes terms RL*l .. RL*l + RL-1. An approximate f32 prefix sum (its
+// association does not matter) predicts the binade each term is added in. Each
+// term is rounded with the unit of its predicted binade, except the terms after
+// which the predicted binade changes (crossings) and ties: those "special" terms
+// count 0 in the integer prefix sum and are added as ordinary f32 adds by a
+// loop, in order, which checks each prediction against the exact sum: each run
+// of terms between special ones must end below 2^(E+1) in the binade predicted
+// for it, and each special term must land in the binade predicted after it.
+// A term that is negative or not finite, and a sum outside [2^-100, 2^127),
+// fail the pass.
+template <int RL>
+__device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, float& s) {
+  static_assert(RL % 4 == 0, "whole 16-byte reads per lane");
+  const uint32_t sb = __builtin_amdgcn_readfirstlane(__float_as_uint(s));
+  if (sb - 0x0d800000u >= 0x7f000000u - 0x0d800000u) return false;  // positive, biased exponent 27 .. 253
+  const float s_in = __uint_as_float(sb);
+  const int lane = threadIdx.x & 63;
+  const int base = RL * lane;
+  float av[RL];
+  const float4* a4 = (const float4*)a;
+  const int last4 = (m >> 2) - 1;
+#pragma unroll
+  for (int k = 0; k < RL / 4; k++) {
+    const float4 v = a4[min(base / 4 + k, last4)];
+    av[4 * k] = v.x;
+    av[4 * k + 1] = v.y;
+    av[4 * k + 2] = v.z;
+    av[4 * k + 3] = v.w;
+  }
+  uint32_t mx = 0u;
+  float tot = 0.0f;
+#pragma unroll
+  for (int j = 0; j < RL; j++) {
+    av[j] = base + j < m ? av[j] : 0.0f;
+    mx = max(mx, __float_as_uint(av[j]));
+    tot = tot + av[j];
+  }
+  if (__ballot(mx >= 0x7f800000u) != 0) return false;  // every term a finite float >= +0
+  const float inclF = wave_incl_scan_f32(tot);
+  const float exclF = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(inclF), 0x138, 0xf, 0xf, false));  // wave_shr:1
+  const float totF = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inclF), 63));
+  const float p0 = s_in + exclF;  // predicted sum before the lane's first term
+  uint32_t ef[RL + 1];            // exponent field of the predicted sum before term j
+  float p = p0;
+#pragma unroll
+  for (int j = 0; j < RL; j++) {
+    ef[j] = __float_as_uint(p) & 0x7f800000u;
+    p = p + av[j];
+  }
+  // after the lane's last term: the next lane's first prediction (wave_shl:1)
+  ef[RL] = (uint32_t)__builtin_amdgcn_update_dpp(__float_as_int(s_in + totF), __float_as_int(p0), 0x130, 0xf, 0xf, false) &
+           0x7f800000u;
+  uint32_t cum[RL], special = 0u, racc = 0u;
+#pragma unroll
+  for (int j = 0; j < RL; j++) {
+    const float q = av[j] * __uint_as_float(0x8a800000u - ef[j]);  // a / u: a power-of-two scaling
+    const uint32_t r = (uint32_t)__builtin_rintf(q);
+    const bool sp = ef[j] != ef[j + 1] || __builtin_amdgcn_fractf(q) == 0.5f;
+    racc += sp ? 0u : r;
+    cum[j] = racc;  // r <= 2^24, so the lane's sum stays below 2^28
+    special |= (sp ? 1u : 0u) << j;
+  }
+  const uint32_t incl = wave_incl_scan_u32(racc);  // wraps harmlessly: only run differences are used
+  const uint32_t excl = incl - racc;
+  const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+  uint32_t S = (sb & 0x7fffffu) | 0x800000u;
+  uint32_t Ef = sb & 0x7f800000u;  // exponent field of the exact running sum
+  uint32_t bstart = 0u;            // the integer prefix where the current run starts
+  // a special term costs the loop the time of ~30 plain-chain adds: past 16 of
+  // them (ties everywhere, say), the plain chain is cheaper (ordinary rows
+  // average 3.5 per pass)
+  for (int it = 0;; it++) {
+    const uint64_t msk = __ballot(special != 0u);
+    if (msk == 0) break;
+    if (it == 16) return false;
+    const int L = (int)__builtin_ctzll(msk);
+    const uint32_t spL = (uint32_t)__builtin_amdgcn_readlane((int)special, L);
+    const int J = (int)__builtin_ctz(spL);  // uniform: the arrays below are indexed in registers
+    const uint32_t before = (uint32_t)__builtin_amdgcn_readlane((int)(J ? excl + cum[J - 1] : excl), L);
+    const uint32_t eb = (uint32_t)__builtin_amdgcn_readlane((int)ef[J], L);
+    const uint32_t ea = (uint32_t)__builtin_amdgcn_readlane((int)ef[J + 1], L);
+    const float term = a[RL * L + J];
+    const uint32_t pre = before - bstart;
+    if (eb != Ef || pre >= (1u << 24) || S + pre >= (1u << 24)) return false;
+    const float se = (float)(S + pre) * __uint_as_float(Ef - (23u << 23));  // exact: S + pre < 2^24
+    const uint32_t nb = __builtin_amdgcn_readfirstlane(__float_as_uint(se + term));
+    if (nb - 0x0d800000u >= 0x7f000000u - 0x0d800000u || (nb & 0x7f800000u) != ea) return false;
+    Ef = nb & 0x7f800000u;
+    S = (nb & 0x7fffffu) | 0x800000u;
+    bstart = before;  // the special term's own rounding counted 0
+    if (lane == L) special = spL & (spL - 1u);
+  }
+  const uint32_t pre = total - bstart;
+  if (pre > (1u << 24) || S + pre > (1u << 24)) return false;  // exactly 2^(E+1) is exact too
+  s = (float)(S + pre) * __uint_as_float(Ef - (23u << 23));
+  return true;
+}
+
+// wave_chain_from's result, bit for bit, for terms that are finite and
+// nonnegative (squares), in fewer dependent steps: the first 128 terms, where
+// the sum crosses binades often, take the plain chain, then passes of 1024
+// terms (chain_pass) each fall back to the plain chain when they cannot vouch
+// for their result; a last run of fewer than 512 terms is cheaper on the plain
+// chain. A pass issues about four times the instructions of the plain chain
+// over the same terms, in a third of its time: it pays where the wave has its
+// SIMD to itself. Whole wave, a in LDS and 16-byte aligned, n a multiple of 4,
+// the result in every lane. The kernels' registers must leave room for the
+// pass's per-lane arrays (indexed by a uniform index in the loop over special
+// terms): a kernel near its register limit puts them on scratch.
+__device__ __forceinline__ float wave_chain_nonneg(const float* __restrict__ a, int n, float s) {
+  constexpr int RL = 16, P = 64 * RL;
+  if (n < 128 + 512) return wave_chain_from(a, n, s);
+  s = wave_chain_from(a, 128, s);
+  int i = 128;
+  // whole passes: a constant count, so the tail's masking folds away here
+  for (; i + P <= n; i += P)
+    if (!chain_pass<RL>(a + i, P, s)) s = wave_chain_from(a + i, P, s);
+  if (n - i >= 512) {
+    if (!chain_pass<RL>(a + i, n - i, s)) s = wave_chain_from(a + i, n - i, s);
+  } else if (n > i) {
+    s = wave_chain_from(a + i, n - i, s);
+  }
+  return s;
+}
+
 // musl scalbnf
 __device__ __forceinline__ float dev_scalbnf(float x, int n) {
   float y = x;

@@ -310,7 +310,7 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
   }
   __syncthreads();
   if (tid < 64) {
-    const float ss = wave_chain_from(sq, n, 0.0f);
+    const float ss = wave_chain_nonneg(sq, n, 0.0f);
     if (tid == 0) s_scale = 1.0f / sqrtf(ss / (float)n + eps);
   }
   __syncthreads();

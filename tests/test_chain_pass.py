@@ -1,0 +1,199 @@
+"""The wave-parallel exact sum behind the decode norms (chain_pass and
+wave_chain_nonneg in nightrun_amd/csrc/nrq_device.h), restated lane for lane
+in numpy float32 and checked bit-exact against the sequential f32 chain, the
+reference's `ss += v * v` loop (crates/nr-model/src/vec.rs:4-14).
+
+The restatement follows the device code: 64 lanes of 16 consecutive terms, an
+f32 prediction of each term's binade, terms rounded to the unit of their
+predicted binade, special terms (binade crossings, ties) resolved in order by
+plain f32 adds, and every check that makes a pass fall back to the plain
+chain (more than 16 special terms in one pass among them). The cases are built
+to reach each of those checks; the fast path must also be the one taken on
+ordinary rows, or the device code would only ever run its fallback. On the
+GPU, tests/test_gpu_rmsnorm.py runs the kernel itself."""
+import numpy as np
+import pytest
+
+F32 = np.float32
+U32 = np.uint32
+RL = 16
+P = 64 * RL
+
+
+def bits(x):
+    return np.asarray(x, F32).view(U32)
+
+
+def f32(u):
+    return np.asarray(u, U32).view(F32)
+
+
+def serial(a, s):
+    """The sequential chain s + a[0] + ... + a[n-1], one rounding per add."""
+    s = F32(s)
+    for v in np.asarray(a, F32):
+        s = F32(s + v)
+    return s
+
+
+def chain_pass(a, s):
+    """(ok, s + a[0] + ... + a[m-1]) for m = len(a) <= 1024, as chain_pass<16>."""
+    m = len(a)
+    sb = int(bits(s))
+    if not (0x0D800000 <= sb < 0x7F000000):
+        return False, s
+    av = np.zeros(P, F32)
+    av[:m] = a
+    av = av.reshape(64, RL)
+    if int(bits(av).max()) >= 0x7F800000:
+        return False, s
+    tot = np.zeros(64, F32)
+    for j in range(RL):
+        tot = (tot + av[:, j]).astype(F32)
+    incl_f = np.cumsum(tot, dtype=F32)  # any association: a prediction
+    excl_f = np.concatenate([[F32(0)], incl_f[:-1]]).astype(F32)
+    p0 = (F32(s) + excl_f).astype(F32)
+    ef = np.zeros((64, RL + 1), U32)
+    p = p0.copy()
+    for j in range(RL):
+        ef[:, j] = bits(p) & 0x7F800000
+        p = (p + av[:, j]).astype(F32)
+    ef[:63, RL] = bits(p0[1:]) & 0x7F800000
+    ef[63, RL] = int(bits(F32(s) + incl_f[-1])) & 0x7F800000
+    inv_u = f32((0x8A800000 - ef[:, :RL].astype(np.int64)).astype(U32))
+    with np.errstate(over="ignore", invalid="ignore"):
+        q = (av * inv_u).astype(F32)
+        r = np.rint(np.clip(q, 0, 4294967040)).astype(np.uint64).astype(U32)
+        frac = (q - np.floor(q)).astype(F32)
+    sp = (ef[:, :RL] != ef[:, 1:]) | (frac == F32(0.5))
+    sp[(np.arange(64)[:, None] * RL + np.arange(RL)[None, :]) >= m] = False
+    r = np.where(sp, U32(0), r)
+    cum = np.cumsum(r, axis=1, dtype=U32)
+    racc = cum[:, -1]
+    incl = np.cumsum(racc, dtype=U32)
+    excl = (incl - racc).astype(U32)
+    total = int(incl[-1])
+    S = (sb & 0x7FFFFF) | 0x800000
+    Ef = sb & 0x7F800000
+    bstart = 0
+    for it, (L, J) in enumerate(zip(*np.nonzero(sp))):  # lane-major, term order within a lane
+        if it == 16:  # the plain chain is cheaper than more special terms
+            return False, s
+        before = (int(excl[L]) + (int(cum[L, J - 1]) if J else 0)) & 0xFFFFFFFF
+        pre = (before - bstart) & 0xFFFFFFFF
+        if int(ef[L, J]) != Ef or pre >= 1 << 24 or S + pre >= 1 << 24:
+            return False, s
+        se = F32(F32(S + pre) * f32(Ef - (23 << 23)))
+        nb = int(bits(F32(se + F32(a[RL * L + J]))))
+        if not (0x0D800000 <= nb < 0x7F000000) or (nb & 0x7F800000) != int(ef[L, J + 1]):
+            return False, s
+        Ef = nb & 0x7F800000
+        S = (nb & 0x7FFFFF) | 0x800000
+        bstart = before
+    pre = (total - bstart) & 0xFFFFFFFF
+    if pre > 1 << 24 or S + pre > 1 << 24:
+        return False, s
+    return True, F32(F32(S + pre) * f32(Ef - (23 << 23)))
+
+
+def chain_nonneg(a, s, stats=None):
+    """wave_chain_nonneg: 128 plain terms, then passes of up to 1024 terms while
+    at least 512 remain, then the plain chain."""
+    a = np.asarray(a, F32)
+    n = len(a)
+    if n < 128 + 512:
+        return serial(a, s)
+    s = serial(a[:128], s)
+    i = 128
+    while n - i >= 512:
+        m = min(P, n - i)
+        ok, out = chain_pass(a[i:i + m], s)
+        if stats is not None:
+            stats.append(ok)
+        s = out if ok else serial(a[i:i + m], s)
+        i += m
+    return serial(a[i:], s) if n > i else s
+
+
+def family(kind, n, rng):
+    g = rng.standard_normal(n).astype(F32)
+    if kind == "squares":
+        return (g * g).astype(F32)
+    if kind == "small_squares":
+        x = (g * F32(0.02)).astype(F32)
+        return (x * x).astype(F32)
+    if kind == "softmax":
+        return np.exp(-rng.uniform(0, 20, n)).astype(F32)
+    if kind == "ones_past_2p24":  # every term a tie once the sum passes 2^24
+        return np.ones(n, F32)
+    if kind == "quarters":
+        return (rng.integers(0, 4, n) * 0.25).astype(F32)
+    if kind == "powers_of_two":
+        return np.ldexp(F32(1), rng.integers(-30, 30, n)).astype(F32)
+    if kind == "huge_jumps":
+        return np.where(rng.integers(0, 50, n) == 0, F32(1e30), rng.random(n)).astype(F32)
+    if kind == "negatives":
+        return np.where(rng.integers(0, 200, n) == 0, -rng.random(n), rng.random(n)).astype(F32)
+    if kind == "nan_inf":
+        x = rng.random(n).astype(F32)
+        x[rng.integers(0, n, 2)] = [np.inf, np.nan]
+        return x
+    if kind == "subnormal":
+        return np.ldexp(rng.random(n), -140).astype(F32)
+    if kind == "near_overflow":
+        return (rng.random(n) * 3e37).astype(F32)
+    if kind == "halves":
+        return (rng.integers(0, 3, n) + 0.5).astype(F32)
+    if kind == "near_powers":  # sums that sit just below powers of two: mispredictions
+        x = (rng.random(n) * 1e-6).astype(F32)
+        x[::64] = (np.ldexp(F32(1), rng.integers(0, 8, len(x[::64]))) * (1 - 1e-7 * rng.integers(0, 40, len(x[::64]))))
+        return x.astype(F32)
+    raise ValueError(kind)
+
+
+KINDS = ["squares", "small_squares", "softmax", "ones_past_2p24", "quarters", "powers_of_two", "huge_jumps",
+         "negatives", "nan_inf", "subnormal", "near_overflow", "halves", "near_powers"]
+
+
+def same(x, y):
+    x, y = F32(x), F32(y)
+    return (np.isnan(x) and np.isnan(y)) or int(bits(x)) == int(bits(y))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_chain_matches_sequential_sum(kind):
+    rng = np.random.default_rng(KINDS.index(kind))
+    for t in range(8):
+        n = int(rng.choice([640, 1100, 2048, 2560, 4096, 5000]))
+        a = family(kind, n, rng)
+        s0 = F32(1 << 24) if kind == "ones_past_2p24" else (F32(rng.random() * 10) if t % 3 == 0 else F32(0))
+        want = F32(np.add.accumulate(np.concatenate([[s0], a]).astype(F32), dtype=F32)[-1])
+        assert same(want, serial(a, s0))
+        got = chain_nonneg(a, s0)
+        assert same(got, want), f"{kind} n={n}: {got!r} vs {want!r}"
+
+
+def test_ordinary_rows_take_the_fast_path():
+    rng = np.random.default_rng(7)
+    stats = []
+    for n in (2048, 2560, 4096):
+        for _ in range(6):
+            x = rng.standard_normal(n).astype(F32)
+            chain_nonneg((x * x).astype(F32), F32(0), stats)
+    assert len(stats) >= 30 and all(stats), f"{stats.count(False)} of {len(stats)} passes fell back"
+
+
+def test_a_planted_rounding_slip_is_caught():
+    """The bit-exact comparison has teeth: rounding every term down instead
+    of to nearest changes the sum of ordinary squares."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(2048).astype(F32)
+    a = (x * x).astype(F32)
+    want = serial(a, F32(0))
+    s = serial(a[:128], F32(0))
+    sb = int(bits(s))
+    S = (sb & 0x7FFFFF) | 0x800000
+    inv_u = f32(0x8A800000 - (sb & 0x7F800000))
+    slip = S + int(np.floor(a[128:512] * inv_u).astype(np.int64).sum())
+    assert not same(F32(F32(slip) * f32((sb & 0x7F800000) - (23 << 23))), serial(a[:512], F32(0)))
+    assert same(chain_nonneg(a, F32(0)), want)

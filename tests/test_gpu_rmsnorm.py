@@ -47,6 +47,20 @@ def rows_for(n, rng):
     ties = np.full(n, 2.0 ** -12)  # squares 2^-24: halves of the running sum's unit past 1
     ties[0] = 1.0
     out.append(("ties_after_one", ties))
+    # past the first 128 terms: the sum sits at 2^20 (unit 2^-3) and every square
+    # 1/16 is an exact tie, so each term ends a parallel run early
+    flat = np.full(n, 0.25)
+    flat[0] = 1024.0
+    out.append(("all_ties_steady", flat))
+    # squares m^2/16 against the unit 2^-3: odd m is a tie, even m exact
+    mix = 0.25 * rng.integers(1, 8, n) * rng.choice([-1, 1], n)
+    mix[0] = 1024.0
+    out.append(("mixed_ties_steady", mix))
+    # a slow ramp: the sum crosses binades at scattered positions late in the row
+    out.append(("late_crossings", np.sqrt(np.linspace(1e-3, 4.0, n)) * rng.choice([-1, 1], n)))
+    spikes = rng.normal(0, 1e-3, n)
+    spikes[rng.integers(128, n, 6)] = rng.normal(0, 30, 6)
+    out.append(("late_spikes", spikes))
     return out
 
 
