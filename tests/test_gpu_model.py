@@ -244,6 +244,16 @@ def test_llama_1b_greedy_token_identical(gpu, oracle):
     run_pair(oracle, cfg, w, 1152, prompt, 128, prefill=True)
 
 
+@pytest.mark.parametrize("ctx", [1024, 4096])
+def test_tiny_model_long_context(gpu, oracle, ctx):
+    """700 prompt positions (six 128-position chunks of the decode attention's
+    value loop), in a 1024- and a 4096-position cache (the attention's LDS
+    holds ctx scores): prefill and 12 greedy steps bit-exact with the oracle."""
+    w = oracle.gen_model(TINY, 3100 + ctx)
+    prompt = np.random.default_rng(ctx).integers(0, TINY["vocab"], 700).astype(np.uint32)
+    run_pair(oracle, TINY, w, ctx, prompt, 12, prefill=True)
+
+
 @pytest.mark.parametrize("n", [1, 5, 63, 64, 65, 70, 130])
 def test_tiny_model_prefill(gpu, oracle, n):
     """Device prefill (64-token batched chunks) == the oracle's prefill: the
