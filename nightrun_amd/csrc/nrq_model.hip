@@ -532,6 +532,25 @@ __global__ __launch_bounds__(NT) void attention_kernel(
     else if (vdma == 1) __builtin_amdgcn_s_waitcnt(2 | (7 << 4) | (15 << 8));
     asm volatile("" ::: "memory");
   };
+  // With the q/k norm (Qwen3), the step's own q, k, v, the norm weights and
+  // the rope table go to LDS before the cache rows are requested: the stores
+  // wait for these loads only, and the norms and rope below run while the
+  // cache rows arrive. (A load issued after the cache rows would wait for all
+  // of them: vmcnt counts in issue order.) stg sits in the product stages,
+  // free until the value loop.
+  float* stg = prod + 2 * hd;  // qn | kn | (cos, sin) pairs | v, hd floats each
+  const bool early = !PF && qn;
+  if (early) {
+    if (tid < hd) {
+      qs[tid] = q_in[(size_t)h * hd + tid];
+      kcur[tid] = k_in[(size_t)g * hd + tid];
+      stg[tid] = qn[tid];
+      stg[hd + tid] = kn[tid];
+      stg[2 * hd + tid] = rope_cs[tid];
+      stg[3 * hd + tid] = v_in[(size_t)g * hd + tid];
+    }
+    asm volatile("" ::: "memory");
+  }
   load_key(tid, kr);
   if constexpr (kTwoRounds) load_key(tid + NT, kr2);
   if (producer) {
@@ -545,9 +564,11 @@ __global__ __launch_bounds__(NT) void attention_kernel(
     // Qwen3: the head's q and its KV head's k RMS-normalized (vec.rs:17-28,
     // infer.rs:533-541; squares in the product stage, free until the scores),
     // then rope with pair j = (j, j + hd/2) when neox; in LDS, in place.
-    for (int i = tid; i < hd; i += NT) {
-      qs[i] = q_in[(size_t)h * hd + i];
-      kcur[i] = k_in[(size_t)g * hd + i];
+    if (!early) {
+      for (int i = tid; i < hd; i += NT) {
+        qs[i] = q_in[(size_t)h * hd + i];
+        kcur[i] = k_in[(size_t)g * hd + i];
+      }
     }
     __syncthreads();
     if (qn) {
@@ -562,15 +583,16 @@ __global__ __launch_bounds__(NT) void attention_kernel(
       if (tid == 64) red[1] = 1.0f / sqrtf(chain_sum(sqk, hd) / (float)hd + eps);
       __syncthreads();
       const float sq_ = red[0], sk_ = red[1];
-      for (int i = tid; i < hd; i += NT) {
-        qs[i] = qs[i] * (sq_ * qn[i]);
-        kcur[i] = kcur[i] * (sk_ * kn[i]);
+      for (int i = tid; i < hd; i += NT) {  // qn set: the weights are staged
+        qs[i] = qs[i] * (sq_ * stg[i]);
+        kcur[i] = kcur[i] * (sk_ * stg[hd + i]);
       }
       __syncthreads();
     }
     for (int i = tid; i < half; i += NT) {
       const int ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
-      const float cs = rope_cs[2 * i], sn = rope_cs[2 * i + 1];
+      const float cs = early ? stg[2 * hd + 2 * i] : rope_cs[2 * i];
+      const float sn = early ? stg[2 * hd + 2 * i + 1] : rope_cs[2 * i + 1];
       const float qa = qs[ia], qb = qs[ib];
       qs[ia] = qa * cs - qb * sn;
       qs[ib] = qa * sn + qb * cs;
@@ -584,7 +606,7 @@ __global__ __launch_bounds__(NT) void attention_kernel(
       }
     }
     for (int i = tid; i < hd; i += NT) {
-      const uint32_t vb = f32_to_f16_bits(v_in[(size_t)g * hd + i]);
+      const uint32_t vb = f32_to_f16_bits(early ? stg[3 * hd + i] : v_in[(size_t)g * hd + i]);
       vcur[i] = f16_bits_to_f32(vb);
       if (writer) vc[kvi(pos, i)] = (uint16_t)vb;
     }
