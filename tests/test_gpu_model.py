@@ -244,6 +244,56 @@ def test_llama_1b_greedy_token_identical(gpu, oracle):
     run_pair(oracle, cfg, w, 1152, prompt, 128, prefill=True)
 
 
+WIDE = dict(dim=2048, n_layers=1, n_heads=32, n_kv_heads=8, head_dim=64, ffn_dim=256, vocab=300, norm_eps=1e-5,
+            rope_theta=500000.0)
+
+
+def q8_0_row(q, d_bits):
+    """One embedding row of Q8_0 blocks: q (int8 values, len a multiple of 32)
+    with the f16 scale bits d_bits per block."""
+    q = np.asarray(q, np.int64).reshape(-1, 32)
+    d = np.broadcast_to(np.asarray(d_bits, np.uint16), (q.shape[0],))
+    out = np.zeros((q.shape[0], 34), np.uint8)
+    out[:, 0] = d & 0xFF
+    out[:, 1] = d >> 8
+    out[:, 2:] = (q & 0xFF).astype(np.uint8)
+    return out
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4k_m"])
+@pytest.mark.parametrize("prefill", [False, True])
+def test_wide_norm_sums_on_crafted_rows(gpu, oracle, fmt, prefill):
+    """Hidden width 2048, so the fused norms' sum of squares takes the
+    wave-parallel exact path. The prompt's embedding rows are crafted for
+    it: after a large first value every square is an exact tie (the pass gives
+    up past 16 special terms and falls back), squares mixing ties and exact
+    multiples of the unit, a ramp crossing binades late, and an ordinary row.
+    Logits and KV bit-identical to the oracle."""
+    w = oracle.gen_model(WIDE, 6161)
+    if fmt == "q4k_m":
+        shapes = oracle.layer_shapes(WIDE)
+        for l, lw in enumerate(w["layers"]):
+            for i, name in enumerate(oracle.LAYER_MATS):
+                dt = MIXES["q4k_m"][name]
+                rows, cols = shapes[name]
+                lw[name] = oracle.gen_weights(dt, 611 + 16 * l + i, rows, cols)
+                lw["dtypes"][name] = dt
+    dim, nb = WIDE["dim"], WIDE["dim"] // 32
+    emb = w["embed"].reshape(WIDE["vocab"], nb, 34)
+    rng = np.random.default_rng(61)
+    # f16 0x3000 = 0.125, 0x1800 = 2^-9
+    big_then_ties = np.ones(dim, np.int64)
+    big_then_ties[0] = 80  # x = 10 (d 0.125): the sum sits at 100, unit 2^-17
+    emb[1] = np.concatenate([q8_0_row(big_then_ties[:32], 0x3000), q8_0_row(big_then_ties[32:], 0x1800)])
+    mixed = rng.integers(1, 4, dim)  # squares (q * 2^-9)^2: q = 1, 3 ties, q = 2 exact
+    mixed[0] = 80
+    emb[2] = np.concatenate([q8_0_row(mixed[:32], 0x3000), q8_0_row(mixed[32:], 0x1800)])
+    ramp = np.clip(np.round(np.sqrt(np.linspace(1, 16000, dim))), 1, 127).astype(np.int64) * rng.choice([-1, 1], dim)
+    emb[3] = q8_0_row(ramp, 0x2000)  # d = 2^-7
+    prompt = np.array([1, 2, 3, 4, 1, 3], np.uint32)  # token 4: an ordinary generated row
+    run_pair(oracle, WIDE, w, 32, prompt, 4, prefill=prefill)
+
+
 @pytest.mark.parametrize("ctx", [1024, 4096])
 def test_tiny_model_long_context(gpu, oracle, ctx):
     """700 prompt positions (six 128-position chunks of the decode attention's
