@@ -339,9 +339,9 @@ __device__ __forceinline__ float wave_incl_scan_f32(float x) {
 __device__ __forceinline__ int f32_exp(float x) { return (int)((__float_as_uint(x) >> 23) & 0xffu) - 127; }
 
 // One pass of wave_chain_nonneg over a[0 .. m), m <= 64 * RL: s <- s + a[0] +
-// ... + a[m-1] exactly as the sequential f32
-// chain gives it. Returns false (s unchanged) when the pass cannot vouch for its
-// result; the caller then runs the plain chain over the same terms.
+// ... + a[m-1] exactly as the sequential f32 chain gives it. Returns false (s
+// unchanged) when the pass cannot vouch for its result; the caller then runs
+// the plain chain over the same terms.
 //
 // While the running sum s is a normal float in one binade [2^E, 2^(E+1)), it is
 // a multiple of the binade's unit u = 2^(E-23), and so is every rounded s + a.
@@ -408,7 +408,9 @@ __device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, f
   for (int j = 0; j < RL; j++) {
     const float q = av[j] * __uint_as_float(0x8a800000u - ef[j]);  // a / u: a power-of-two scaling
     const uint32_t r = (uint32_t)__builtin_rintf(q);
-    const bool sp = ef[j] != ef[j + 1] || __builtin_amdgcn_fractf(q) == 0.5f;
+    // only real terms are special: the zeros past m add nothing, and a zero in a
+    // lane's last slot may sit between two predictions made in different orders
+    const bool sp = base + j < m && (ef[j] != ef[j + 1] || __builtin_amdgcn_fractf(q) == 0.5f);
     racc += sp ? 0u : r;
     cum[j] = racc;  // r <= 2^24, so the lane's sum stays below 2^28
     special |= (sp ? 1u : 0u) << j;
@@ -455,7 +457,7 @@ __device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, f
 // terms (chain_pass) each fall back to the plain chain when they cannot vouch
 // for their result; a last run of fewer than 512 terms is cheaper on the plain
 // chain. A pass issues about four times the instructions of the plain chain
-// over the same terms, in a third of its time: it pays where the wave has its
+// over the same terms, in about half its time: it pays where the wave has its
 // SIMD to itself. Whole wave, a in LDS and 16-byte aligned, n a multiple of 4,
 // the result in every lane. The kernels' registers must leave room for the
 // pass's per-lane arrays (indexed by a uniform index in the loop over special

@@ -66,7 +66,7 @@ def chain_pass(a, s):
         r = np.rint(np.clip(q, 0, 4294967040)).astype(np.uint64).astype(U32)
         frac = (q - np.floor(q)).astype(F32)
     sp = (ef[:, :RL] != ef[:, 1:]) | (frac == F32(0.5))
-    sp[(np.arange(64)[:, None] * RL + np.arange(RL)[None, :]) >= m] = False
+    sp[(np.arange(64)[:, None] * RL + np.arange(RL)[None, :]) >= m] = False  # only real terms (as the device code)
     r = np.where(sp, U32(0), r)
     cum = np.cumsum(r, axis=1, dtype=U32)
     racc = cum[:, -1]
