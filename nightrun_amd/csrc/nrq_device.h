@@ -355,15 +355,25 @@ __device__ __forceinline__ int f32_exp(float x) { return (int)((__float_as_uint(
 // association does not matter) predicts the binade each term is added in. Each
 // term is rounded with the unit of its predicted binade, except the terms after
 // which the predicted binade changes (crossings) and ties: those "special" terms
-// count 0 in the integer prefix sum and are added as ordinary f32 adds by a
-// loop, in order, which checks each prediction against the exact sum: each run
+// count 0 in the integer prefix sum and are added as ordinary f32 adds, in
+// order, by a chain that checks each prediction against the exact sum: each run
 // of terms between special ones must end below 2^(E+1) in the binade predicted
 // for it, and each special term must land in the binade predicted after it.
+// (The binade predicted before a special term is the one predicted after the
+// previous special term, or s's own for the first: lane 0 predicts from s
+// itself, and the predicted binade only changes at special terms.)
 // A term that is negative or not finite, and a sum outside [2^-100, 2^127),
 // fail the pass.
+//
+// The special terms' indices go to lanes 0, 1, ... in term order (a prefix sum
+// of the lanes' counts places them); one gather from work (the integer prefix
+// before each term and the binade predicted after it, which the pass writes)
+// and from a fetches their data. Only the f32 adds run one special term at a
+// time; every check runs on all of them at once afterwards.
 template <int RL>
-__device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, float& s) {
+__device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, float& s, uint32_t* __restrict__ work) {
   static_assert(RL % 4 == 0, "whole 16-byte reads per lane");
+  constexpr int kMaxSpecial = 48;  // past this many, the plain chain is cheaper
   const uint32_t sb = __builtin_amdgcn_readfirstlane(__float_as_uint(s));
   if (sb - 0x0d800000u >= 0x7f000000u - 0x0d800000u) return false;  // positive, biased exponent 27 .. 253
   const float s_in = __uint_as_float(sb);
@@ -403,7 +413,7 @@ __device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, f
   // after the lane's last term: the next lane's first prediction (wave_shl:1)
   ef[RL] = (uint32_t)__builtin_amdgcn_update_dpp(__float_as_int(s_in + totF), __float_as_int(p0), 0x130, 0xf, 0xf, false) &
            0x7f800000u;
-  uint32_t cum[RL], special = 0u, racc = 0u;
+  uint32_t cum[RL], special = 0u, racc = 0u;  // cum[j]: the lane's roundings before term j
 #pragma unroll
   for (int j = 0; j < RL; j++) {
     const float q = av[j] * __uint_as_float(0x8a800000u - ef[j]);  // a / u: a power-of-two scaling
@@ -411,39 +421,67 @@ __device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, f
     // only real terms are special: the zeros past m add nothing, and a zero in a
     // lane's last slot may sit between two predictions made in different orders
     const bool sp = base + j < m && (ef[j] != ef[j + 1] || __builtin_amdgcn_fractf(q) == 0.5f);
-    racc += sp ? 0u : r;
-    cum[j] = racc;  // r <= 2^24, so the lane's sum stays below 2^28
+    cum[j] = racc;
+    racc += sp ? 0u : r;  // r <= 2^24, so the lane's sum stays below 2^28
     special |= (sp ? 1u : 0u) << j;
   }
   const uint32_t incl = wave_incl_scan_u32(racc);  // wraps harmlessly: only run differences are used
   const uint32_t excl = incl - racc;
   const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-  uint32_t S = (sb & 0x7fffffu) | 0x800000u;
   uint32_t Ef = sb & 0x7f800000u;  // exponent field of the exact running sum
   uint32_t bstart = 0u;            // the integer prefix where the current run starts
-  // a special term costs the loop the time of ~30 plain-chain adds: past 16 of
-  // them (ties everywhere, say), the plain chain is cheaper (ordinary rows
-  // average 3.5 per pass)
-  for (int it = 0;; it++) {
-    const uint64_t msk = __ballot(special != 0u);
-    if (msk == 0) break;
-    if (it == 16) return false;
-    const int L = (int)__builtin_ctzll(msk);
-    const uint32_t spL = (uint32_t)__builtin_amdgcn_readlane((int)special, L);
-    const int J = (int)__builtin_ctz(spL);  // uniform: the arrays below are indexed in registers
-    const uint32_t before = (uint32_t)__builtin_amdgcn_readlane((int)(J ? excl + cum[J - 1] : excl), L);
-    const uint32_t eb = (uint32_t)__builtin_amdgcn_readlane((int)ef[J], L);
-    const uint32_t ea = (uint32_t)__builtin_amdgcn_readlane((int)ef[J + 1], L);
-    const float term = a[RL * L + J];
-    const uint32_t pre = before - bstart;
-    if (eb != Ef || pre >= (1u << 24) || S + pre >= (1u << 24)) return false;
-    const float se = (float)(S + pre) * __uint_as_float(Ef - (23u << 23));  // exact: S + pre < 2^24
-    const uint32_t nb = __builtin_amdgcn_readfirstlane(__float_as_uint(se + term));
-    if (nb - 0x0d800000u >= 0x7f000000u - 0x0d800000u || (nb & 0x7f800000u) != ea) return false;
-    Ef = nb & 0x7f800000u;
-    S = (nb & 0x7fffffu) | 0x800000u;
-    bstart = before;  // the special term's own rounding counted 0
-    if (lane == L) special = spL & (spL - 1u);
+  uint32_t S = (sb & 0x7fffffu) | 0x800000u;
+  const uint32_t cnt = (uint32_t)__builtin_popcount(special);
+  const uint32_t cincl = wave_incl_scan_u32(cnt);
+  const int K = __builtin_amdgcn_readlane((int)cincl, 63);  // special terms in the pass
+  if (K != 0) {
+    if (K > kMaxSpecial) return false;
+    uint32_t* w_before = work;             // per term: the integer prefix before it
+    uint32_t* w_after = work + 64 * RL;    // per term: the binade predicted after it
+    uint32_t* w_index = work + 128 * RL;   // the special terms' indices, in order
+#pragma unroll
+    for (int k = 0; k < RL / 4; k++) {
+      ((uint4*)(w_before + base))[k] = make_uint4(excl + cum[4 * k], excl + cum[4 * k + 1], excl + cum[4 * k + 2],
+                                                  excl + cum[4 * k + 3]);
+      ((uint4*)(w_after + base))[k] = make_uint4(ef[4 * k + 1], ef[4 * k + 2], ef[4 * k + 3], ef[4 * k + 4]);
+    }
+    uint32_t rem = special, slot = cincl - cnt;
+    while (__ballot(rem != 0u) != 0) {
+      if (rem != 0u) {
+        w_index[slot++] = (uint32_t)(base + __builtin_ctz(rem));
+        rem &= rem - 1u;
+      }
+    }
+    const uint32_t idx = lane < K ? w_index[lane] : 0u;
+    const uint32_t g_before = w_before[idx], g_after = w_after[idx];
+    const float g_term = a[idx];
+    // the previous special term's prefix and binade after (the pass start's in lane 0)
+    uint32_t p_before = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)g_before, 0x138, 0xf, 0xf, false);
+    const uint32_t p_after = (uint32_t)__builtin_amdgcn_update_dpp((int)Ef, (int)g_after, 0x138, 0xf, 0xf, false);
+    // kept out of the subtraction: folded into it, as v_subrev_u32_dpp, the
+    // shift gave the difference with the opposite sign on gfx950
+    asm volatile("" : "+v"(p_before));
+    const uint32_t pre = g_before - p_before;  // the run before the special term
+    const float unit = __uint_as_float(p_after - (23u << 23));         // that run's unit
+    // S in a vector register: the chain below stays on the vector unit
+    uint32_t Sv = S, nbv = 0u;
+    asm volatile("" : "+v"(Sv));
+    for (int k = 0; k < K; k++) {
+      const uint32_t X = Sv + (uint32_t)__builtin_amdgcn_readlane((int)pre, k);
+      const float se = (float)X * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(unit), k));  // exact when X < 2^24
+      const uint32_t nb = __float_as_uint(se + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g_term), k)));
+      Sv = (nb & 0x7fffffu) | 0x800000u;
+      nbv = lane == k ? nb : nbv;
+    }
+    // lane k: the sum after special term k (nbv) and before it (S of the previous one, plus the run)
+    const uint32_t p_nb = (uint32_t)__builtin_amdgcn_update_dpp((int)sb, (int)nbv, 0x138, 0xf, 0xf, false);
+    const uint32_t X = ((p_nb & 0x7fffffu) | 0x800000u) + pre;
+    const bool bad = lane < K && ((pre >= (1u << 24)) | (X >= (1u << 24)) |
+                                  (nbv - 0x0d800000u >= 0x7f000000u - 0x0d800000u) | ((nbv & 0x7f800000u) != g_after));
+    if (__ballot(bad) != 0) return false;
+    S = __builtin_amdgcn_readfirstlane(Sv);
+    Ef = (uint32_t)__builtin_amdgcn_readlane((int)g_after, K - 1);
+    bstart = (uint32_t)__builtin_amdgcn_readlane((int)g_before, K - 1);
   }
   const uint32_t pre = total - bstart;
   if (pre > (1u << 24) || S + pre > (1u << 24)) return false;  // exactly 2^(E+1) is exact too
@@ -457,21 +495,22 @@ __device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, f
 // terms (chain_pass) each fall back to the plain chain when they cannot vouch
 // for their result; a last run of fewer than 512 terms is cheaper on the plain
 // chain. A pass issues about four times the instructions of the plain chain
-// over the same terms, in about half its time: it pays where the wave has its
-// SIMD to itself. Whole wave, a in LDS and 16-byte aligned, n a multiple of 4,
-// the result in every lane. The kernels' registers must leave room for the
-// pass's per-lane arrays (indexed by a uniform index in the loop over special
-// terms): a kernel near its register limit puts them on scratch.
-__device__ __forceinline__ float wave_chain_nonneg(const float* __restrict__ a, int n, float s) {
+// over the same terms, in a fraction of its time: it pays where the wave has
+// its SIMD to itself. Whole wave, a in LDS and 16-byte aligned, n a multiple of
+// 4, the result in every lane; work is kChainWork words of LDS that no other
+// wave touches meanwhile (n < 640 needs none).
+constexpr int kChainWork = 2 * 1024 + 64;
+__device__ __forceinline__ float wave_chain_nonneg(const float* __restrict__ a, int n, float s, uint32_t* __restrict__ work) {
   constexpr int RL = 16, P = 64 * RL;
+  static_assert(2 * P + 64 == kChainWork, "the pass records two words per term and one per lane");
   if (n < 128 + 512) return wave_chain_from(a, n, s);
   s = wave_chain_from(a, 128, s);
   int i = 128;
   // whole passes: a constant count, so the tail's masking folds away here
   for (; i + P <= n; i += P)
-    if (!chain_pass<RL>(a + i, P, s)) s = wave_chain_from(a + i, P, s);
+    if (!chain_pass<RL>(a + i, P, s, work)) s = wave_chain_from(a + i, P, s);
   if (n - i >= 512) {
-    if (!chain_pass<RL>(a + i, n - i, s)) s = wave_chain_from(a + i, n - i, s);
+    if (!chain_pass<RL>(a + i, n - i, s, work)) s = wave_chain_from(a + i, n - i, s);
   } else if (n > i) {
     s = wave_chain_from(a + i, n - i, s);
   }

@@ -263,6 +263,7 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
                                                        const float* __restrict__ w, int n, float eps, float rs,
                                                        float* __restrict__ out, uint8_t* __restrict__ xq) {
   __shared__ __align__(16) float sq[kNormMax];
+  __shared__ __align__(16) uint32_t chain_work[kChainWork];
   {
     const size_t r = blockIdx.x;
     x += r * n;
@@ -310,7 +311,7 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
   }
   __syncthreads();
   if (tid < 64) {
-    const float ss = wave_chain_nonneg(sq, n, 0.0f);
+    const float ss = wave_chain_nonneg(sq, n, 0.0f, chain_work);
     if (tid == 0) s_scale = 1.0f / sqrtf(ss / (float)n + eps);
   }
   __syncthreads();

@@ -536,7 +536,8 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
     ws_lds_barrier();
     float* scale_slot = sq + n;  // one float past the squares
     if (wave == 0) {
-      const float ss = wave_chain_nonneg(sq, n, 0.0f);
+      // the x and add stages (2n floats) are dead here: the pass workspace when n >= 1024
+      const float ss = n >= kChainWork / 2 ? wave_chain_nonneg(sq, n, 0.0f, (uint32_t*)nxs) : wave_chain_from(sq, n, 0.0f);
       if (lane == 0) scale_slot[0] = 1.0f / sqrtf(ss / (float)n + A.eps);
     }
     ws_lds_barrier();

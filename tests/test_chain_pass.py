@@ -7,7 +7,7 @@ The restatement follows the device code: 64 lanes of 16 consecutive terms, an
 f32 prediction of each term's binade, terms rounded to the unit of their
 predicted binade, special terms (binade crossings, ties) resolved in order by
 plain f32 adds, and every check that makes a pass fall back to the plain
-chain (more than 16 special terms in one pass among them). The cases are built
+chain (more than 48 special terms in one pass among them). The cases are built
 to reach each of those checks; the fast path must also be the one taken on
 ordinary rows, or the device code would only ever run its fallback. On the
 GPU, tests/test_gpu_rmsnorm.py runs the kernel itself."""
@@ -68,28 +68,34 @@ def chain_pass(a, s):
     sp = (ef[:, :RL] != ef[:, 1:]) | (frac == F32(0.5))
     sp[(np.arange(64)[:, None] * RL + np.arange(RL)[None, :]) >= m] = False  # only real terms (as the device code)
     r = np.where(sp, U32(0), r)
-    cum = np.cumsum(r, axis=1, dtype=U32)
-    racc = cum[:, -1]
+    racc = np.sum(r, axis=1, dtype=U32)
+    cum = (np.cumsum(r, axis=1, dtype=U32) - r).astype(U32)  # before term j
     incl = np.cumsum(racc, dtype=U32)
     excl = (incl - racc).astype(U32)
     total = int(incl[-1])
     S = (sb & 0x7FFFFF) | 0x800000
     Ef = sb & 0x7F800000
     bstart = 0
-    for it, (L, J) in enumerate(zip(*np.nonzero(sp))):  # lane-major, term order within a lane
-        if it == 16:  # the plain chain is cheaper than more special terms
-            return False, s
-        before = (int(excl[L]) + (int(cum[L, J - 1]) if J else 0)) & 0xFFFFFFFF
+    specials = list(zip(*np.nonzero(sp)))  # lane-major, term order within a lane
+    if len(specials) > 48:  # the plain chain is cheaper than more special terms
+        return False, s
+    # the binade predicted before each special term is the one predicted after
+    # the previous (s's own for the first): the device code relies on it
+    for k, (L, J) in enumerate(specials):
+        assert int(ef[L, J]) == (Ef if k == 0 else int(ef[specials[k - 1][0], specials[k - 1][1] + 1]))
+    ok = True
+    for L, J in specials:  # only the f32 adds are sequential; the checks could run after
+        before = (int(excl[L]) + int(cum[L, J])) & 0xFFFFFFFF
         pre = (before - bstart) & 0xFFFFFFFF
-        if int(ef[L, J]) != Ef or pre >= 1 << 24 or S + pre >= 1 << 24:
-            return False, s
-        se = F32(F32(S + pre) * f32(Ef - (23 << 23)))
+        X = S + pre
+        se = F32(F32(X & 0xFFFFFFFF) * f32((Ef - (23 << 23)) & 0xFFFFFFFF))
         nb = int(bits(F32(se + F32(a[RL * L + J]))))
-        if not (0x0D800000 <= nb < 0x7F000000) or (nb & 0x7F800000) != int(ef[L, J + 1]):
-            return False, s
-        Ef = nb & 0x7F800000
+        ok &= pre < 1 << 24 and X < 1 << 24 and 0x0D800000 <= nb < 0x7F000000 and (nb & 0x7F800000) == int(ef[L, J + 1])
+        Ef = int(ef[L, J + 1])
         S = (nb & 0x7FFFFF) | 0x800000
         bstart = before
+    if not ok:
+        return False, s
     pre = (total - bstart) & 0xFFFFFFFF
     if pre > 1 << 24 or S + pre > 1 << 24:
         return False, s
