@@ -7,6 +7,22 @@
  * -ffp-contract=off keeps every a*b+c as two rounded operations, as Rust
  * (which never contracts) evaluates them; the AVX2 restatements use explicit
  * _mm256_fmadd_ps exactly where the reference does.
+ *
+ * Pins (each function is checked against something other than itself):
+ *   f16 conversions   reference known values, all 65536 patterns against IEEE,
+ *                     hand-built subnormal ties (tests/test_oracle.py)
+ *   quantize_q8_0     ties away, the f32 `x + 0.5`, the -127 clamp, `v * inv`,
+ *   quantize_q8k      `amax / 127`, `iscale * v`, `d = 1 / iscale`: hand-derived
+ *                     blocks (tests/test_oracle_scalar_steps.py)
+ *   dot_q8_scalar     `(acc * dw) * dx` and the block chain
+ *                     (tests/test_oracle_scalar_steps.py, tests/test_oracle.py)
+ *   dot_q4k/q6k       the f32 step orders of the scalar and AVX2 kernels
+ *                     (tests/test_oracle_kquant_order.py,
+ *                     tests/test_oracle_scalar_steps.py)
+ *   AVX2 dots, x4     the hsum tree and per-block FMA (tests/test_oracle.py,
+ *                     tests/test_oracle_kquant_order.py); x4 == 1-wide
+ *   unpack, dequant   packer round trips over every 6-bit value
+ *   integer sums      brute force on independently unpacked quants
  */
 #include "nrq_oracle.h"
 

@@ -178,6 +178,63 @@ def test_quantize_device_entry_points(gpu, oracle):
     assert np.array_equal(ok.cpu().numpy().reshape(-1, 292), oracle.quantize_q8k(src))
 
 
+def test_hand_derived_step_pins_on_device(gpu):
+    """The blocks of tests/test_oracle_scalar_steps.py, whose results under the
+    reference's f32 steps are derived by hand there, through the device
+    quantizers, the decode matvec and both prefill tiles (16 x 16 under 1024
+    rows, 32 x 32 from 1024), compared with the hand-derived literals."""
+    import torch
+
+    from nightrun_amd import device
+    from tests.test_oracle_kquant_order import q6k_block, q8k_block
+    from tests.test_oracle_scalar_steps import q8_0_block
+
+    near = 0.5 - 2.0 ** -25
+    srcs = np.zeros((5, 32), dtype=np.float32)
+    srcs[0, :6] = [127.0, 2.5, -2.5, near, -near, 1.5 - 2.0 ** -23]
+    srcs[1, 3] = -177 * 2.0 ** -24
+    srcs[2, :2] = [130.96875, 15.984375 - 2.0 ** -20]
+    srcs[3, 7] = 127 * (1 + 2.0 ** -11) + 2.0 ** -17
+    o8 = torch.zeros(5 * 34, dtype=torch.uint8, device="cuda")
+    device.quantize_q8_0(dev(srcs.reshape(-1)), o8)
+    torch.cuda.synchronize()
+    b = o8.cpu().numpy().reshape(5, 34)
+    d = b[:, 0].astype(np.int64) | b[:, 1].astype(np.int64) << 8
+    qs = b[:, 2:].view(np.int8)
+    assert list(d[:4]) == [0x3C00, 0x0001, 0x3C20, 0x3C01]
+    assert list(qs[0, :6]) == [127, 3, -3, 1, -1, 1]
+    assert qs[1, 3] == -127 and list(qs[2, :2]) == [127, 16]
+
+    k = np.zeros((2, 256), dtype=np.float32)
+    k[0, :5] = [-128.0, 2.5, -2.5, near, -near]
+    k[1, :2] = [7.0, -(6.91796875 - 2.0 ** -21)]
+    ok = torch.zeros(2 * 292, dtype=torch.uint8, device="cuda")
+    device.quantize_q8k(dev(k.reshape(-1)), ok)
+    torch.cuda.synchronize()
+    kb = ok.cpu().numpy().reshape(2, 292)
+    kd = kb[:, 0:4].copy().view(np.float32).ravel()
+    kq = kb[:, 4:260].view(np.int8)
+    assert kd[0] == 1.0 and list(kq[0, :5]) == [-128, 3, -3, 1, -1]
+    assert kd[1] == -(7 / 128 - 2.0 ** -28) and list(kq[1, :2]) == [-128, 127]
+
+    # dot_q8_scalar: ((acc*dw)*dx), two blocks chained
+    w8 = np.stack([q8_0_block(0x3C01, [127, 127]), q8_0_block(0x3C01, [1])]).reshape(1, 68)
+    x8 = np.stack([q8_0_block(0x3C02, [127, 2]), q8_0_block(0x3C01, [1])]).reshape(-1)
+    # dot_q6k_scalar: d_all before the sum
+    q = np.full(256, 32, dtype=np.int64)
+    q8 = np.zeros(256, dtype=np.int64)
+    q[0], q8[0], q[1], q8[1] = 33, 127, 33, 2
+    w6 = q6k_block(0x3C01, [127] + [0] * 15, q).reshape(1, 210)
+    x6 = q8k_block(1 + 2.0 ** -10, q8).reshape(-1)
+    for dtype, w, x, cols, want in ((1, w8, x8, 64, 16432.03125), (3, w6, x6, 256, 16415 + 7 / 512)):
+        assert gpu_matvec(dtype, 0, w, x, 1, cols)[0] == want
+        for rows in (40, 1056):
+            wr = np.ascontiguousarray(np.repeat(w, rows, axis=0))
+            xs = np.ascontiguousarray(np.tile(x, 5))
+            assert np.all(gpu_matvec(dtype, 0, wr, x, rows, cols) == want)
+            assert np.all(gpu_matmul(dtype, 0, wr, xs, rows, cols, 5) == want)
+
+
 # ---- f16 scale decode --------------------------------------------------------------
 
 
