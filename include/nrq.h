@@ -142,7 +142,7 @@ int nrq_dev_block_sums(int dtype, const void *w, const void *x, int32_t *out, si
  * the musl algorithms the reference's libm crate ports; vec.rs:30-52,
  * rope.rs:49-65 call them). Diagnostic path. */
 int nrq_dev_mathf(int fn, const float *x, float *y, size_t n, void *stream);
-/* rmsnorm (crates/nr-core/src/vec.rs:4-14) of each of `rows` rows of n f32 in
+/* rmsnorm (crates/nr-tensor/src/vec.rs:4-14) of each of `rows` rows of n f32 in
  * HBM: ss += v*v in element order, scale = 1/sqrtf(ss/n + eps), out = x *
  * scale * w. The decode and prefill steps run the same kernel; n is a multiple
  * of 256, at most 8192. */

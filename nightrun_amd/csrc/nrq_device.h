@@ -497,8 +497,10 @@ __device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, f
 // chain. A pass issues about four times the instructions of the plain chain
 // over the same terms, in a fraction of its time: it pays where the wave has
 // its SIMD to itself. Whole wave, a in LDS and 16-byte aligned, n a multiple of
-// 4, the result in every lane; work is kChainWork words of LDS that no other
-// wave touches meanwhile (n < 640 needs none).
+// 4; the result is valid in lane 0 (after a fallback or a short tail it comes
+// from wave_chain_from, whose other lanes hold partial sums); work is
+// kChainWork words of LDS that no other wave touches meanwhile (n < 640 needs
+// none).
 constexpr int kChainWork = 2 * 1024 + 64;
 __device__ __forceinline__ float wave_chain_nonneg(const float* __restrict__ a, int n, float s, uint32_t* __restrict__ work) {
   constexpr int RL = 16, P = 64 * RL;

@@ -76,3 +76,43 @@ def test_oracle_is_not_reachable_from_the_product():
             if f.endswith((".py", ".hip", ".h", ".cpp")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "oracle" not in text.lower(), os.path.join(dirpath, f)
+
+
+def test_m0_is_written_only_by_the_dma_asm():
+    """The LDS DMA helpers (nrq_wstream.hip, nrq_model.hip) set m0 in inline
+    asm right before their global_load_lds instruction, without the compiler
+    knowing (the compiler-tracked builtin adds vmcnt(0) waits that stall the
+    DMA pipelines). That is sound only while no compiler-generated code keeps
+    a value in m0: this disassembles the library's gfx950 code objects and
+    checks that every instruction naming m0 is such an `s_mov_b32 m0, sN`
+    directly followed by a global_load_lds, and that no instruction which
+    reads m0 implicitly appears."""
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+
+    from nightrun_amd import _lib
+
+    objdump = "/opt/rocm/llvm/bin/llvm-objdump"
+    if not os.path.exists(objdump):
+        pytest.skip("llvm-objdump not installed")
+    with tempfile.TemporaryDirectory() as tmp:
+        lib = os.path.join(tmp, "libnrq.so")
+        shutil.copy(_lib.LIB_PATH, lib)
+        subprocess.run([objdump, "--offloading", lib], cwd=tmp, check=True, capture_output=True)
+        cos = glob.glob(os.path.join(tmp, "libnrq.so.*gfx950"))
+        assert cos, "no gfx950 code object in libnrq.so"
+        lines = []
+        for co in cos:
+            out = subprocess.run([objdump, "-d", co], check=True, capture_output=True, text=True).stdout
+            lines += [ln.split("//")[0].strip() for ln in out.splitlines() if ln.startswith(("\t", " "))]
+    ins = [ln for ln in lines if ln]
+    writes = 0
+    for i, ln in enumerate(ins):
+        assert not re.match(r"(s_sendmsg|s_movrel|v_movrel|s_set_gpr_idx|ds_gws|buffer_load\w*.*\blds\b)", ln), ln
+        if re.search(r"\bm0\b", ln):
+            assert re.match(r"s_mov_b32 m0, s\d+$", ln), ln
+            assert ins[i + 1].startswith("global_load_lds_dword"), (ln, ins[i + 1])
+            writes += 1
+    assert writes > 0

@@ -1,7 +1,7 @@
 """The wave-parallel exact sum behind the decode norms (chain_pass and
 wave_chain_nonneg in nightrun_amd/csrc/nrq_device.h), restated lane for lane
 in numpy float32 and checked bit-exact against the sequential f32 chain, the
-reference's `ss += v * v` loop (crates/nr-model/src/vec.rs:4-14).
+reference's `ss += v * v` loop (crates/nr-tensor/src/vec.rs:4-14).
 
 The restatement follows the device code: 64 lanes of 16 consecutive terms, an
 f32 prediction of each term's binade, terms rounded to the unit of their

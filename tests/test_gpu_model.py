@@ -266,7 +266,7 @@ def test_wide_norm_sums_on_crafted_rows(gpu, oracle, fmt, prefill):
     """Hidden width 2048, so the fused norms' sum of squares takes the
     wave-parallel exact path. The prompt's embedding rows are crafted for
     it: after a large first value every square is an exact tie (the pass gives
-    up past 16 special terms and falls back), squares mixing ties and exact
+    up past 48 special terms and falls back), squares mixing ties and exact
     multiples of the unit, a ramp crossing binades late, and an ordinary row.
     Logits and KV bit-identical to the oracle."""
     w = oracle.gen_model(WIDE, 6161)
@@ -409,9 +409,29 @@ def test_qwen3_recipe_matches_oracle(gpu, oracle, cfg, prefill):
     run_pair(oracle, cfg, w, 128, prompt, 10, prefill=prefill)
 
 
+LLAMA_HD96 = dict(dim=384, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=96, ffn_dim=512, vocab=1000,
+                  norm_eps=1e-5, rope_theta=500000.0)
+QWEN_HD96 = dict(LLAMA_HD96, norm_eps=1e-6, rope_theta=1000000.0, recipe=dict(rope="neox"))
+
+
+@pytest.mark.parametrize("cfg", [LLAMA_HD96, QWEN_HD96, QWEN_HD128], ids=["llama-hd96", "qwen-hd96", "qwen-hd128"])
+@pytest.mark.parametrize("prefill", [False, True], ids=["decode", "prefill"])
+def test_wide_heads_long_context(gpu, oracle, cfg, prefill):
+    """96- and 128-wide heads (768-thread attention, 64-position value chunks
+    in a three-slot ring) over 330 prompt positions, six chunks, so every ring
+    slot is reused; the Qwen3 models take the early LDS staging of the step's
+    own rows in decode. Then 8 greedy steps; logits, tokens and the KV cache
+    bit-exact against the oracle."""
+    qk = "recipe" in cfg
+    w = oracle.gen_model(cfg, 808 + cfg["head_dim"] + 2 * qk, qk_norm=qk)
+    prompt = np.random.default_rng(cfg["head_dim"]).integers(0, cfg["vocab"], 330).astype(np.uint32)
+    run_pair(oracle, cfg, w, 512, prompt, 8, prefill=prefill)
+
+
 def test_granite_recipe_kquant_matches_oracle(gpu, oracle):
     """Adjacent rope and muP scalars with Q4_K/Q6_K layers: the residual scale
-    goes through the standalone norm kernel (the fused norm takes Q8_0 only)."""
+    is applied by the fused K-quant norm + matvec launches in decode and by
+    norm_kernel in prefill."""
     w = oracle.gen_model(GRANITE, 707)
     shapes = oracle.layer_shapes(GRANITE)
     for l, lw in enumerate(w["layers"]):
