@@ -409,7 +409,7 @@ def test_qwen3_recipe_matches_oracle(gpu, oracle, cfg, prefill):
     run_pair(oracle, cfg, w, 128, prompt, 10, prefill=prefill)
 
 
-LLAMA_HD96 = dict(dim=384, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=96, ffn_dim=512, vocab=1000,
+LLAMA_HD96 = dict(dim=768, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=96, ffn_dim=512, vocab=1000,
                   norm_eps=1e-5, rope_theta=500000.0)
 QWEN_HD96 = dict(LLAMA_HD96, norm_eps=1e-6, rope_theta=1000000.0, recipe=dict(rope="neox"))
 
