@@ -210,9 +210,15 @@ __device__ inline float chain_from(const float* __restrict__ a, int n, float s) 
   int g = 0;
   if (n16 >= 3) {
     float4 R0[4], R1[4], R2[4];
+    // The running sum passes through the empty asm statements around each
+    // group's loads, so the loads stay right after the adds that free their
+    // registers: left alone, the compiler moves them next to their first use
+    // and the whole load latency is paid once per group.
     auto ld = [&](float4* R, int gg) {
+      asm volatile("" : "+v"(s) : : "memory");
 #pragma unroll
       for (int k = 0; k < 4; k++) R[k] = a4[4 * gg + k];
+      asm volatile("" : "+v"(s) : : "memory");
     };
     auto add = [&](const float4* R) {
 #pragma unroll

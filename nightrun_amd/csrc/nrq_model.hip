@@ -441,25 +441,36 @@ constexpr int kAttRing = 3 * 1024 * 16;  // bytes of the value ring: three chunk
 // base + i: its query was roped by rope_append_kernel and every key and
 // value row, its own included, is read from the cache (the chunk's rows were
 // all appended before this launch); out and out_q8 are row i of [B][...].
+// With DS > 1 (decode), DS workgroups serve one head: each runs steps 1-3
+// for the whole head and step 4 for its HD / DS dimensions (the chain and the
+// products of the other dimensions run on other CUs, whose LDS bandwidth the
+// product stage and value ring would otherwise share). Workgroup b serves
+// head 8 * (q / DS) + b % 8, dimension group q % DS (q = b / 8): the DS
+// workgroups of a head share XCD b % 8 and its L2 (needs n_heads % 8 == 0).
 // LDS: att[ctx] | prod[2][kAttProd] | q[hd] | kcur[hd] | vcur[hd] | red[32]
-template <int HD, bool PF = false, int NT = att_threads(HD)>
+template <int HD, bool PF = false, int NT = att_threads(HD), int DS = 1>
 __global__ __launch_bounds__(NT) void attention_kernel(
     const float* __restrict__ q_in, const float* __restrict__ k_in, const float* __restrict__ v_in,
     const float* __restrict__ rope_cs, const int* __restrict__ ctl, int n_heads, int n_kv_heads, int ctx, int layer,
     float scale, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, float* __restrict__ out,
     uint8_t* __restrict__ out_q8, const float* __restrict__ qn, const float* __restrict__ kn, float eps, int neox) {
   constexpr int hd = HD, half = HD / 2, g8 = HD / 8;
-  constexpr int C = (8192 / HD) & ~63 ? (8192 / HD) & ~63 : 64;  // positions per product chunk
+  static_assert(DS == 1 || (!PF && HD % (8 * DS) == 0 && HD / DS == 32), "dimension groups of 32");
+  constexpr int DW = HD / DS;   // dimensions of this workgroup's value chains
+  constexpr int g8w = DW / 8;   // their 16-byte pieces per position
+  constexpr int C = DS > 1 ? 256 : (8192 / HD) & ~63 ? (8192 / HD) & ~63 : 64;  // positions per product chunk
   constexpr int CP = C + 4;
-  static_assert(HD * CP <= kAttProd, "product chunk exceeds its LDS stage");
-  constexpr int cw = (HD + 63) / 64;  // chain waves
+  static_assert(DW * CP <= kAttProd, "product chunk exceeds its LDS stage");
+  constexpr int cw = (DW + 63) / 64;  // chain waves
   constexpr int nprod = NT - 64 * cw;
-  constexpr int npc = C * g8;  // 16-byte value pieces per chunk
+  constexpr int npc = C * g8w;  // 16-byte value pieces per chunk
   static_assert(npc <= 2 * nprod, "two pieces per producer thread");
   static_assert(npc % 64 == 0 && 3 * npc * 16 <= kAttRing, "whole-wave DMAs within the value ring");
   constexpr bool kTwoRounds = HD <= 64;  // second round of key rows held in registers
   extern __shared__ __align__(16) float sm[];
-  const int h = blockIdx.x, tid = threadIdx.x;
+  const int bq = (int)blockIdx.x >> 3;
+  const int h = DS > 1 ? 8 * (bq / DS) + ((int)blockIdx.x & 7) : (int)blockIdx.x, tid = threadIdx.x;
+  const int dim0 = DS > 1 ? (bq % DS) * DW : 0;  // this workgroup's first value dimension
   const int tok = PF ? (int)blockIdx.y : 0;
   const int pos = ctl[CTL_POS] + tok, n = pos + 1;
   const int self = PF ? -1 : pos;  // the position served from LDS rather than the cache
@@ -469,7 +480,7 @@ __global__ __launch_bounds__(NT) void attention_kernel(
     if (out_q8) out_q8 += (size_t)tok * (n_heads * hd / 32) * kQ8_0Bytes;
   }
   const int gqa = n_heads / n_kv_heads, g = h / gqa;
-  const bool writer = (h % gqa) == 0;
+  const bool writer = (h % gqa) == 0 && dim0 == 0;
   float* att = sm;
   float* prod = sm + ((ctx + 127) & ~127);
   float* qs = prod + 2 * kAttProd;
@@ -512,7 +523,7 @@ __global__ __launch_bounds__(NT) void attention_kernel(
       const int wbase = 64 * pw + nprod * j;  // the wave's first piece
       if (wbase >= npc) break;
       const int idx = wbase + (tid & 63);
-      const int tl = idx % C, i0 = 8 * (idx / C);
+      const int tl = idx % C, i0 = dim0 + 8 * (idx / C);
       const int t = min(c * C + tl, n - 1);
       const uint32_t dst = __builtin_amdgcn_readfirstlane(
           (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint4*)(vring + (size_t)slot * npc + wbase));
@@ -696,7 +707,7 @@ __global__ __launch_bounds__(NT) void attention_kernel(
       float vv[8];
       if (t == self) {
 #pragma unroll
-        for (int q = 0; q < 8; q++) vv[q] = vcur[i0 + q];
+        for (int q = 0; q < 8; q++) vv[q] = vcur[dim0 + i0 + q];
       } else {
         const uint4 rv = r[idx];
         const uint32_t vw[4] = {rv.x, rv.y, rv.z, rv.w};
@@ -727,7 +738,7 @@ __global__ __launch_bounds__(NT) void attention_kernel(
         vload(cc + 3);  // into the slot of chunk cc, consumed before the last barrier
         vwait();        // chunk cc + 2 (chunk cc + 3 outstanding), read after the barrier
       }
-    } else if (tid < hd) {
+    } else if (tid < DW) {
       o = chain_from(prod + (cc & 1) * kAttProd + tid * CP, min(C, n - cc * C), o);
     }
     __syncthreads();
@@ -736,9 +747,9 @@ __global__ __launch_bounds__(NT) void attention_kernel(
   // requests past the last chunk land in unread slots; none may still be
   // writing to LDS when the workgroup ends
   if (producer) __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
-  if (tid < hd) {
-    out[(size_t)h * hd + tid] = o;
-    if (out_q8) quant_q8_0_lane(o, tid & 31, out_q8 + (size_t)((h * hd + tid) >> 5) * kQ8_0Bytes);
+  if (tid < DW) {
+    out[(size_t)h * hd + dim0 + tid] = o;
+    if (out_q8) quant_q8_0_lane(o, tid & 31, out_q8 + (size_t)((h * hd + dim0 + tid) >> 5) * kQ8_0Bytes);
   }
 }
 
@@ -1570,6 +1581,8 @@ static void step_mark(nrq_model* m, int stage) {
 }
 
 // One decode step, enqueued on m->stream (infer.rs:510-595 + argmax).
+int att_dim_split(const nrq_model_config& c);
+
 int enqueue_step(nrq_model* m) {
   const auto& c = m->cfg;
   const int d = c.dim, kvd = m->kv_dim, att = m->att_dim, ffn = c.ffn_dim;
@@ -1600,11 +1613,13 @@ int enqueue_step(nrq_model* m) {
     }
     {
       const bool q8 = Ly.m[3].dt == NRQ_Q8_0;
+      const int ds = att_dim_split(c);
       auto* kern = c.head_dim == 32   ? nrq::attention_kernel<32>
-                   : c.head_dim == 64 ? nrq::attention_kernel<64>
+                   : c.head_dim == 64 ? (ds == 2 ? nrq::attention_kernel<64, false, nrq::kAttNT, 2>
+                                                 : nrq::attention_kernel<64>)
                    : c.head_dim == 96 ? nrq::attention_kernel<96>
                                       : nrq::attention_kernel<128>;
-      hipLaunchKernelGGL(kern, dim3(c.n_heads), dim3(nrq::att_threads(c.head_dim)), m->att_lds, m->stream, m->q, m->k, m->v,
+      hipLaunchKernelGGL(kern, dim3(c.n_heads * ds), dim3(nrq::att_threads(c.head_dim)), m->att_lds, m->stream, m->q, m->k, m->v,
                          m->rope_cs, m->ctl, c.n_heads, c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->attn,
                          q8 ? m->xq : nullptr, Ly.q_norm, Ly.k_norm, c.norm_eps, m->rope_neox);
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: attention launch failed");
@@ -1688,6 +1703,15 @@ AttGroupFn att_group_for(int gh, size_t* lds, int ctx) {
     case 4: *lds = nrq::AttGroup<HD, 4>::lds_bytes(ctx); return nrq::attention_group_kernel<HD, 4>;
     default: *lds = 0; return nullptr;
   }
+}
+
+// Workgroups per head of the decode attention: two (32 value dimensions each,
+// on one XCD) for 64-wide heads when the head count allows the XCD mapping;
+// NRQ_ATT_SPLIT=1 forces one.
+int att_dim_split(const nrq_model_config& c) {
+  const char* env = getenv("NRQ_ATT_SPLIT");
+  if (env && env[0] == '1') return 1;
+  return c.head_dim == 64 && c.n_heads % 8 == 0 ? 2 : 1;
 }
 
 // The grouped prefill attention for this model's shape, or null (then one

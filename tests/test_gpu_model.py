@@ -304,6 +304,22 @@ def test_tiny_model_long_context(gpu, oracle, ctx):
     run_pair(oracle, TINY, w, ctx, prompt, 12, prefill=True)
 
 
+TINY8 = dict(TINY, dim=512, n_heads=8, n_kv_heads=2)
+
+
+@pytest.mark.parametrize("split", ["2", "1"])
+def test_decode_attention_dimension_split(gpu, oracle, monkeypatch, split):
+    """Eight 64-wide heads: the decode attention runs two workgroups per head
+    (32 value dimensions each, 256-position value chunks) by default, one with
+    NRQ_ATT_SPLIT=1. 1100 prompt positions, so the split kernel's value loop
+    runs five chunks and reuses every ring slot; then 12 greedy steps, each
+    bit-exact against the oracle."""
+    monkeypatch.setenv("NRQ_ATT_SPLIT", split)
+    w = oracle.gen_model(TINY8, 5150)
+    prompt = np.random.default_rng(5150).integers(0, TINY8["vocab"], 1100).astype(np.uint32)
+    run_pair(oracle, TINY8, w, 2048, prompt, 12, prefill=True)
+
+
 @pytest.mark.parametrize("n", [1, 5, 63, 64, 65, 70, 130])
 def test_tiny_model_prefill(gpu, oracle, n):
     """Device prefill (64-token batched chunks) == the oracle's prefill: the
