@@ -390,6 +390,12 @@ __device__ __forceinline__ void ws_q8k_half(const float o[8], int r, uint32_t* x
 constexpr int kFusedNormMax = 4096;
 constexpr int kFusedNormPT = kFusedNormMax / 256;
 
+// Fused-norm LDS, n floats per array: x (then its squares, in place) | norm
+// weight | add | pad | scale. The add array and the pad are the ordered sum's
+// workspace (kChainWork words) once the squares exist.
+__host__ __device__ inline int ws_norm_pad(int n) { return n < kChainWork ? (kChainWork - n + 3) & ~3 : 0; }
+__host__ __device__ inline size_t ws_norm_floats(int n) { return 3 * (size_t)n + ws_norm_pad(n) + 4; }
+
 __device__ __forceinline__ void ws_dma16_g(const void* g, uint32_t m0) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(g) : "memory");
 }
@@ -447,17 +453,17 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
   };
 
   // The activation (or the norm's inputs) first, so an in-order vmcnt wait below covers it.
-  float* nxs = (float*)(smem + G.total);  // fused norm: x | add | weight | squares, n floats each
+  float* nxs = (float*)(smem + G.total);  // fused norm: x (then squares) | weight | add | pad | scale
   const int n = bpr * (FMT == kQ8_0 ? 32 : 256);
   if constexpr (QNT) {  // the f32 activation, quantized after the barrier below
     const uint32_t dst = ws_lds_addr(nxs);
     for (int k = wave; k < n / 256; k += NW) ws_dma16_g(A.nx + 256 * k + 4 * lane, dst + (uint32_t)k * 1024u);
   } else if constexpr (NORM) {
     const int nk = n / 256;  // 1 KiB DMAs per array
-    const float* src[3] = {A.nx, A.nadd, A.nw};
+    const float* src[3] = {A.nx, A.nw, A.nadd};
 #pragma unroll
     for (int a = 0; a < 3; a++) {
-      if (a == 1 && !A.nadd) continue;
+      if (a == 2 && !A.nadd) continue;
       const uint32_t dst = ws_lds_addr(nxs + (size_t)a * n);
       for (int k = wave; k < nk; k += NW) ws_dma16_g(src[a] + 256 * k + 4 * lane, dst + (uint32_t)k * 1024u);
     }
@@ -501,9 +507,10 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
   ws_lds_barrier();
   if constexpr (NORM) {
     const float* xs = nxs;
-    const float* as = nxs + n;
-    const float* wsn = nxs + 2 * (size_t)n;
-    float* sq = nxs + 3 * (size_t)n;
+    const float* wsn = nxs + n;
+    const float* as = nxs + 2 * (size_t)n;
+    // each run's squares overwrite its x, read just before by the same thread
+    float* sq = nxs;
     // Thread t owns the 8-value runs j = t + NT*k; four consecutive runs (an
     // aligned lane quad) make one Q8_0 block.
     const int nrun = n >> 3;
@@ -534,10 +541,11 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
       }
     }
     ws_lds_barrier();
-    float* scale_slot = sq + n;  // one float past the squares
+    float* scale_slot = nxs + 3 * (size_t)n + ws_norm_pad(n);
     if (wave == 0) {
-      // the x and add stages (2n floats) are dead here: the pass workspace when n >= 1024
-      const float ss = n >= kChainWork / 2 ? wave_chain_nonneg(sq, n, 0.0f, (uint32_t*)nxs) : wave_chain_from(sq, n, 0.0f);
+      // the add array and the pad (at least kChainWork words) are dead here: the pass workspace
+      const float ss = n >= kChainWork / 2 ? wave_chain_nonneg(sq, n, 0.0f, (uint32_t*)(nxs + 2 * (size_t)n))
+                                           : wave_chain_from(sq, n, 0.0f);
       if (lane == 0) scale_slot[0] = 1.0f / sqrtf(ss / (float)n + A.eps);
     }
     ws_lds_barrier();
@@ -685,7 +693,7 @@ static int launch_ws_t(WsArgs A, int bpr, int rpw, void* stream) {
   const int nstages = (int)(tiles_per_wave < NS ? tiles_per_wave : NS);
   const WSGeom<FMT> G(bpr, rpw, nstages, NW, URM);
   // fused norm: x, add, weight, squares (n floats each) and the scale
-  const size_t lds = G.total + (NORM ? (size_t)4 * bpr * (FMT == kQ8_0 ? 32 : 256) * 4 + 16 : 0) +
+  const size_t lds = G.total + (NORM ? ws_norm_floats(bpr * (FMT == kQ8_0 ? 32 : 256)) * 4 : 0) +
                      (QNT ? (size_t)bpr * 256 * 4 : 0);
   if (lds > 160 * 1024) return NRQ_LAUNCH_TOO_WIDE;
   if (grid == 0) return 0;
