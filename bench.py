@@ -409,7 +409,6 @@ def measure_decode(fill=1024, n=128):
     cfg = LLAMA_1B
     w = synth_model(cfg, 0x5EED0005)
     blob = nrm_blob(cfg, w)
-    del w
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     f = nrm.NrmFile(blob)
@@ -479,7 +478,10 @@ def measure_decode(fill=1024, n=128):
             "prefill": {"tokens": int(fill), "chunks_of": 64, "seconds": round(pf_dt, 4),
                         "tok_s": round(fill / pf_dt, 1),
                         "what": "nrq_model_prefill of the random prompt from position 0 (KV 0..1023), host sync "
-                                "per chunk, logits of the last token copied back"}}
+                                "per chunk, logits of the last token copied back"},
+            # for the host-side comparison, removed before the line is printed
+            "_weights": w, "_prompt": prompt,
+            "_tokens": [int(np.argmax(lg))] + [int(t) for t in out]}
 
 
 def step_stages(m, token, steps=8):
@@ -620,30 +622,66 @@ def cpu_baseline_matvec(name, seconds):
             "runs": runs, **cpu_info()}
 
 
-def cpu_baseline_decode(seconds, fill=1024):
-    """The oracle's restatement of InferCtx::forward (scalar-order kernels,
-    parallel.rs-style pool) on the same architecture, greedy, at the GPU leg's
-    KV positions: the model is moved to position `fill` without computing the
-    cache rows before it (their cost does not depend on their values), then
-    decodes for about `seconds` (at most 128 steps)."""
+def cpu_baseline_decode(seconds, fill=1024, device=None):
+    """The reference's decode on this host's cores, restated by the oracle:
+    the x86 path nrhost runs (AVX2 matvec dots, F16C attention dot and axpy,
+    the parallel.rs pool on every core: tools/nrhost/src/main.rs:41-51,
+    108-153) and the scalar-order path, greedy at the GPU leg's KV positions.
+    For the rates the model is moved to position `fill` without computing the
+    cache rows before it (their cost does not depend on their values).
+    With the GPU leg's weights, prompt and tokens (`device`), the x86 path also
+    prefills the same prompt and decodes greedily, and its tokens are compared
+    with the device's, which follow the scalar order."""
     import oracle as O
 
     threads = host_cores()
     cfg = dict(O.LLAMA_1B)
-    w = O.gen_model(cfg, 0x5EED0005)
-    m = O.Model(cfg, w, ctx=fill + 136, threads=threads)
-    m.seek(fill)
-    tok = O.argmax(m.forward(1))  # warm-up step at position fill
-    n = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds and n < 128:
-        tok = O.argmax(m.forward(tok))
-        n += 1
-    dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} greedy decode steps at KV positions {fill + 1}..{fill + n} of the Llama-3.2-1B-shape Q8_0 "
-                      f"model (scalar-order kernels, {threads} threads) in {dt:.1f} s; cache rows before {fill} "
-                      f"not computed (same cost per step)"}
+    w = device["_weights"] if device else O.gen_model(cfg, 0x5EED0005)
+
+    def rate(order, secs):
+        m = O.Model(cfg, w, ctx=fill + 136, threads=threads, order=order)
+        m.seek(fill)
+        tok = O.argmax(m.forward(1))  # warm-up step at position fill
+        n = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < secs and n < 128:
+            tok = O.argmax(m.forward(tok))
+            n += 1
+        return n, time.perf_counter() - t0
+
+    n1, dt1 = rate(O.ORDER_AVX2, seconds)
+    n0, dt0 = rate(O.ORDER_SCALAR, seconds / 2)
+    out = {"value": round(n1 / dt1, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+           "sample": f"{n1} greedy decode steps at KV positions {fill + 1}..{fill + n1} of the Llama-3.2-1B-shape Q8_0 "
+                     f"model in {dt1:.1f} s, x86 path (AVX2 dots, F16C attention) on {threads} threads; cache rows "
+                     f"before {fill} not computed (same cost per step)",
+           "scalar_order": {"value": round(n0 / dt0, 3), "unit": "tok/s", "cores": threads,
+                            "sample": f"{n0} steps the same way with the scalar-order kernels"}}
+    if device:
+        dev = device["_tokens"]
+        m = O.Model(cfg, w, ctx=fill + 136, threads=threads, order=O.ORDER_AVX2)
+        t0 = time.perf_counter()
+        lg = m.prefill(device["_prompt"])
+        pf = time.perf_counter() - t0
+        toks, gaps = [], []
+        t0 = time.perf_counter()
+        while len(toks) < len(dev) and (len(toks) < 8 or time.perf_counter() - t0 < seconds):
+            top2 = np.sort(lg)[-2:]
+            gaps.append(float(top2[1] - top2[0]))
+            toks.append(O.argmax(lg))
+            # after a divergence the x86 run keeps its own tokens
+            lg = m.forward(toks[-1])
+        same = [a == b for a, b in zip(toks, dev)]
+        first_diff = same.index(False) if not all(same) else None
+        out["x86_vs_device_tokens"] = {
+            "compared": len(toks), "identical": int(sum(same)), "first_difference": first_diff,
+            "top2_gap_min": round(min(gaps), 6), "top2_gap_median": round(float(np.median(gaps)), 6),
+            "top2_gap_at_first_difference": None if first_diff is None else round(gaps[first_diff], 6),
+            "prefill_tok_s": round(fill / pf, 3),
+            "what": f"the same {fill}-token prompt through the x86 path's prefill (4-token AVX2 tiles), then greedy "
+                    "decode; compared position by position with the device's scalar-order tokens (the first is "
+                    "the prompt's argmax); the top-2 logit gap of each x86 step"}
+    return out
 
 
 def cpu_baseline_crc(seconds):
@@ -774,9 +812,12 @@ def main():
         cpu = cpu_baseline_matvec(args.config, args.cpu_seconds)
         progress("cpu matvec")
         if decode is not None:
-            cpu["decode"] = cpu_baseline_decode(args.cpu_seconds)
+            cpu["decode"] = cpu_baseline_decode(args.cpu_seconds, device=decode)
             cpu["verify_crc"] = cpu_baseline_crc(min(args.cpu_seconds, 5.0))
             progress("cpu decode")
+    if decode is not None:
+        for k in ("_weights", "_prompt", "_tokens"):
+            decode.pop(k, None)
     dtype, rows, cols, _, desc = CONFIGS[args.config]
     out = {
         "metric": METRIC,

@@ -288,6 +288,9 @@ def _model_lib():
         L.nro_model_prefill_chunk.argtypes, L.nro_model_prefill_chunk.restype = [vp, C.POINTER(C.c_uint32), C.c_int], f32p
         L.nro_model_pos.argtypes, L.nro_model_pos.restype = [vp], C.c_int
         L.nro_model_reset.argtypes = [vp]
+        L.nro_model_set_order.argtypes = [vp, C.c_int]
+        L.nro_dot_f16.argtypes, L.nro_dot_f16.restype = [C.c_int, vp, vp, sz], C.c_float
+        L.nro_axpy_f16.argtypes = [C.c_int, vp, C.c_float, vp, sz]
         L.nro_model_seek.argtypes = [vp, C.c_int]
         L.nro_model_kcache.argtypes, L.nro_model_kcache.restype = [vp], C.POINTER(C.c_uint16)
         L.nro_model_vcache.argtypes, L.nro_model_vcache.restype = [vp], C.POINTER(C.c_uint16)
@@ -448,15 +451,33 @@ def gen_model(cfg: dict, seed: int, dtype: int = Q8_0, qk_norm: bool = False) ->
     return w
 
 
-class Model:
-    """InferCtx restated on the CPU (scalar f32 order throughout)."""
+def dot_f16(order: int, k_bits: np.ndarray, q: np.ndarray) -> float:
+    """kernels::dot_f16 (kernels.rs:146-160): scalar, or dot_f16_f16c (:174-201) with ORDER_AVX2."""
+    k = np.ascontiguousarray(k_bits, dtype=np.uint16)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    return _model_lib().nro_dot_f16(order, _p(k), _p(q), min(k.size, q.size))
 
-    def __init__(self, cfg: dict, weights: dict, ctx: int, threads: int = 1):
+
+def axpy_f16(order: int, out: np.ndarray, a: float, v_bits: np.ndarray) -> np.ndarray:
+    """kernels::axpy_f16 (kernels.rs:163-173): scalar, or axpy_f16_f16c (:203-220) with ORDER_AVX2."""
+    o = np.ascontiguousarray(out, dtype=np.float32).copy()
+    v = np.ascontiguousarray(v_bits, dtype=np.uint16)
+    _model_lib().nro_axpy_f16(order, _p(o), a, _p(v), min(o.size, v.size))
+    return o
+
+
+class Model:
+    """InferCtx restated on the CPU: scalar f32 order throughout by default;
+    order=ORDER_AVX2 runs the x86 host's kernels instead (AVX2 matvec dots
+    and 4-token prefill tiles, F16C attention dot and axpy)."""
+
+    def __init__(self, cfg: dict, weights: dict, ctx: int, threads: int = 1, order: int = ORDER_SCALAR):
         L = _model_lib()
         dims = (C.c_int * 8)(cfg["dim"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"],
                              cfg["ffn_dim"], cfg["vocab"], ctx)
         self.cfg, self.w, self.ctx = cfg, weights, ctx
         self.h = L.nro_model_new(dims, cfg["norm_eps"], cfg["rope_theta"], threads)
+        L.nro_model_set_order(self.h, order)
         out = weights.get("output", weights["embed"])  # infer.rs:415-419: tied unless a head is given
         out_dt = weights.get("output_dtype", weights["embed_dtype"])
         L.nro_model_set_globals(self.h, _p(weights["embed"]), weights["embed_dtype"], _p(out), out_dt,

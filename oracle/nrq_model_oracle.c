@@ -15,6 +15,7 @@
  * the crate present, their bits are "parity unpinned" against the reference;
  * the tests pin them against glibc within 1 ulp instead.
  */
+#include <immintrin.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -282,6 +283,46 @@ static void axpy_f16_(float *out, float a, const uint16_t *v, size_t n) {
     for (size_t i = 0; i < n; i++) out[i] += a * nro_f16_to_f32(v[i]);
 }
 
+/* kernels.rs:174-201, dot_f16_f16c: eight lane accumulators, one
+ * fmadd(f32(k), q, acc) per 8-element chunk, then the 128-bit halves added,
+ * movehl, add_ss with lane 1: ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)); the tail
+ * past the last whole chunk as the scalar kernel. cvtph_ps is exact, as
+ * f16_to_f32 is. */
+__attribute__((target("avx2,fma,f16c"))) static float dot_f16_f16c_(const uint16_t *k, const float *q, size_t n) {
+    __m256 acc = _mm256_setzero_ps();
+    size_t chunks = n / 8;
+    for (size_t i = 0; i < chunks; i++) {
+        __m256 kf = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(k + 8 * i)));
+        acc = _mm256_fmadd_ps(kf, _mm256_loadu_ps(q + 8 * i), acc);
+    }
+    __m128 s4 = _mm_add_ps(_mm256_extractf128_ps(acc, 1), _mm256_castps256_ps128(acc));
+    s4 = _mm_add_ps(s4, _mm_movehl_ps(s4, s4));
+    s4 = _mm_add_ss(s4, _mm_shuffle_ps(s4, s4, 1));
+    float sum = _mm_cvtss_f32(s4);
+    for (size_t i = chunks * 8; i < n; i++) sum += nro_f16_to_f32(k[i]) * q[i];
+    return sum;
+}
+
+/* kernels.rs:203-220, axpy_f16_f16c: out = fmadd(a, f32(v), out) per element of
+ * whole 8-element chunks (one rounding), the tail as the scalar kernel. */
+__attribute__((target("avx2,fma,f16c"))) static void axpy_f16_f16c_(float *out, float a, const uint16_t *v, size_t n) {
+    __m256 av = _mm256_set1_ps(a);
+    size_t chunks = n / 8;
+    for (size_t i = 0; i < chunks; i++) {
+        __m256 vf = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(v + 8 * i)));
+        _mm256_storeu_ps(out + 8 * i, _mm256_fmadd_ps(av, vf, _mm256_loadu_ps(out + 8 * i)));
+    }
+    for (size_t i = chunks * 8; i < n; i++) out[i] += a * nro_f16_to_f32(v[i]);
+}
+
+float nro_dot_f16(int order, const uint16_t *k, const float *q, size_t n) {
+    return order == NRO_ORDER_AVX2 ? dot_f16_f16c_(k, q, n) : dot_f16_(k, q, n);
+}
+void nro_axpy_f16(int order, float *out, float a, const uint16_t *v, size_t n) {
+    if (order == NRO_ORDER_AVX2) axpy_f16_f16c_(out, a, v, n);
+    else axpy_f16_(out, a, v, n);
+}
+
 /* ---- InferCtx (infer.rs) ------------------------------------------------------- */
 
 #define NRO_MAX_LAYERS 64
@@ -289,6 +330,9 @@ static void axpy_f16_(float *out, float a, const uint16_t *v, size_t n) {
 
 struct nro_model {
     int dim, n_layers, n_heads, n_kv_heads, head_dim, kv_dim, ffn_dim, vocab, ctx, threads;
+    /* kernel order: scalar (the default, what the device reproduces) or the
+     * x86 host's (AVX2 dots, F16C attention: cpu::fast_path / fast_f16) */
+    int order;
     float eps;
     /* the recipe (infer.rs:447-461): rope style, muP scalars */
     int neox;
@@ -411,6 +455,7 @@ void nro_model_set_qk_norm(nro_model *m, int l, const float *q_norm, const float
 
 int nro_model_pos(const nro_model *m) { return m->pos; }
 void nro_model_reset(nro_model *m) { m->pos = 0; }
+void nro_model_set_order(nro_model *m, int order) { m->order = order; }
 /* Timing aid for the CPU baseline: moves to position pos (< ctx) without
  * computing the cache rows before it (they keep their contents). */
 void nro_model_seek(nro_model *m, int pos) {
@@ -440,7 +485,7 @@ static void dequant_row_(const uint8_t *w, int dt, size_t r, size_t cols, float 
 static void acts_matvec_(nro_model *m, float *y, const uint8_t *w, int dt, const float *x, size_t rows, size_t cols) {
     if (dt == NRO_Q8_0) nro_quantize_q8_0(x, cols, m->xq);
     else nro_quantize_q8k(x, cols, m->xq);
-    nro_matvec(dt, NRO_ORDER_SCALAR, y, w, m->xq, rows, cols, m->threads);
+    nro_matvec(dt, m->order, y, w, m->xq, rows, cols, m->threads);
 }
 
 /* Acts::matmul (infer.rs:137-174): per-row quantize, batched matmul */
@@ -451,7 +496,7 @@ static void acts_matmul_(nro_model *m, float *y, const uint8_t *w, int dt, const
         if (dt == NRO_Q8_0) nro_quantize_q8_0(xs + b * cols, cols, m->xq + b * xb);
         else nro_quantize_q8k(xs + b * cols, cols, m->xq + b * xb);
     }
-    nro_matmul(dt, NRO_ORDER_SCALAR, y, w, m->xq, rows, cols, batch, m->threads);
+    nro_matmul(dt, m->order, y, w, m->xq, rows, cols, batch, m->threads);
 }
 
 /* causal attention of one token at `pos` over layer l's cache (infer.rs:553-572) */
@@ -464,14 +509,14 @@ static void attend_(nro_model *m, int l, size_t pos, const float *q, float *out)
         float *att = m->att + h * (size_t)m->ctx;
         for (size_t t = 0; t <= pos; t++) {
             size_t krow = ((size_t)l * m->ctx + t) * m->kv_dim + kvh;
-            att[t] = dot_f16_(m->kc + krow, qh, hd) * scale;
+            att[t] = nro_dot_f16(m->order, m->kc + krow, qh, hd) * scale;
         }
         nro_softmax(att, pos + 1);
         float *o = out + h * hd;
         for (size_t i = 0; i < hd; i++) o[i] = 0.0f;
         for (size_t t = 0; t <= pos; t++) {
             size_t vrow = ((size_t)l * m->ctx + t) * m->kv_dim + kvh;
-            axpy_f16_(o, att[t], m->vc + vrow, hd);
+            nro_axpy_f16(m->order, o, att[t], m->vc + vrow, hd);
         }
     }
 }

@@ -138,6 +138,12 @@ void nro_rope_apply(float *x, size_t n, size_t head_dim, const float *freqs, siz
  * weights w[7] = {q, k, v, o, gate, up, down} with their dtype ids. */
 typedef struct nro_model nro_model;
 nro_model *nro_model_new(const int dims[8], float eps, float theta, int threads);
+/* the kernels' f32 order: NRO_ORDER_SCALAR (default) or NRO_ORDER_AVX2, the
+ * x86 host's AVX2 matvec dots and F16C attention (kernels.rs:174-220) */
+void nro_model_set_order(nro_model *m, int order);
+/* dot_f16 / axpy_f16 (kernels.rs:146-173) in the given order */
+float nro_dot_f16(int order, const uint16_t *k, const float *q, size_t n);
+void nro_axpy_f16(int order, float *out, float a, const uint16_t *v, size_t n);
 void nro_model_free(nro_model *m);
 void nro_model_set_recipe(nro_model *m, int neox, float embed_scale, float attn_scale, float residual_scale,
                           float logit_scale);

@@ -18,6 +18,11 @@ show that each gives another value. Reference steps:
   quantize_q8k   kquant.rs:145-187  `iscale = -128/max`, `nearest_int(iscale*v)`
                                     ((v +- 0.5) as i32, ties away from zero),
                                     `.min(127)`, `d = 1/iscale`
+  dot_f16_f16c   kernels.rs:174-201 lane i takes elements 8c + i, one fmadd per
+                                    chunk, hsum ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7)),
+                                    tail added after in scalar
+  axpy_f16_f16c  kernels.rs:203-220 one fmadd per element of whole chunks, tail
+                                    `out += a * v` (two roundings)
 """
 from fractions import Fraction as Fr
 
@@ -290,3 +295,95 @@ def test_q8k_scale_and_quants_come_from_iscale(oracle):
     d, qs, _ = O.q8k_fields(blk)
     assert float(d[0]) == d_ref and float(d[0]) != -7 / 128
     assert qs[0, 0] == -128 and qs[0, 1] == 127
+
+
+# ---- dot_f16_f16c / axpy_f16_f16c (the x86 host's attention kernels) ---------------
+
+
+def f16_bits(vals):
+    import oracle as O
+
+    out = np.array([O.f32_to_f16(float(v)) for v in vals], dtype=np.uint16)
+    assert all(O.f16_to_f32(int(b)) == float(v) for b, v in zip(out, vals)), "values must be exact f16"
+    return out
+
+
+def test_dot_f16_f16c_lanes_and_hsum_tree(oracle):
+    """kernels.rs:174-201: lane i of the accumulator takes elements 8c + i; the
+    halves are added (lane i + lane i+4), then movehl and add_ss:
+    ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)). Elements: k0*q0 = 2^15 * 2^10 = 2^25
+    (lane 0), k1*q1 = 1 (lane 1), k4*q4 = -2^25 (lane 4). The tree cancels
+    a0 + a4 first and returns 1. The scalar kernel (element order) reaches
+    2^25 + 1, which rounds to 2^25 (spacing 4), and returns 0; a sequential
+    lane sum does the same."""
+    O = oracle
+    k = f16_bits([2.0 ** 15, 1, 0, 0, -(2.0 ** 15), 0, 0, 0])
+    q = np.array([1024, 1, 0, 0, 1024, 0, 0, 0], np.float32)
+    assert O.dot_f16(O.ORDER_AVX2, k, q) == 1.0
+    assert O.dot_f16(O.ORDER_SCALAR, k, q) == 0.0
+    lanes = [2.0 ** 25, 1, 0, 0, -(2.0 ** 25), 0, 0, 0]
+    seq = F32(0)
+    for v in lanes:
+        seq = F32(seq + F32(v))
+    assert float(seq) == 0.0
+
+
+def test_dot_f16_f16c_fuses_each_chunk_and_adds_the_tail_after(oracle):
+    """One fmadd per 8-element chunk and lane: lane 0 holds k0*q0 = -1 after
+    chunk 0, then fma(k8, q8, -1) with k8 = 1 + 2^-10 (f16 0x3C01) and
+    q8 = 1 + 2^-14: the exact product is 1 + 2^-10 + 2^-14 + 2^-24, and one
+    rounding of the sum leaves 2^-10 + 2^-14 + 2^-24 (15 significant bits,
+    exact). Multiply-then-add first rounds the product to 1 + 2^-10 + 2^-14
+    (2^-24 is half a spacing, tie to even) and returns 2^-10 + 2^-14: the
+    scalar kernel's value. With n = 17 the tail element 16 (k = 2^-10,
+    q = -1) is added after the hsum, in scalar: 2^-14 + 2^-24."""
+    O = oracle
+    k = np.zeros(16, np.uint16)
+    q = np.zeros(16, np.float32)
+    k[0], q[0] = f16_bits([-1.0])[0], 1.0
+    k[8], q[8] = 0x3C01, 1 + 2.0 ** -14
+    fused = 2.0 ** -10 + 2.0 ** -14 + 2.0 ** -24
+    assert O.dot_f16(O.ORDER_AVX2, k, q) == fused
+    assert O.dot_f16(O.ORDER_SCALAR, k, q) == 2.0 ** -10 + 2.0 ** -14
+    k17 = np.concatenate([k, f16_bits([2.0 ** -10])])
+    q17 = np.concatenate([q, np.array([-1.0], np.float32)])
+    assert O.dot_f16(O.ORDER_AVX2, k17, q17) == 2.0 ** -14 + 2.0 ** -24
+
+
+def test_axpy_f16_f16c_fuses_whole_chunks_only(oracle):
+    """kernels.rs:203-220: out = fmadd(a, f32(v), out) for each element of the
+    whole 8-element chunks, the tail out += a * f32(v) in scalar. With
+    a = 1 + 2^-14, v = 1 + 2^-10 (0x3C01) and out = -1: fused
+    2^-10 + 2^-14 + 2^-24, unfused 2^-10 + 2^-14 (see above). Nine elements:
+    the first eight are fused, the ninth (the tail) is not."""
+    O = oracle
+    a = 1 + 2.0 ** -14
+    v = np.full(9, 0x3C01, np.uint16)
+    out = np.full(9, -1.0, np.float32)
+    got = O.axpy_f16(O.ORDER_AVX2, out, a, v)
+    fused, unfused = 2.0 ** -10 + 2.0 ** -14 + 2.0 ** -24, 2.0 ** -10 + 2.0 ** -14
+    assert list(got[:8]) == [fused] * 8 and got[8] == unfused
+    assert np.all(O.axpy_f16(O.ORDER_SCALAR, out, a, v) == unfused)
+
+
+def test_f16c_kernels_within_the_reference_tolerance(oracle):
+    """On random rows both orders agree with the float64 closed form well
+    inside f32 accuracy (the reference's attention tests are tolerance-only,
+    tests/kernels.rs:130-226)."""
+    O = oracle
+    rng = np.random.default_rng(9)
+    for n in (8, 64, 67, 128):
+        kf = rng.normal(0, 1, n).astype(np.float32)
+        k = np.array([O.f32_to_f16(float(x)) for x in kf], np.uint16)
+        kd = O.f16_to_f32_array(k).astype(np.float64)
+        q = rng.normal(0, 1, n).astype(np.float32)
+        want = float(np.dot(kd, q.astype(np.float64)))
+        bound = 4 * n * 2.0 ** -24 * float(np.dot(np.abs(kd), np.abs(q.astype(np.float64))))
+        for order in (O.ORDER_SCALAR, O.ORDER_AVX2):
+            assert abs(O.dot_f16(order, k, q) - want) <= bound
+        out = rng.normal(0, 1, n).astype(np.float32)
+        a = float(rng.normal())
+        want_o = out.astype(np.float64) + a * kd
+        for order in (O.ORDER_SCALAR, O.ORDER_AVX2):
+            got = O.axpy_f16(order, out, np.float32(a), k).astype(np.float64)
+            assert np.all(np.abs(got - want_o) <= 2.0 ** -22 * (np.abs(out) + np.abs(a * kd)) + 1e-30)
