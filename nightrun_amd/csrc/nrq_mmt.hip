@@ -204,8 +204,9 @@ __device__ __forceinline__ void md_load<kQ8_0>(MdLoad<kQ8_0>& L, const uint8_t* 
 // Q6_K loads by half: half 0 = groups 0-7 and their weights, plus d and the
 // scales (read at the block's start); half 1 = groups 8-15.
 __device__ __forceinline__ void md_load_q6k_half(MdLoad<kQ6K>& L, const uint8_t* __restrict__ xb,
-                                                 const uint8_t* __restrict__ wb, int kg, int hh, const uint32_t* xo) {
-  if (hh == 0) md_load_windows(L.x, xb, xo);
+                                                 const uint8_t* __restrict__ wb, int kg, int hh, const uint32_t* xo,
+                                                 bool windows = true) {
+  if (hh == 0 && windows) md_load_windows(L.x, xb, xo);
   const uint8_t* w4 = wb - ((uintptr_t)wb & 3u);  // the block is 2-byte aligned
 #pragma unroll
   for (int u = 0; u < 2; u++) {
@@ -230,10 +231,11 @@ __device__ __forceinline__ void md_load<kQ6K>(MdLoad<kQ6K>& L, const uint8_t* __
 // Q4_K block: contributions c[e] of this lane's 16 outputs (row l % 32,
 // tile tokens 8(e/4) + 4kg + e%4). `ta` is this lane's operand token.
 // prefetch() runs once L is no longer read (it loads the next block into L).
-template <typename PF>
+template <typename PF, typename PX>
 __device__ __forceinline__ void md_q4k(MdLoad<kQ4K>& L, uint8_t* stg, uint32_t* scal, int ta, int kg, float c[16],
-                                       PF prefetch) {
+                                       PF prefetch, PX prefetch_x) {
   md_stage(L.x, stg, ta + 32 * kg);
+  prefetch_x();  // the windows are in the stage: the next block's may load into L.x now
   const uint8_t* at = stg + ta * kMdTokB;  // operand token ta in the stage
   if (kg == 0) scal[128 + ta] = *(const uint32_t*)(at + 288);  // token ta's d
   const u32x4 h = L.h;
@@ -355,10 +357,11 @@ __device__ __forceinline__ void md_q8(MdLoad<kQ8_0>& L, uint32_t* scal, int ta, 
 
 // Q6_K block, `sh` = its start's byte offset (0 or 2) past the aligned windows.
 // prefetch(half) runs once that half of L is no longer read.
-template <typename PF>
+template <typename PF, typename PX>
 __device__ __forceinline__ void md_q6k(MdLoad<kQ6K>& L, uint32_t sh, uint8_t* stg, uint32_t* scal, int ta, int kg,
-                                       float c[16], PF prefetch) {
+                                       float c[16], PF prefetch, PX prefetch_x) {
   md_stage(L.x, stg, ta + 32 * kg);
+  prefetch_x();  // the windows are in the stage: the next block's may load into L.x now
   const uint8_t* at = stg + ta * kMdTokB;  // operand token ta in the stage
   if (kg == 0) scal[128 + ta] = *(const uint32_t*)(at + 288);
   uint32_t S[4];  // scales[16], realigned
@@ -445,7 +448,7 @@ struct MdMats {
 // rounds ahead of the block being computed.
 template <int FMT, int KS, int NB>
 __global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* __restrict__ X, int bpr, int batch,
-                                                      int ntt, int nrt) {
+                                                      int ntt, int nrt, int early_x) {
   constexpr int OWN = 16 / KS;  // chain elements per lane when KS > 1
   constexpr size_t BS = FMT == kQ4K ? kQ4KBytes : FMT == kQ6K ? kQ6KBytes : kQ8_0Bytes;
   constexpr size_t XS = FMT == kQ8_0 ? kQ8_0Bytes : kQ8KBytes;  // activation block bytes
@@ -524,9 +527,10 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* _
         if constexpr (FMT == kQ8_0) {
           md_q8(cur, scal, ta, kg, c, [&]() {});
         } else if constexpr (FMT == kQ4K) {
-          md_q4k(cur, stg, scal, ta, kg, c, [&]() {});
+          md_q4k(cur, stg, scal, ta, kg, c, [&]() {}, [&]() {});
         } else {
-          md_q6k(cur, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), stg, scal, ta, kg, c, [&](int) {});
+          md_q6k(cur, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), stg, scal, ta, kg, c, [&](int) {},
+                 [&]() {});
         }
         finish(k, c);
       }
@@ -562,9 +566,10 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* _
         if constexpr (FMT == kQ8_0) {
           md_q8(cur, scal, ta, kg, c, [&]() {});
         } else if constexpr (FMT == kQ4K) {
-          md_q4k(cur, stg, scal, ta, kg, c, [&]() {});
+          md_q4k(cur, stg, scal, ta, kg, c, [&]() {}, [&]() {});
         } else {
-          md_q6k(cur, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), stg, scal, ta, kg, c, [&](int) {});
+          md_q6k(cur, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), stg, scal, ta, kg, c, [&](int) {},
+                 [&]() {});
         }
         finish(k, c);
       }
@@ -597,10 +602,23 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* _
         if constexpr (FMT == kQ8_0) {
           md_q8(L, scal, ta, kg, c, [&]() { md_load<kQ8_0>(L, xn, wn, kg, xo); });
         } else if constexpr (FMT == kQ4K) {
-          md_q4k(L, stg, scal, ta, kg, c, [&]() { md_load<kQ4K>(L, xn, wn, kg, xo); });
+          // the next block's activation windows as soon as this block's are staged,
+          // its weights once this block's are consumed
+          // (early_x, uniform: the windows with the weights instead, once all are consumed)
+          md_q4k(L, stg, scal, ta, kg, c, [&]() {
+            if (!early_x) md_load_windows(L.x, xn, xo);
+            L.h = *(const u32x4*)wn;
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) L.q[cc] = *(const u32x4*)(wn + 16 + 32 * cc + 16 * kg);
+          }, [&]() {
+            if (early_x) md_load_windows(L.x, xn, xo);
+          });
         } else {
           md_q6k(L, (uint32_t)((uintptr_t)(wrow + (size_t)b * BS) & 3u), stg, scal, ta, kg, c,
-                 [&](int hh) { md_load_q6k_half(L, xn, wn, kg, hh, xo); });
+                 [&](int hh) { md_load_q6k_half(L, xn, wn, kg, hh, xo, !early_x); },
+                 [&]() {
+                   if (early_x) md_load_windows(L.x, xn, xo);
+                 });
         }
         finish(k, c);
       }
@@ -661,8 +679,14 @@ int md_launch_t(const MatmulGroupLaunch& G) {
   if (nwg > 0x7fffffffL) return NRQ_LAUNCH_BAD_ARG;
   const size_t lds = (size_t)KS * kMdScalDw * 4 + (KS > 1 ? (size_t)2 * KS * 1024 * 4 : 0) +
                      (FMT == kQ8_0 ? 0 : (size_t)KS * kMdStage);
+  // one buffer: the next block's activation windows load as soon as the
+  // current block's are staged (Q6_K, and Q4_K rows of 16+ blocks: down 30.5 ->
+  // 27.7 us, o 13.4 -> 12.4 us on the Qwen3-4B layer at M = 64; q|k|v, 10
+  // blocks, 13.4 -> 13.8 us, so not there), else with its weights
+  const char* ex = getenv("NRQ_MMT_EARLY_X");
+  const int early_x = ex && ex[0] ? ex[0] == '1' : (FMT == kQ6K || (FMT == kQ4K && G.bpr >= 16));
   hipLaunchKernelGGL((mmd_kernel<FMT, KS, NB>), dim3((unsigned)nwg), dim3(64 * KS), lds, (hipStream_t)G.stream, M,
-                     (const uint8_t*)G.xs, G.bpr, G.batch, ntt, nrt);
+                     (const uint8_t*)G.xs, G.bpr, G.batch, ntt, nrt, early_x);
   return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
 }
 
