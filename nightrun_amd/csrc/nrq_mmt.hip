@@ -711,8 +711,10 @@ int md_launch(const MatmulGroupLaunch& L, int ks, int nb) {
 // Block splits per tile: none when the tiles alone give two waves per CU
 // (a whole row of blocks per wave, double-buffered, beat two splits by 3-6%
 // on 9728 x 2560); else the fewest that give about one wave per SIMD (4 per
-// CU), and at most 4 for rows of 16 blocks or fewer (more splits leave each
-// wave one or two blocks). Measured on the Qwen3-4B layer shapes at M = 64.
+// CU), and at most 4 for rows of fewer than 16 blocks (more splits leave each
+// wave one or two blocks; the o projection's 16-block rows take 8 with the
+// early activation loads, 12.4 -> 12.0 us). Measured on the Qwen3-4B layer
+// shapes at M = 64.
 int md_choose(int dtype, long row_tiles, int batch, int bpr) {
   const char* env = getenv("NRQ_MMT_SPLITS");  // tuning override: 1, 2, 4 or 8
   if (env && env[0]) {
@@ -720,7 +722,7 @@ int md_choose(int dtype, long row_tiles, int batch, int bpr) {
     if (ks == 1 || ks == 2 || ks == 4 || ks == 8) return ks;
   }
   const long tiles = row_tiles * ((batch + 31) / 32);
-  const int cap = bpr <= 16 ? 4 : 8;
+  const int cap = bpr < 16 ? 4 : 8;
   // Q8_0 blocks are an eighth of a K-quant block's work: aim for twice the waves
   const long want = dtype == kQ8_0 ? 8L * 256 : 4L * 256;
   if (dtype != kQ8_0 && tiles >= 2L * 256) return 1;
