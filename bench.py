@@ -550,6 +550,35 @@ def measure_qwen3(fill=512, n=64):
                                "source": "docs/benchmarks.md:63-64, docs/baseline-x86.md:144"}}
 
 
+def measure_qwen3_eager(steps, fill=512):
+    """The Qwen3-4B leg's model and prompt, then `steps` greedy decode steps
+    launched eagerly (nrq_model_forward, no graph): a kernel trace of the
+    K-quant step without the captured-graph path."""
+    import torch
+
+    from nightrun_amd import nrm
+
+    cfg = QWEN3_4B
+    w = synth_model(cfg, 0x5EED0044, dtypes=QWEN3_DTYPES, embed_dtype=3, qk_norm=True)
+    blob = nrm_blob(cfg, w, arch=2, name=b"qwen3-4b")
+    del w
+    f = nrm.NrmFile(blob)
+    m = f.load(fill + steps + 8, verify=False)
+    del blob
+    prompt = np.random.default_rng(44).integers(0, cfg["vocab"], fill).astype(np.uint32)
+    lg = m.prefill(prompt)
+    tok = int(np.argmax(lg))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = int(np.argmax(m.forward(tok)))
+    dt = time.perf_counter() - t0
+    m.close()
+    return {"workload": "Qwen3-4B architecture, Q4_K_M formats, eager greedy steps (nrq_model_forward, logits "
+                        f"copied back each step) at positions {fill}..{fill + steps - 1}",
+            "steps": steps, "ms_per_step": round(dt / steps * 1e3, 4)}
+
+
 def host_cores():
     """Threads for the CPU baselines: every CPU this process may run on, up to
     the 16-core host share a one-GPU box gives a job (the pool is not sized past
@@ -734,6 +763,8 @@ def main():
     ap.add_argument("--also", default="cfg1,cfg3", help="other matvec configs reported beside (comma list)")
     ap.add_argument("--qwen3-only", action="store_true", help="only the Qwen3-4B decode/prefill leg")
     ap.add_argument("--no-qwen3", action="store_true", help="skip the Qwen3-4B decode/prefill leg")
+    ap.add_argument("--qwen3-eager", type=int, default=0, metavar="STEPS",
+                    help="only: the Qwen3-4B model, then STEPS eagerly launched greedy steps (no graph)")
     ap.add_argument("--prefill-only", type=int, default=0, metavar="TOKENS",
                     help="only time nrq_model_prefill of TOKENS tokens on the Llama-3.2-1B-shape model")
     ap.add_argument("--crc-only", type=int, default=0, metavar="BYTES",
@@ -743,6 +774,12 @@ def main():
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration << 20)
+        return
+    if args.qwen3_eager:
+        import nightrun_amd
+
+        nightrun_amd.init(0)
+        print(json.dumps({"decode_qwen3_eager": measure_qwen3_eager(args.qwen3_eager)}))
         return
     if args.qwen3_only:
         import nightrun_amd
