@@ -235,10 +235,11 @@ def measure_matvec(name, steps, warmup, order):
     return out
 
 
-def measure_prefill(reps=3):
+def measure_prefill(reps=3, order=0):
     """One Qwen3-4B layer's seven matmuls at M = 64 (Q8_K activations) in its
     four groups (q|k|v and gate|up share an activation and one launch), as one
-    graph of `reps` layers over rotating weight copies."""
+    graph of `reps` layers over rotating weight copies. order 1: the AVX2 f32
+    order (the x86 host's 4-token tiles), one launch per matrix."""
     import torch
 
     import nightrun_amd
@@ -270,8 +271,13 @@ def measure_prefill(reps=3):
     def layer(i):
         for g in groups:
             dt, cols, xq = mats[g[0]][0], mats[g[0]][2], mats[g[0]][4]
-            device.matmul_group(dt, [mats[j][5] for j in g], [mats[j][3][i % copies] for j in g],
-                                [mats[j][1] for j in g], xq, cols, 64, stream=stream)
+            if order == 0:
+                device.matmul_group(dt, [mats[j][5] for j in g], [mats[j][3][i % copies] for j in g],
+                                    [mats[j][1] for j in g], xq, cols, 64, stream=stream)
+            else:
+                for j in g:
+                    device.matmul(dt, order, mats[j][5], mats[j][3][i % copies], xq, mats[j][1], cols, 64,
+                                  stream=stream)
 
     flush = MallFlush()
     flush(stream)
@@ -282,6 +288,7 @@ def measure_prefill(reps=3):
     torch.cuda.empty_cache()
     return {"workload": "Qwen3-4B layer at M=64: Q/K/V/O/gate/up Q4_K, down Q6_K (hidden 2560, attention 4096, "
                         "KV 1024, ffn 9728), per-row Q8_K activations",
+            "order": "scalar" if order == 0 else "avx2",
             "us_per_layer": round(per * 1e6, 2), "tok_s_36_layers": round(64 / (36 * per), 1),
             "gbs": round(tot_bytes / per / 1e9, 1), "int8_tops": round(tot_ops / per / 1e12, 2),
             "mfma_frac_of_int8_peak": round(tot_ops / per / 1e12 / INT8_PEAK_TOPS, 4),
@@ -834,6 +841,8 @@ def main():
     prefill = None if args.no_prefill else measure_prefill()
     if prefill is not None:
         progress("prefill layer")
+        prefill["avx2_order"] = measure_prefill(order=1)
+        progress("prefill layer, AVX2 order")
     decode = None if args.no_decode else measure_decode(n=args.decode_tokens)
     if decode is not None:
         progress(f"decode {decode['tok_s']} tok/s")

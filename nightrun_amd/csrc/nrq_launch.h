@@ -103,6 +103,9 @@ struct MatmulGroupLaunch {
   void* stream;
 };
 int launch_mmt_group(int dtype, const MatmulGroupLaunch& G);
+// AVX2-order batched matmul on int8 MFMA (nrq_mma.hip): 32-row x 32-token
+// K-quant tiles, 8-row x 32-token Q8_0 tiles.
+int launch_mma(int dtype, const MatmulLaunch& L);
 int launch_quantize_q8_0(const QuantLaunch& L);
 // y[0..n) = +0.0 (a kernel, not hipMemsetAsync, so it is safe under graph capture)
 int launch_fill_zero(float* y, long long n, void* stream);

@@ -1,9 +1,10 @@
 // Batched matmul (prefill): y[b][r] = dot(W[r,:], xs[b]).
 // The reference guarantees matmul == per-token matvec bit for bit
 // (kernels.rs:84-90, kquant.rs:566-569). Scalar order runs the int8-MFMA tile
-// kernels (nrq_mmt.hip, nrq_mmq.hip). AVX2 order runs the decode kernel once per token,
-// which is bitwise equal by construction: the reference's 4-wide AVX2 tiles
-// return the 1-wide result per lane (kernels.rs:222-223).
+// kernels (nrq_mmt.hip, nrq_mmq.hip). AVX2 order runs the int8-MFMA tiles of
+// nrq_mma.hip from two tokens, and the decode kernel for one: both equal the
+// 1-wide AVX2 dot per token, as the reference's 4-wide tiles do
+// (kernels.rs:222-223).
 #include "nrq_device.h"
 #include "nrq_launch.h"
 
@@ -12,6 +13,7 @@ namespace nrq {
 int launch_matmul(int dtype, int order, const MatmulLaunch& L) {
   if (L.rows <= 0 || L.bpr <= 0 || L.batch <= 0) return 0;
   if (order == kOrderScalar) return launch_mmq(dtype, L);
+  if (L.batch >= 2) return launch_mma(dtype, L);
   const size_t xb = dtype == kQ8_0 ? (size_t)kQ8_0Bytes : (size_t)kQ8KBytes;
   for (int b = 0; b < L.batch; b++) {
     MatvecLaunch M;

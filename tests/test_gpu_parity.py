@@ -411,7 +411,7 @@ def test_benchmark_configs_bitexact(gpu, oracle, cfg, order):
     assert_bitwise(gpu_matvec(dtype, order, w, x, rows, cols), want, cfg)
 
 
-# ---- prefill matmul (int8 MFMA tile in scalar order) -------------------------------------
+# ---- prefill matmul (int8 MFMA tiles, both orders) ---------------------------------------
 
 # Qwen3-4B layer at M = 64 tokens: hidden 2560, attention width 4096, ffn 9728,
 # 8 KV heads x 128 (kv width 1024); Q/K/V/O/gate/up Q4_K, down Q6_K.
@@ -421,33 +421,38 @@ QWEN3_4B_LAYER = {
 }
 
 
+@pytest.mark.parametrize("order", ORDERS)
 @pytest.mark.parametrize("name", list(QWEN3_4B_LAYER))
-def test_prefill_qwen3_4b_layer_bitexact(gpu, oracle, name):
+def test_prefill_qwen3_4b_layer_bitexact(gpu, oracle, name, order):
     """Batched M = 64 matmul on the layer's real shapes equals the oracle's
-    matmul (== 64 matvecs, tests/kquant.rs:297-329) bit for bit."""
+    matmul (== 64 matvecs, tests/kquant.rs:297-329) bit for bit, in the
+    scalar order and in the AVX2 order (the 4-wide x4 tiles of
+    kquant.rs:566-639)."""
     dtype, rows, cols = QWEN3_4B_LAYER[name]
     seed = 0x5EED0004 + list(QWEN3_4B_LAYER).index(name)
     w = oracle.gen_weights(dtype, seed, rows, cols)
     xs = oracle.quantize_act(dtype, oracle.Rng(seed ^ 0x77).normal(64 * cols))
-    want = oracle.matmul(dtype, 0, w, xs, rows, cols, 64, threads=THREADS)
-    assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, 64), want, name)
+    want = oracle.matmul(dtype, order, w, xs, rows, cols, 64, threads=THREADS)
+    assert_bitwise(gpu_matmul(dtype, order, w, xs, rows, cols, 64), want, f"{name} {ONAMES[order]}")
 
 
+@pytest.mark.parametrize("order", ORDERS)
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_matmul_batches_past_64(gpu, oracle, dtype):
-    """The reference's matmul takes any batch; a launch covers it in 64-token
+def test_matmul_batches_past_64(gpu, oracle, dtype, order):
+    """The reference's matmul takes any batch; a launch covers it in 32-token
     tiles (batch 65 and 130: a one-token tile and a partial tile)."""
     qk = oracle.QK[dtype]
     rows, cols = 50, 3 * qk
     w = oracle.gen_weights(dtype, 91, rows, cols)
     for batch in (65, 130):
         xs = oracle.quantize_act(dtype, oracle.Rng(92 + batch).normal(batch * cols))
-        assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, batch),
-                       oracle.matmul(dtype, 0, w, xs, rows, cols, batch, threads=THREADS), f"batch {batch}")
+        assert_bitwise(gpu_matmul(dtype, order, w, xs, rows, cols, batch),
+                       oracle.matmul(dtype, order, w, xs, rows, cols, batch, threads=THREADS), f"batch {batch}")
 
 
+@pytest.mark.parametrize("order", ORDERS)
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_matmul_long_rows_and_odd_block_counts(gpu, oracle, dtype):
+def test_matmul_long_rows_and_odd_block_counts(gpu, oracle, dtype, order):
     """Rows longer than a split holds (70 blocks, 5 tokens: one split, idle
     token tiles), an odd block count at a full 64-token batch (Q6_K blocks of
     one row then alternate their 4-byte alignment), and a row count that is
@@ -457,13 +462,14 @@ def test_matmul_long_rows_and_odd_block_counts(gpu, oracle, dtype):
         cols = bpr * qk
         w = oracle.gen_weights(dtype, 700 + bpr, rows, cols)
         xs = oracle.quantize_act(dtype, oracle.Rng(701 + bpr).normal(batch * cols))
-        assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, batch),
-                       oracle.matmul(dtype, 0, w, xs, rows, cols, batch, threads=THREADS),
+        assert_bitwise(gpu_matmul(dtype, order, w, xs, rows, cols, batch),
+                       oracle.matmul(dtype, order, w, xs, rows, cols, batch, threads=THREADS),
                        f"rows {rows} bpr {bpr} batch {batch}")
 
 
+@pytest.mark.parametrize("order", ORDERS)
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_matmul_adversarial_and_saturated(gpu, oracle, dtype):
+def test_matmul_adversarial_and_saturated(gpu, oracle, dtype, order):
     """Adversarial activations, the reference quantizers' weights, and the
     saturated blocks of tests/kquant.rs:210-245 through the MFMA path."""
     qk = oracle.QK[dtype]
@@ -471,14 +477,71 @@ def test_matmul_adversarial_and_saturated(gpu, oracle, dtype):
     rng = oracle.Rng(400 + dtype)
     w = oracle.quantize_weights_ref(dtype, rng.adversarial(rows * cols))
     xs = oracle.quantize_act(dtype, rng.adversarial(batch * cols))
-    assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, batch), oracle.matmul(dtype, 0, w, xs, rows, cols, batch))
+    assert_bitwise(gpu_matmul(dtype, order, w, xs, rows, cols, batch),
+                   oracle.matmul(dtype, order, w, xs, rows, cols, batch))
     if dtype != 1:
         from tests.test_oracle import saturated_blocks
 
         q4, q6 = saturated_blocks(oracle)
         ws = np.repeat(q4 if dtype == 2 else q6, rows * 4, axis=0)
-        assert_bitwise(gpu_matmul(dtype, 0, ws, xs, rows, cols, batch),
-                       oracle.matmul(dtype, 0, ws, xs, rows, cols, batch))
+        assert_bitwise(gpu_matmul(dtype, order, ws, xs, rows, cols, batch),
+                       oracle.matmul(dtype, order, ws, xs, rows, cols, batch))
+
+
+def _q8k_raw(d, qs):
+    """Q8_K blocks from raw fields (bsums consistent with qs)."""
+    qs = np.asarray(qs, dtype=np.int8).reshape(-1, 256)
+    out = np.zeros((qs.shape[0], 292), dtype=np.uint8)
+    out[:, 0:4] = np.full((qs.shape[0], 1), d, dtype=np.float32).view(np.uint8)
+    out[:, 4:260] = qs.view(np.uint8)
+    out[:, 260:292] = qs.astype(np.int16).reshape(-1, 16, 16).sum(axis=2).astype(np.int16).view(np.uint8)
+    return out
+
+
+@pytest.mark.parametrize("dtype", [2, 3])
+def test_matmul_avx2_extreme_integer_sums(gpu, oracle, dtype):
+    """The AVX2 order's per-lane integer sums at their extremes, where the
+    MFMA tile splits each scaled weight into two int8 operands: Q6_K scale
+    -128 against quants 0 (sc * (q - 32) = 4096) and activations -128, a lane
+    sum of -2^24 (kquant.rs:495-499); Q4_K scale 63 against nibbles 15; and
+    mixed signs and scales. Batches of 2 and 33 (the smallest MFMA batch, and
+    a one-token second tile), 37 rows (a partial row tile), 3 blocks a row."""
+    rows, bpr = 37, 3
+    cols = 256 * bpr
+    rng = np.random.default_rng(1234 + dtype)
+    if dtype == 3:
+        w = np.zeros((rows * bpr, 210), dtype=np.uint8)
+        w[:, 192:208] = np.array(-128, dtype=np.int8).view(np.uint8)
+        w[:, 208:210] = np.array([oracle.f32_to_f16(1.0)], dtype=np.uint16).view(np.uint8)
+        mixed = rng.integers(0, 256, size=(rows * bpr, 208), dtype=np.uint8)
+        w[1::2, :208] = mixed[1::2]  # odd blocks: random quants and signed scales
+    else:
+        w = np.zeros((rows * bpr, 144), dtype=np.uint8)
+        w[:, 0:2] = np.array([oracle.f32_to_f16(1.0)], dtype=np.uint16).view(np.uint8)
+        w[:, 2:4] = np.array([oracle.f32_to_f16(0.5)], dtype=np.uint16).view(np.uint8)
+        w[:, 4:] = 0xFF  # every 6-bit scale and min 63, every nibble 15
+        mixed = rng.integers(0, 256, size=(rows * bpr, 140), dtype=np.uint8)
+        w[1::2, 4:] = mixed[1::2]
+    for batch in (2, 33):
+        qs = np.full((batch * bpr, 256), -128, dtype=np.int8)
+        qs[1::2] = rng.integers(-128, 128, size=qs[1::2].shape, dtype=np.int8)
+        xs = _q8k_raw(1.0, qs)
+        assert_bitwise(gpu_matmul(dtype, 1, w, xs, rows, cols, batch),
+                       oracle.matmul(dtype, 1, w, xs, rows, cols, batch), f"batch {batch}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_matmul_avx2_small_shapes(gpu, oracle, dtype):
+    """AVX2-order matmul at the small cases of the MFMA tiles: one block a
+    row, fewer rows than a tile (1, 7, 9), one token (the decode kernel), two
+    tokens, and rows just past one and two 32-row tiles."""
+    qk = oracle.QK[dtype]
+    for rows, bpr, batch in ((1, 1, 2), (7, 2, 3), (9, 1, 1), (33, 2, 2), (65, 5, 31)):
+        cols = bpr * qk
+        w = oracle.gen_weights(dtype, 1300 + rows, rows, cols)
+        xs = oracle.quantize_act(dtype, oracle.Rng(1301 + rows).normal(batch * cols))
+        assert_bitwise(gpu_matmul(dtype, 1, w, xs, rows, cols, batch),
+                       oracle.matmul(dtype, 1, w, xs, rows, cols, batch), f"rows {rows} bpr {bpr} batch {batch}")
 
 
 @pytest.mark.parametrize("dtype", [1, 2, 3])
