@@ -130,6 +130,69 @@ __device__ __forceinline__ int nearest_int(float v) {
   return v >= 0.0f ? rust_f32_to_i32(v + 0.5f) : rust_f32_to_i32(v - 0.5f);
 }
 
+// One Q8_K block (kquant.rs:157-187) from 32 lanes of a half-wave, lane r
+// holding values 8r .. 8r+7 of the block: the first index of the largest |v|
+// (a strict `>` scan; NaN never wins), iscale = -128 / v[that index],
+// q = min(nearest_int(iscale * v), 127), d = 1 / iscale, an all-zero block
+// when the largest |v| is not > 0. Returns lane r's 8 quants (lo, hi), the
+// 16-value sum of lanes r & ~1 and r | 1 (ps), and d's f32 bits.
+__device__ __forceinline__ void q8k_half_lanes(const float o[8], int r, uint32_t* lo_out, uint32_t* hi_out,
+                                               int* ps_out, uint32_t* d_bits_out) {
+  // this lane's largest |v| and its first value holding it
+  float al = -1.0f, mine = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    float ae = fabsf(o[e]);
+    if (ae != ae) ae = -1.0f;
+    if (ae > al) {
+      al = ae;
+      mine = o[e];
+    }
+  }
+  // the half-wave's largest: max over quads and 16-lane rows (DPP), then the
+  // row pair; no NaN is left, so the max is exact in any order
+  float a = al;
+  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0xB1, 0xF, 0xF, false)));
+  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x4E, 0xF, 0xF, false)));
+  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x124, 0xF, 0xF, false)));
+  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x128, 0xF, 0xF, false)));
+  a = fmaxf(a, __shfl_xor(a, 16, 32));
+  // the first index holding it: the first such lane of the half-wave, its first such value
+  const unsigned long long has = __ballot(al == a);
+  const uint32_t hw = (uint32_t)(has >> (__lane_id() & 32));
+  const float mx = __shfl(mine, (int)__builtin_ctz(hw | 0x80000000u), 32);
+  const bool zero = !(a > 0.0f);
+  const float iscale = -128.0f / mx;
+  int q[8];
+  int p = 0;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const int t = nearest_int(iscale * o[e]);
+    q[e] = zero ? 0 : (t > 127 ? 127 : t);
+    p += q[e];
+  }
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    lo |= (uint32_t)(q[e] & 0xff) << (8 * e);
+    hi |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
+  }
+  *lo_out = lo;
+  *hi_out = hi;
+  *ps_out = p + __builtin_amdgcn_update_dpp(0, p, 0xB1, 0xF, 0xF, false);  // lane r ^ 1 (quad_perm [1,0,3,2])
+  *d_bits_out = zero ? 0u : __float_as_uint(1.0f / iscale);
+}
+
+// Lane r's part of the 292-byte Q8_K block at gout (4-byte aligned): its 8
+// quants, bsums[r / 2] from the even lanes, d from lane 0.
+__device__ __forceinline__ void q8k_half_store(uint8_t* gout, int r, uint32_t lo, uint32_t hi, int ps,
+                                               uint32_t d_bits) {
+  *(uint32_t*)(gout + 4 + 8 * r) = lo;
+  *(uint32_t*)(gout + 8 + 8 * r) = hi;
+  if ((r & 1) == 0) *(int16_t*)(gout + 260 + r) = (int16_t)ps;
+  if (r == 0) *(uint32_t*)gout = d_bits;
+}
+
 // q8::quantize (q8.rs:27-44) of one 32-value block held one value per lane of
 // a 32-lane group: amax over the group, d = f16(amax / 127), round half away
 // from zero, clamp to [-127, 127]. Returns this lane's quant and the f16 bits of d.

@@ -254,14 +254,17 @@ constexpr int kNormPT = kNormMax / kNormNT;  // values per thread
 // Optional residual x += rs * add (saxpy, vec.rs:68-72; rs is residual_scale), then
 // rmsnorm (vec.rs:4-14): ss += v*v in element order, scale = 1/sqrtf(ss/n + eps),
 // out = x * scale * w. Writes out (f32) and, when xq != null, its Q8_0 blocks
-// (q8.rs:27-44). One workgroup; n <= kNormMax, a multiple of 256. Thread t
-// owns the 8-value runs t + 256k (four consecutive runs, an aligned lane quad,
-// make one Q8_0 block), loaded once, all loads issued before the first use;
-// wave 0 runs the sequential sum of squares. Workgroup r takes row r of
-// [rows][n] x, add, out and xq (one row per workgroup in a prefill chunk).
+// (q8.rs:27-44), when xqk != null its Q8_K blocks (kquant.rs:157-187). One
+// workgroup; n <= kNormMax, a multiple of 256. Thread t owns the 8-value runs
+// t + 256k (four consecutive runs, an aligned lane quad, make one Q8_0 block;
+// 32, an aligned half-wave, one Q8_K block), loaded once, all loads issued
+// before the first use; wave 0 runs the sequential sum of squares. Workgroup r
+// takes row r of [rows][n] x, add, out, xq and xqk (one row per workgroup in a
+// prefill chunk).
 __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, const float* __restrict__ add,
                                                        const float* __restrict__ w, int n, float eps, float rs,
-                                                       float* __restrict__ out, uint8_t* __restrict__ xq) {
+                                                       float* __restrict__ out, uint8_t* __restrict__ xq,
+                                                       uint8_t* __restrict__ xqk) {
   __shared__ __align__(16) float sq[kNormMax];
   __shared__ __align__(16) uint32_t chain_work[kChainWork];
   {
@@ -270,6 +273,7 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
     if (add) add += r * n;
     out += r * n;
     if (xq) xq += r * (size_t)(n / 32) * kQ8_0Bytes;
+    if (xqk) xqk += r * (size_t)(n / 256) * kQ8KBytes;
   }
   __shared__ float s_scale;
   const int tid = threadIdx.x;
@@ -335,6 +339,12 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
         qs[2] = (uint16_t)hi;
         qs[3] = (uint16_t)(hi >> 16);
         if ((j & 3) == 0) *(uint16_t*)blk = (uint16_t)d_bits;
+      }
+      if (xqk) {  // n is a multiple of 256: whole half-waves take this branch
+        uint32_t lo, hi, d_bits;
+        int ps;
+        q8k_half_lanes(o, j & 31, &lo, &hi, &ps, &d_bits);
+        q8k_half_store(xqk + (size_t)(j >> 5) * kQ8KBytes, j & 31, lo, hi, ps, d_bits);
       }
     }
   }
@@ -1453,9 +1463,8 @@ int matvec(nrq_model* m, const Mat& w, const uint8_t* xq, float* y, int rows, in
 int norm_quant(nrq_model* m, float* xr, const float* add, const float* w, int dt) {
   const auto& c = m->cfg;
   hipLaunchKernelGGL(nrq::norm_kernel, dim3(1), dim3(nrq::kNormNT), 0, m->stream, xr, add, w, c.dim, c.norm_eps,
-                     m->res_scale, m->xb, dt == NRQ_Q8_0 ? m->xq : nullptr);
+                     m->res_scale, m->xb, dt == NRQ_Q8_0 ? m->xq : nullptr, dt != NRQ_Q8_0 ? m->xq : nullptr);
   if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: norm launch failed");
-  if (dt != NRQ_Q8_0) return quantize_for(m, dt, m->xb, c.dim, m->xq);
   return NRQ_OK;
 }
 
@@ -1768,12 +1777,12 @@ int matmul_rows(nrq_model* m, const Mat& w, const uint8_t* xs, float* y, int row
 // rows are quantized once per format; m->bxq holds the Q8_0 blocks when
 // `have_q8` (written by the producing kernel), m->bxq2 the Q8_K ones.
 int matmul_group_rows(nrq_model* m, const Mat* const* ws, float* const* ys, const int* rows, int n, const float* x,
-                      int cols, int B, bool have_q8) {
+                      int cols, int B, bool have_q8, bool have_q8k = false) {
   bool need_q8 = false, need_q8k = false;
   for (int i = 0; i < n; i++) (ws[i]->dt == NRQ_Q8_0 ? need_q8 : need_q8k) = true;
   int rc;
   if (need_q8 && !have_q8 && (rc = quantize_for(m, NRQ_Q8_0, x, B * cols, m->bxq))) return rc;
-  if (need_q8k && (rc = quantize_for(m, NRQ_Q4_K, x, B * cols, m->bxq2))) return rc;
+  if (need_q8k && !have_q8k && (rc = quantize_for(m, NRQ_Q4_K, x, B * cols, m->bxq2))) return rc;
   bool same = n > 1;
   for (int i = 1; i < n; i++) same = same && ws[i]->dt == ws[0]->dt;
   if (same) {  // one launch for the group where the prefill kernel takes it
@@ -1803,6 +1812,12 @@ bool any_q8(const Mat* const* ws, int n) {
   return false;
 }
 
+bool any_kquant(const Mat* const* ws, int n) {
+  for (int i = 0; i < n; i++)
+    if (ws[i]->dt != NRQ_Q8_0) return true;
+  return false;
+}
+
 // InferCtx::prefill_chunk (infer.rs:601-750) for B tokens at positions
 // pos..pos+B-1 (ctl[CTL_POS] = pos): batched norms and matmuls, all the
 // chunk's K/V appended, then causal attention for every (head, token); the
@@ -1825,11 +1840,11 @@ int enqueue_prefill(nrq_model* m, int B) {
       const Mat* ws[3] = {&Ly.m[0], &Ly.m[1], &Ly.m[2]};
       float* ys[3] = {m->bq, m->bk, m->bv};
       const int rows[3] = {att, kvd, kvd};
-      const bool q8 = any_q8(ws, 3);
+      const bool q8 = any_q8(ws, 3), q8k = any_kquant(ws, 3);
       hipLaunchKernelGGL(nrq::norm_kernel, dim3(B), dim3(nrq::kNormNT), 0, m->stream, m->bx, pending, Ly.attn_norm,
-                         d, c.norm_eps, m->res_scale, m->bxn, q8 ? m->bxq : nullptr);
+                         d, c.norm_eps, m->res_scale, m->bxn, q8 ? m->bxq : nullptr, q8k ? m->bxq2 : nullptr);
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: norm launch failed");
-      if ((rc = matmul_group_rows(m, ws, ys, rows, 3, m->bxn, d, B, q8))) return rc;
+      if ((rc = matmul_group_rows(m, ws, ys, rows, 3, m->bxn, d, B, q8, q8k))) return rc;
     }
     const size_t rlds = Ly.q_norm ? (size_t)(c.n_heads + c.n_kv_heads) * (c.head_dim + 1) * 4 : 0;
     hipLaunchKernelGGL(nrq::rope_append_kernel, dim3(B), dim3(256), rlds, m->stream, m->bq, m->bk, m->bv, m->brope,
@@ -1863,22 +1878,28 @@ int enqueue_prefill(nrq_model* m, int B) {
       const Mat* ws[2] = {&Ly.m[4], &Ly.m[5]};
       float* ys[2] = {m->bgate, m->bup};
       const int rows[2] = {ffn, ffn};
-      const bool q8 = any_q8(ws, 2);
+      const bool q8 = any_q8(ws, 2), q8k = any_kquant(ws, 2);
       hipLaunchKernelGGL(nrq::norm_kernel, dim3(B), dim3(nrq::kNormNT), 0, m->stream, m->bx, m->bxb, Ly.ffn_norm, d,
-                         c.norm_eps, m->res_scale, m->bxn, q8 ? m->bxq : nullptr);
+                         c.norm_eps, m->res_scale, m->bxn, q8 ? m->bxq : nullptr, q8k ? m->bxq2 : nullptr);
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: norm launch failed");
-      if ((rc = matmul_group_rows(m, ws, ys, rows, 2, m->bxn, d, B, q8))) return rc;
+      if ((rc = matmul_group_rows(m, ws, ys, rows, 2, m->bxn, d, B, q8, q8k))) return rc;
     }
     {
       const bool q8 = Ly.m[6].dt == NRQ_Q8_0;
       const long long n = (long long)B * ffn;
-      hipLaunchKernelGGL(nrq::swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, m->stream, m->bgate,
-                         m->bup, (int)n, q8 ? m->bxq : nullptr);
-      if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: swiglu launch failed");
+      if (q8) {
+        hipLaunchKernelGGL(nrq::swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, m->stream, m->bgate,
+                           m->bup, (int)n, m->bxq);
+        if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: swiglu launch failed");
+      } else {
+        // swiglu inside the Q8_K quantizer, as in the decode step (vec.rs:45-52)
+        nrq::QuantLaunch Q{m->bgate, m->bxq2, n, m->stream, m->bup};
+        if (nrq::launch_quantize_q8k(Q)) return mfail(NRQ_ERR_DEVICE, "model: swiglu quantize launch failed");
+      }
       const Mat* ws[1] = {&Ly.m[6]};
       float* ys[1] = {m->bxb};
       const int rows[1] = {d};
-      if ((rc = matmul_group_rows(m, ws, ys, rows, 1, m->bgate, ffn, B, q8))) return rc;
+      if ((rc = matmul_group_rows(m, ws, ys, rows, 1, m->bgate, ffn, B, q8, !q8))) return rc;
     }
     pending = m->bxb;
   }
@@ -2316,7 +2337,7 @@ int nrq_dev_rmsnorm(const float* x, const float* w, float* out, size_t rows, siz
   if (rows > (size_t)INT_MAX) return mfail(NRQ_ERR_SHAPE, "nrq_dev_rmsnorm: too many rows");
   // norm_kernel updates x in place only when it adds a residual; here it reads x
   hipLaunchKernelGGL(nrq::norm_kernel, dim3((unsigned)rows), dim3(nrq::kNormNT), 0, (hipStream_t)stream,
-                     const_cast<float*>(x), nullptr, w, (int)n, eps, 1.0f, out, nullptr);
+                     const_cast<float*>(x), nullptr, w, (int)n, eps, 1.0f, out, nullptr, nullptr);
   return hipGetLastError() == hipSuccess ? NRQ_OK : mfail(NRQ_ERR_DEVICE, "nrq_dev_rmsnorm: launch failed");
 }
 

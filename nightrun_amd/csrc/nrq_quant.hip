@@ -38,79 +38,29 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restr
   }
 }
 
-// One 256-thread workgroup per Q8_K block. With `up`, the values quantized
-// are swiglu(src, up) = src / (1 + expf(-src)) * up (vec.rs:45-52), also
-// written back over src.
+// One Q8_K block per 256-thread workgroup: thread t loads value t (and with
+// `up` forms swiglu(src, up) = src / (1 + expf(-src)) * up, vec.rs:45-52,
+// written back over src), then the first half-wave quantizes the block,
+// lane r holding values 8r .. 8r+7 (q8k_half_lanes, nrq_device.h).
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(float* __restrict__ src, uint8_t* __restrict__ dst,
                                                            const float* __restrict__ up) {
-  __shared__ float s_abs[4];
-  __shared__ int s_idx[4];
-  __shared__ int s_q[256];
-  __shared__ float s_v[256];
+  __shared__ __align__(16) float s_v[256];
   const long long b = blockIdx.x;
-  const int i = threadIdx.x;
-  float v = src[b * 256 + i];
+  const int t = threadIdx.x;
+  float v = src[b * 256 + t];
   if (up) {
-    v = v / (1.0f + dev_expf(-v)) * up[b * 256 + i];
-    src[b * 256 + i] = v;
+    v = v / (1.0f + dev_expf(-v)) * up[b * 256 + t];
+    src[b * 256 + t] = v;
   }
-  s_v[i] = v;
-  // The first index holding the largest |v| (strict `>` scan, NaN never wins).
-  float a = fabsf(v);
-  if (a != a) a = -1.0f;
-  int idx = i;
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    float oa = __shfl_xor(a, m);
-    int oi = __shfl_xor(idx, m);
-    if (oa > a || (oa == a && oi < idx)) {
-      a = oa;
-      idx = oi;
-    }
-  }
-  const int wave = i >> 6;
-  if ((i & 63) == 0) {
-    s_abs[wave] = a;
-    s_idx[wave] = idx;
-  }
+  s_v[t] = v;
   __syncthreads();
-  float ba = s_abs[0];
-  int bi = s_idx[0];
-  for (int w = 1; w < 4; w++) {
-    if (s_abs[w] > ba || (s_abs[w] == ba && s_idx[w] < bi)) {
-      ba = s_abs[w];
-      bi = s_idx[w];
-    }
-  }
-  uint8_t* blk = dst + b * kQ8KBytes;
-  if (!(ba > 0.0f)) {  // amax == 0: all-zero block (kquant.rs:168-172)
-    blk[4 + i] = 0;
-    if (i < 4) blk[i] = 0;
-    if (i < 32) blk[260 + i] = 0;
-    return;
-  }
-  const float max = s_v[bi];  // s_v was written before the barrier above
-  const float iscale = -128.0f / max;
-  int q = nearest_int(iscale * v);
-  q = q > 127 ? 127 : q;
-  const int8_t q8 = (int8_t)q;
-  blk[4 + i] = (uint8_t)q8;
-  s_q[i] = q8;
-  __syncthreads();
-  if (i < 16) {
-    int s = 0;
-    for (int k = 0; k < 16; k++) s += s_q[i * 16 + k];
-    int16_t s16 = (int16_t)s;
-    blk[260 + 2 * i] = (uint8_t)(s16 & 0xff);
-    blk[261 + 2 * i] = (uint8_t)((uint16_t)s16 >> 8);
-  }
-  if (i == 0) {
-    float d = 1.0f / iscale;
-    uint32_t db = __float_as_uint(d);
-    blk[0] = (uint8_t)(db & 0xff);
-    blk[1] = (uint8_t)((db >> 8) & 0xff);
-    blk[2] = (uint8_t)((db >> 16) & 0xff);
-    blk[3] = (uint8_t)(db >> 24);
+  if (t < 32) {
+    const float4 p0 = ((const float4*)s_v)[2 * t], p1 = ((const float4*)s_v)[2 * t + 1];
+    const float o[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+    uint32_t lo, hi, d_bits;
+    int ps;
+    q8k_half_lanes(o, t, &lo, &hi, &ps, &d_bits);
+    q8k_half_store(dst + b * kQ8KBytes, t, lo, hi, ps, d_bits);
   }
 }
 
@@ -164,7 +114,7 @@ int launch_quantize_q8_0(const QuantLaunch& L) {
 int launch_quantize_q8k(const QuantLaunch& L) {
   if (L.n <= 0) return 0;
   if (L.n % 256) return NRQ_LAUNCH_BAD_ARG;
-  long long nb = L.n / 256;
+  const long long nb = L.n / 256;
   hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)L.stream,
                      const_cast<float*>(L.src), (uint8_t*)L.dst, L.up);
   return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;

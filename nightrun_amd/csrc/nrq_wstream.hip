@@ -319,58 +319,16 @@ struct WSGeom {
 // 1.0), fused into a Q8_0 matvec's prologue: LDS holds x, add and the norm
 // weight (DMA, issued before the weight tiles), then the squares; the result
 // is quantized to Q8_0 (q8.rs:27-44) straight into the activation layout.
-// One Q8_K block (kquant.rs:157-187) from 32 lanes of a half-wave, lane r
-// holding values 8r .. 8r+7 of the block: the first index of the largest |v|
-// (a strict `>` scan; NaN never wins), iscale = -128 / v[that index],
-// q = min(nearest_int(iscale * v), 127), d = 1 / iscale, an all-zero block
-// when the largest |v| is not > 0. Written into the kernel's activation layout
-// (Q4_K: qs, 16-value sums as i16 pairs, d; Q6_K: qs, -32 * 16-value sums, d)
-// and, when gout != null, as the standard 292-byte block.
+// One Q8_K block (kquant.rs:157-187) from a half-wave (q8k_half_lanes,
+// nrq_device.h), written into the kernel's activation layout (Q4_K: qs,
+// 16-value sums as i16 pairs, d; Q6_K: qs, -32 * 16-value sums, d) and, when
+// gout != null, as the standard 292-byte block.
 template <int FMT>
 __device__ __forceinline__ void ws_q8k_half(const float o[8], int r, uint32_t* xb, uint8_t* gout) {
-  float a = -1.0f;
-  int idx = 8 * r;
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    float ae = fabsf(o[e]);
-    if (ae != ae) ae = -1.0f;
-    if (ae > a) {
-      a = ae;
-      idx = 8 * r + e;
-    }
-  }
-#pragma unroll
-  for (int m = 16; m >= 1; m >>= 1) {
-    const float oa = __shfl_xor(a, m, 32);
-    const int oi = __shfl_xor(idx, m, 32);
-    if (oa > a || (oa == a && oi < idx)) {
-      a = oa;
-      idx = oi;
-    }
-  }
-  float mine = o[0];
-#pragma unroll
-  for (int e = 1; e < 8; e++) mine = (idx & 7) == e ? o[e] : mine;
-  const float mx = __shfl(mine, idx >> 3, 32);
-  const bool zero = !(a > 0.0f);
-  const float iscale = -128.0f / mx;
-  int q[8];
-  int p = 0;
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const int t = nearest_int(iscale * o[e]);
-    q[e] = zero ? 0 : (t > 127 ? 127 : t);
-    p += q[e];
-  }
-  uint32_t lo = 0, hi = 0;
-#pragma unroll
-  for (int e = 0; e < 4; e++) {
-    lo |= (uint32_t)(q[e] & 0xff) << (8 * e);
-    hi |= (uint32_t)(q[4 + e] & 0xff) << (8 * e);
-  }
-  const int ps = p + __shfl_xor(p, 1, 32);          // the 16-value sum of lanes r & ~1, r | 1
-  const int ps2 = __shfl_down(ps, 2, 32);           // the next pair's sum
-  const uint32_t d_bits = zero ? 0u : __float_as_uint(1.0f / iscale);
+  uint32_t lo, hi, d_bits;
+  int ps;
+  q8k_half_lanes(o, r, &lo, &hi, &ps, &d_bits);
+  const int ps2 = __shfl_down(ps, 2, 32);  // the next pair's sum
   ((uint2*)xb)[r] = make_uint2(lo, hi);
   if constexpr (FMT == kQ4K) {
     if ((r & 3) == 0) xb[64 + (r >> 2)] = ((uint32_t)ps & 0xffffu) | ((uint32_t)ps2 << 16);
@@ -379,12 +337,7 @@ __device__ __forceinline__ void ws_q8k_half(const float o[8], int r, uint32_t* x
     if ((r & 1) == 0) xb[64 + (r >> 1)] = (uint32_t)(-32 * ps);
     if (r == 0) xb[80] = d_bits;
   }
-  if (gout) {
-    *(uint32_t*)(gout + 4 + 8 * r) = lo;  // 4-byte aligned: blocks are 292 bytes
-    *(uint32_t*)(gout + 8 + 8 * r) = hi;
-    if ((r & 1) == 0) *(int16_t*)(gout + 260 + r) = (int16_t)ps;
-    if (r == 0) *(uint32_t*)gout = d_bits;
-  }
+  if (gout) q8k_half_store(gout, r, lo, hi, ps, d_bits);
 }
 
 constexpr int kFusedNormMax = 4096;

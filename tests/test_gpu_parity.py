@@ -138,6 +138,18 @@ def quant_inputs(oracle, n):
     special[9::43] = -np.inf
     special[11::47] = f.tiny / 4
     cases.append(special)
+    # the largest |v| twice with opposite signs: the first index sets the
+    # scale's sign (kquant.rs:162-167); positions in one lane, across quads,
+    # 16-lane rows and half-waves of a 256-value block, and the same with +-inf
+    pairs = [(0, 1), (1, 0), (7, 8), (8, 7), (31, 32), (32, 31), (100, 200), (200, 100), (255, 0), (0, 255),
+             (128, 127), (127, 128)]
+    for big in (np.float32(2.0), np.float32(np.inf)):
+        tie = rng.vec(n) * np.float32(0.5)
+        for k in range(n // 256):
+            p1, p2 = pairs[k % len(pairs)]
+            tie[256 * k + p1] = -big
+            tie[256 * k + p2] = big
+        cases.append(tie)
     return cases
 
 
