@@ -1627,7 +1627,8 @@ int enqueue_step(nrq_model* m) {
                    : c.head_dim == 64 ? (ds == 2 ? nrq::attention_kernel<64, false, nrq::kAttNT, 2>
                                                  : nrq::attention_kernel<64>)
                    : c.head_dim == 96 ? nrq::attention_kernel<96>
-                                      : nrq::attention_kernel<128>;
+                                      : (ds == 4 ? nrq::attention_kernel<128, false, 768, 4>
+                                                 : nrq::attention_kernel<128>);
       hipLaunchKernelGGL(kern, dim3(c.n_heads * ds), dim3(nrq::att_threads(c.head_dim)), m->att_lds, m->stream, m->q, m->k, m->v,
                          m->rope_cs, m->ctl, c.n_heads, c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->attn,
                          q8 ? m->xq : nullptr, Ly.q_norm, Ly.k_norm, c.norm_eps, m->rope_neox);
@@ -1714,13 +1715,14 @@ AttGroupFn att_group_for(int gh, size_t* lds, int ctx) {
   }
 }
 
-// Workgroups per head of the decode attention: two (32 value dimensions each,
-// on one XCD) for 64-wide heads when the head count allows the XCD mapping;
-// NRQ_ATT_SPLIT=1 forces one.
+// Workgroups per head of the decode attention, 32 value dimensions each (all
+// of a head's on one XCD) when the head count allows that mapping: two for
+// 64-wide heads, four for 128-wide ones; NRQ_ATT_SPLIT=1 forces one.
 int att_dim_split(const nrq_model_config& c) {
   const char* env = getenv("NRQ_ATT_SPLIT");
   if (env && env[0] == '1') return 1;
-  return c.head_dim == 64 && c.n_heads % 8 == 0 ? 2 : 1;
+  if (c.n_heads % 8) return 1;
+  return c.head_dim == 64 ? 2 : c.head_dim == 128 ? 4 : 1;
 }
 
 // The grouped prefill attention for this model's shape, or null (then one

@@ -305,19 +305,25 @@ def test_tiny_model_long_context(gpu, oracle, ctx):
 
 
 TINY8 = dict(TINY, dim=512, n_heads=8, n_kv_heads=2)
+QWEN8_HD128 = dict(dim=1024, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=128, ffn_dim=512, vocab=1000,
+                   norm_eps=1e-6, rope_theta=1000000.0, recipe=dict(rope="neox"))
 
 
-@pytest.mark.parametrize("split", ["2", "1"])
-def test_decode_attention_dimension_split(gpu, oracle, monkeypatch, split):
-    """Eight 64-wide heads: the decode attention runs two workgroups per head
-    (32 value dimensions each, 256-position value chunks) by default, one with
-    NRQ_ATT_SPLIT=1. 1100 prompt positions, so the split kernel's value loop
-    runs five chunks and reuses every ring slot; then 12 greedy steps, each
-    bit-exact against the oracle."""
-    monkeypatch.setenv("NRQ_ATT_SPLIT", split)
-    w = oracle.gen_model(TINY8, 5150)
-    prompt = np.random.default_rng(5150).integers(0, TINY8["vocab"], 1100).astype(np.uint32)
-    run_pair(oracle, TINY8, w, 2048, prompt, 12, prefill=True)
+@pytest.mark.parametrize("split", ["default", "1"])
+@pytest.mark.parametrize("cfg", [TINY8, QWEN8_HD128], ids=["hd64", "qwen-hd128"])
+def test_decode_attention_dimension_split(gpu, oracle, monkeypatch, cfg, split):
+    """Eight heads: the decode attention runs 32 value dimensions per
+    workgroup (two per 64-wide head, four per 128-wide Qwen3 head with its
+    q/k norms, 256-position value chunks) by default, one workgroup per head
+    with NRQ_ATT_SPLIT=1. 1100 prompt positions, so the split kernel's value
+    loop runs five chunks and reuses every ring slot; then 12 greedy steps,
+    each bit-exact against the oracle."""
+    if split == "1":
+        monkeypatch.setenv("NRQ_ATT_SPLIT", split)
+    qk = "recipe" in cfg
+    w = oracle.gen_model(cfg, 5150, qk_norm=qk)
+    prompt = np.random.default_rng(5150).integers(0, cfg["vocab"], 1100).astype(np.uint32)
+    run_pair(oracle, cfg, w, 2048, prompt, 12, prefill=True)
 
 
 @pytest.mark.parametrize("n", [1, 5, 63, 64, 65, 70, 130])
