@@ -326,6 +326,29 @@ def test_decode_attention_dimension_split(gpu, oracle, monkeypatch, cfg, split):
     run_pair(oracle, cfg, w, 2048, prompt, 12, prefill=True)
 
 
+# Q4_K_M's layer formats: q, k, o, gate, up Q4_K; v, down Q6_K
+Q4K_M = {"wq": 2, "wk": 2, "wv": 3, "wo": 2, "w_gate": 2, "w_up": 2, "w_down": 3}
+
+
+@pytest.mark.parametrize("prefill", [False, True], ids=["decode", "prefill"])
+def test_qwen3_q4k_m_layer_formats(gpu, oracle, prefill):
+    """Qwen3 (q/k norms, Neox rope, 128-wide heads) with the Q4_K_M layer
+    formats: in the decode step the fused norm + q|k launch (Q4_K) also stores
+    the Q8_K activation that v's Q6_K matvec reads, and the Q6_K down
+    projection takes swiglu from the Q8_K quantizer. Logits, tokens and the KV
+    cache bit-exact against the oracle."""
+    cfg = QWEN8_HD128
+    w = oracle.gen_model(cfg, 4242, qk_norm=True)
+    shapes = oracle.layer_shapes(cfg)
+    for l, lw in enumerate(w["layers"]):
+        for i, name in enumerate(oracle.LAYER_MATS):
+            rows, cols = shapes[name]
+            lw[name] = oracle.gen_weights(Q4K_M[name], 4300 + 16 * l + i, rows, cols)
+            lw["dtypes"][name] = Q4K_M[name]
+    prompt = np.random.default_rng(4242).integers(0, cfg["vocab"], 70).astype(np.uint32)
+    run_pair(oracle, cfg, w, 128, prompt, 8, prefill=prefill)
+
+
 @pytest.mark.parametrize("n", [1, 5, 63, 64, 65, 70, 130])
 def test_tiny_model_prefill(gpu, oracle, n):
     """Device prefill (64-token batched chunks) == the oracle's prefill: the
