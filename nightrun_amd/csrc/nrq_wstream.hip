@@ -678,9 +678,20 @@ static int ws_rows_per_wave(int bpr, int cap) {
   return best;
 }
 
+static int ws_num_cus();
+
 template <int FMT>
 static int launch_ws(const MatvecLaunch& L) {
-  const int rpw = ws_rows_per_wave<FMT>(L.bpr, L.tile_rows);
+  int rpw = ws_rows_per_wave<FMT>(L.bpr, L.tile_rows);
+  // Short matrices: half the rows per wave when that still fills half of each
+  // tile and the default leaves SIMDs without a wave (the Llama-3.2-1B o
+  // projection, 2048 x 2048 Q8_0: four rows per wave, 512 waves, 5.32 us; two
+  // rows, 1024 waves, 4.98 us; single launches after the MALL flush)
+  if (L.tile_rows == 0 && rpw % 2 == 0) {
+    constexpr int TBK = 64 * WS<FMT>::BPL;
+    const long waves = ((long)L.rows + rpw - 1) / rpw;
+    if (waves < 4L * ws_num_cus() && 2L * (rpw / 2) * L.bpr >= TBK) rpw /= 2;
+  }
   WsArgs A{};
   A.w[0] = (const uint8_t*)L.w;
   A.y[0] = L.y;
