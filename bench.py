@@ -480,6 +480,7 @@ def measure_decode(fill=1024, n=128):
             "sampled_tok_s": round(n / sdt, 1),
             "step_stages_us": {"what": f"eager steps at KV {fill + min(n, 16)}.., HIP events after each stage, "
                                        "medians of 8 (the graph replay above runs the same kernels)", **stages},
+            "stage_gbs": stage_gbs(cfg, stages, fill + min(n, 16)),
             "top2_logit_gap": {"steps": len(gaps), "min": round(min(gaps), 6), "median": round(float(np.median(gaps)), 6),
                                "per_step": [round(g, 6) for g in gaps], "forward_tokens_match_generate": bool(same)},
             "prefill": {"tokens": int(fill), "chunks_of": 64, "seconds": round(pf_dt, 4),
@@ -502,6 +503,24 @@ def step_stages(m, token, steps=8):
 
 def kquant_bytes(dt, rows, cols):
     return rows * cols // 256 * (144 if dt == 2 else 210) if dt in (2, 3) else rows * cols // 32 * 34
+
+
+def stage_gbs(cfg, stages, kv_pos, dtypes=None, head_dtype=1):
+    """GB/s of each decode stage: the bytes it reads per token (weights of all
+    layers; attention: the K and V rows of kv_pos positions, f16) over its
+    eager microseconds (events between stages included, so a lower bound)."""
+    d, hd, L = cfg["dim"], cfg["head_dim"], cfg["n_layers"]
+    att, kv, ffn = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd, cfg["ffn_dim"]
+    dt = dtypes or {k: 1 for k in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")}
+    b = {"norm_qkv": L * (kquant_bytes(dt["wq"], att, d) + kquant_bytes(dt["wk"], kv, d) + kquant_bytes(dt["wv"], kv, d)),
+         "attention": L * kv_pos * kv * 2 * 2,
+         "o": L * kquant_bytes(dt["wo"], d, att),
+         "norm_gate_up_swiglu": L * (kquant_bytes(dt["w_gate"], ffn, d) + kquant_bytes(dt["w_up"], ffn, d)),
+         "down": L * kquant_bytes(dt["w_down"], d, ffn),
+         "head": kquant_bytes(head_dtype, cfg["vocab"], d)}
+    out = {k: round(v / (stages[k] * 1e-6) / 1e9, 1) for k, v in b.items() if stages.get(k)}
+    out["weights_and_kv"] = round(sum(b.values()) / (stages["sum"] * 1e-6) / 1e9, 1)
+    return out
 
 
 def measure_qwen3(fill=512, n=64):
@@ -553,6 +572,7 @@ def measure_qwen3(fill=512, n=64):
             "load_seconds": round(load_s, 3),
             "step_stages_us": {"what": f"eager steps at KV {fill + n}.., HIP events after each stage, medians of 8",
                                **stages},
+            "stage_gbs": stage_gbs(cfg, stages, fill + n, dtypes=QWEN3_DTYPES, head_dtype=3),
             "reference_host": {"decode_tok_s": "10.6-11.9", "prefill_batch64_tok_s": 20.7,
                                "source": "docs/benchmarks.md:63-64, docs/baseline-x86.md:144"}}
 
