@@ -407,10 +407,11 @@ __device__ __forceinline__ float wave_incl_scan_f32(float x) {
 
 __device__ __forceinline__ int f32_exp(float x) { return (int)((__float_as_uint(x) >> 23) & 0xffu) - 127; }
 
-// One pass of wave_chain_nonneg over a[0 .. m), m <= 64 * RL: s <- s + a[0] +
-// ... + a[m-1] exactly as the sequential f32 chain gives it. Returns false (s
-// unchanged) when the pass cannot vouch for its result; the caller then runs
-// the plain chain over the same terms.
+// One pass of wg_chain_nonneg over a[0 .. m), m <= 64 * NW * RL, run by all NW
+// waves of a workgroup with the same s: s <- s + a[0] + ... + a[m-1] exactly as
+// the sequential f32 chain gives it, the same value in every lane of every
+// wave. Returns false in every wave (s unchanged) when the pass cannot vouch
+// for its result; the caller then runs the plain chain over the same terms.
 //
 // While the running sum s is a normal float in one binade [2^E, 2^(E+1)), it is
 // a multiple of the binade's unit u = 2^(E-23), and so is every rounded s + a.
@@ -420,34 +421,46 @@ __device__ __forceinline__ int f32_exp(float x) { return (int)((__float_as_uint(
 // S = s / u, an integer in [2^23, 2^24], a run of terms in one binade is S plus
 // an integer prefix sum of the terms' roundings, exact in 32-bit integers.
 //
-// Lane l takes terms RL*l .. RL*l + RL-1. An approximate f32 prefix sum (its
-// association does not matter) predicts the binade each term is added in. Each
-// term is rounded with the unit of its predicted binade, except the terms after
-// which the predicted binade changes (crossings) and ties: those "special" terms
-// count 0 in the integer prefix sum and are added as ordinary f32 adds, in
-// order, by a chain that checks each prediction against the exact sum: each run
-// of terms between special ones must end below 2^(E+1) in the binade predicted
-// for it, and each special term must land in the binade predicted after it.
-// (The binade predicted before a special term is the one predicted after the
-// previous special term, or s's own for the first: lane 0 predicts from s
-// itself, and the predicted binade only changes at special terms.)
+// Lane g = 64 * wave + lane takes terms RL*g .. RL*g + RL-1. An approximate f32
+// prefix sum (its association does not matter) predicts the binade each term
+// is added in. Each term is rounded with the unit of its predicted binade,
+// except the terms after which the predicted binade changes (crossings) and
+// ties: those "special" terms count 0 in the integer prefix sum and are added
+// as ordinary f32 adds, in order, by a chain that checks each prediction
+// against the exact sum: each run of terms between special ones must end below
+// 2^(E+1) in the binade predicted for it, and each special term must land in
+// the binade predicted after it. (The binade predicted before a special term is
+// the one predicted after the previous special term, or s's own for the first:
+// lane 0 predicts from s itself, and the predicted binade only changes at
+// special terms. Across a wave boundary the last lane's prediction after its
+// last term and the next wave's first prediction are the same f32 value,
+// s + the waves' totals added in wave order by every wave alike.)
 // A term that is negative or not finite, and a sum outside [2^-100, 2^127),
 // fail the pass.
 //
-// The special terms' indices go to lanes 0, 1, ... in term order (a prefix sum
-// of the lanes' counts places them); one gather from work (the integer prefix
-// before each term and the binade predicted after it, which the pass writes)
-// and from a fetches their data. Only the f32 adds run one special term at a
-// time; every check runs on all of them at once afterwards.
-template <int RL>
-__device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, float& s, uint32_t* __restrict__ work) {
+// The waves exchange their f32 totals, then their integer totals and special
+// counts, through work; the lanes holding special terms write each one's
+// integer prefix, predicted binade after it and value to its place in term
+// order, and every wave then resolves the special terms alike: only their f32
+// adds run one at a time, every check runs on all of them at once afterwards.
+// work: kWgChainWork words of LDS that nothing else touches during the pass.
+constexpr int kWgMaxSpecial = 48;  // past this many, the plain chain is cheaper
+constexpr int kWgChainWork = 32 + 3 * kWgMaxSpecial;
+template <int NW, int RL>
+__device__ __forceinline__ bool wg_chain_pass(const float* __restrict__ a, int m, float& s, uint32_t* __restrict__ work) {
   static_assert(RL % 4 == 0, "whole 16-byte reads per lane");
-  constexpr int kMaxSpecial = 48;  // past this many, the plain chain is cheaper
+  static_assert(NW >= 1 && NW <= 8, "the exchange holds up to eight waves");
   const uint32_t sb = __builtin_amdgcn_readfirstlane(__float_as_uint(s));
   if (sb - 0x0d800000u >= 0x7f000000u - 0x0d800000u) return false;  // positive, biased exponent 27 .. 253
   const float s_in = __uint_as_float(sb);
   const int lane = threadIdx.x & 63;
-  const int base = RL * lane;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int base = RL * (64 * wave + lane);
+  uint32_t* xf = work;        // [wave]: the wave's f32 total; [8 + wave]: it holds a non-finite term
+  uint32_t* xr = work + 16;   // [wave]: the wave's integer total; [8 + wave]: its special count
+  uint32_t* spb = work + 32;  // special term k: the integer prefix before it,
+  uint32_t* spa = spb + kWgMaxSpecial;  // the binade predicted after it,
+  uint32_t* spt = spa + kWgMaxSpecial;  // the term
   float av[RL];
   const float4* a4 = (const float4*)a;
   const int last4 = (m >> 2) - 1;
@@ -467,20 +480,39 @@ __device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, f
     mx = max(mx, __float_as_uint(av[j]));
     tot = tot + av[j];
   }
-  if (__ballot(mx >= 0x7f800000u) != 0) return false;  // every term a finite float >= +0
-  const float inclF = wave_incl_scan_f32(tot);
-  const float exclF = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(inclF), 0x138, 0xf, 0xf, false));  // wave_shr:1
-  const float totF = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inclF), 63));
-  const float p0 = s_in + exclF;  // predicted sum before the lane's first term
-  uint32_t ef[RL + 1];            // exponent field of the predicted sum before term j
+  const bool nonfinite = __ballot(mx >= 0x7f800000u) != 0;  // every term a finite float >= +0
+  const float inclW = wave_incl_scan_f32(tot);
+  if (lane == 63) {
+    xf[wave] = __float_as_uint(inclW);
+    xf[8 + wave] = nonfinite ? 1u : 0u;
+  }
+  __syncthreads();
+  // the waves' totals before this wave and through it, added in wave order
+  float offW = 0.0f, offN = 0.0f;
+  bool bad_term = false;
+#pragma unroll
+  for (int i = 0; i < NW; i++) {
+    const float t = __uint_as_float(xf[i]);
+    bad_term |= xf[8 + i] != 0u;
+    if (i < wave) offW = offW + t;
+    if (i <= wave) offN = offN + t;
+  }
+  if (bad_term) {
+    __syncthreads();  // every wave has read xf before a next pass may write it again
+    return false;
+  }
+  const float exclW = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(inclW), 0x138, 0xf, 0xf, false));  // wave_shr:1
+  const float p0 = s_in + (offW + exclW);  // predicted sum before the lane's first term
+  uint32_t ef[RL + 1];                     // exponent field of the predicted sum before term j
   float p = p0;
 #pragma unroll
   for (int j = 0; j < RL; j++) {
     ef[j] = __float_as_uint(p) & 0x7f800000u;
     p = p + av[j];
   }
-  // after the lane's last term: the next lane's first prediction (wave_shl:1)
-  ef[RL] = (uint32_t)__builtin_amdgcn_update_dpp(__float_as_int(s_in + totF), __float_as_int(p0), 0x130, 0xf, 0xf, false) &
+  // after the lane's last term: the next lane's first prediction (wave_shl:1);
+  // the last lane's is the next wave's first, s + offN (s + the total after the last wave)
+  ef[RL] = (uint32_t)__builtin_amdgcn_update_dpp(__float_as_int(s_in + offN), __float_as_int(p0), 0x130, 0xf, 0xf, false) &
            0x7f800000u;
   uint32_t cum[RL], special = 0u, racc = 0u;  // cum[j]: the lane's roundings before term j
 #pragma unroll
@@ -495,47 +527,63 @@ __device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, f
     special |= (sp ? 1u : 0u) << j;
   }
   const uint32_t incl = wave_incl_scan_u32(racc);  // wraps harmlessly: only run differences are used
-  const uint32_t excl = incl - racc;
-  const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+  const uint32_t cnt = (uint32_t)__builtin_popcount(special);
+  const uint32_t cincl = wave_incl_scan_u32(cnt);
+  if (lane == 63) {
+    xr[wave] = incl;
+    xr[8 + wave] = cincl;
+  }
+  __syncthreads();
+  uint32_t offR = 0u, total = 0u, offC = 0u, K = 0u;
+#pragma unroll
+  for (int i = 0; i < NW; i++) {
+    const uint32_t r = xr[i], c = xr[8 + i];
+    if (i < wave) {
+      offR += r;
+      offC += c;
+    }
+    total += r;
+    K += c;
+  }
+  const uint32_t excl = offR + incl - racc;
   uint32_t Ef = sb & 0x7f800000u;  // exponent field of the exact running sum
   uint32_t bstart = 0u;            // the integer prefix where the current run starts
   uint32_t S = (sb & 0x7fffffu) | 0x800000u;
-  const uint32_t cnt = (uint32_t)__builtin_popcount(special);
-  const uint32_t cincl = wave_incl_scan_u32(cnt);
-  const int K = __builtin_amdgcn_readlane((int)cincl, 63);  // special terms in the pass
-  if (K != 0) {
-    if (K > kMaxSpecial) return false;
-    uint32_t* w_before = work;             // per term: the integer prefix before it
-    uint32_t* w_after = work + 64 * RL;    // per term: the binade predicted after it
-    uint32_t* w_index = work + 128 * RL;   // the special terms' indices, in order
+  if (K != 0u) {
+    if (K > (uint32_t)kWgMaxSpecial) return false;
+    // the lane's special terms, in order, to their places in term order
+    uint32_t rem = special, slot = offC + cincl - cnt;
+    while (rem != 0u) {
+      const int j = __builtin_ctz(rem);
+      uint32_t b = 0u, af = 0u, tb = 0u;
 #pragma unroll
-    for (int k = 0; k < RL / 4; k++) {
-      ((uint4*)(w_before + base))[k] = make_uint4(excl + cum[4 * k], excl + cum[4 * k + 1], excl + cum[4 * k + 2],
-                                                  excl + cum[4 * k + 3]);
-      ((uint4*)(w_after + base))[k] = make_uint4(ef[4 * k + 1], ef[4 * k + 2], ef[4 * k + 3], ef[4 * k + 4]);
-    }
-    uint32_t rem = special, slot = cincl - cnt;
-    while (__ballot(rem != 0u) != 0) {
-      if (rem != 0u) {
-        w_index[slot++] = (uint32_t)(base + __builtin_ctz(rem));
-        rem &= rem - 1u;
+      for (int jj = 0; jj < RL; jj++) {  // selects, not an indexed register read
+        b = jj == j ? cum[jj] : b;
+        af = jj == j ? ef[jj + 1] : af;
+        tb = jj == j ? __float_as_uint(av[jj]) : tb;
       }
+      spb[slot] = excl + b;
+      spa[slot] = af;
+      spt[slot] = tb;
+      slot++;
+      rem &= rem - 1u;
     }
-    const uint32_t idx = lane < K ? w_index[lane] : 0u;
-    const uint32_t g_before = w_before[idx], g_after = w_after[idx];
-    const float g_term = a[idx];
+    __syncthreads();
+    const uint32_t g_before = lane < (int)K ? spb[lane] : 0u;
+    const uint32_t g_after = lane < (int)K ? spa[lane] : 0u;
+    const float g_term = lane < (int)K ? __uint_as_float(spt[lane]) : 0.0f;
     // the previous special term's prefix and binade after (the pass start's in lane 0)
     uint32_t p_before = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)g_before, 0x138, 0xf, 0xf, false);
     const uint32_t p_after = (uint32_t)__builtin_amdgcn_update_dpp((int)Ef, (int)g_after, 0x138, 0xf, 0xf, false);
     // kept out of the subtraction: folded into it, as v_subrev_u32_dpp, the
     // shift gave the difference with the opposite sign on gfx950
     asm volatile("" : "+v"(p_before));
-    const uint32_t pre = g_before - p_before;  // the run before the special term
-    const float unit = __uint_as_float(p_after - (23u << 23));         // that run's unit
+    const uint32_t pre = g_before - p_before;                   // the run before the special term
+    const float unit = __uint_as_float(p_after - (23u << 23));  // that run's unit
     // S in a vector register: the chain below stays on the vector unit
     uint32_t Sv = S, nbv = 0u;
     asm volatile("" : "+v"(Sv));
-    for (int k = 0; k < K; k++) {
+    for (int k = 0; k < (int)K; k++) {
       const uint32_t X = Sv + (uint32_t)__builtin_amdgcn_readlane((int)pre, k);
       const float se = (float)X * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(unit), k));  // exact when X < 2^24
       const uint32_t nb = __float_as_uint(se + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g_term), k)));
@@ -545,8 +593,8 @@ __device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, f
     // lane k: the sum after special term k (nbv) and before it (S of the previous one, plus the run)
     const uint32_t p_nb = (uint32_t)__builtin_amdgcn_update_dpp((int)sb, (int)nbv, 0x138, 0xf, 0xf, false);
     const uint32_t X = ((p_nb & 0x7fffffu) | 0x800000u) + pre;
-    const bool bad = lane < K && ((pre >= (1u << 24)) | (X >= (1u << 24)) |
-                                  (nbv - 0x0d800000u >= 0x7f000000u - 0x0d800000u) | ((nbv & 0x7f800000u) != g_after));
+    const bool bad = lane < (int)K && ((pre >= (1u << 24)) | (X >= (1u << 24)) |
+                                       (nbv - 0x0d800000u >= 0x7f000000u - 0x0d800000u) | ((nbv & 0x7f800000u) != g_after));
     if (__ballot(bad) != 0) return false;
     S = __builtin_amdgcn_readfirstlane(Sv);
     Ef = (uint32_t)__builtin_amdgcn_readlane((int)g_after, K - 1);
@@ -558,33 +606,32 @@ __device__ __forceinline__ bool chain_pass(const float* __restrict__ a, int m, f
   return true;
 }
 
+__device__ __forceinline__ float wave_lane0_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
 // wave_chain_from's result, bit for bit, for terms that are finite and
-// nonnegative (squares), in fewer dependent steps: the first 128 terms, where
-// the sum crosses binades often, take the plain chain, then passes of 1024
-// terms (chain_pass) each fall back to the plain chain when they cannot vouch
-// for their result; a last run of fewer than 512 terms is cheaper on the plain
-// chain. A pass issues about four times the instructions of the plain chain
-// over the same terms, in a fraction of its time: it pays where the wave has
-// its SIMD to itself. Whole wave, a in LDS and 16-byte aligned, n a multiple of
-// 4; the result is valid in lane 0 (after a fallback or a short tail it comes
-// from wave_chain_from, whose other lanes hold partial sums); work is
-// kChainWork words of LDS that no other wave touches meanwhile (n < 640 needs
-// none).
-constexpr int kChainWork = 2 * 1024 + 64;
-__device__ __forceinline__ float wave_chain_nonneg(const float* __restrict__ a, int n, float s, uint32_t* __restrict__ work) {
-  constexpr int RL = 16, P = 64 * RL;
-  static_assert(2 * P + 64 == kChainWork, "the pass records two words per term and one per lane");
-  if (n < 128 + 512) return wave_chain_from(a, n, s);
-  s = wave_chain_from(a, 128, s);
+// nonnegative (squares), computed by all NW waves of a workgroup together and
+// returned in every lane of every wave: the first 128 terms, where the sum
+// crosses binades often, take the plain chain in every wave alike, then passes
+// of up to 64 * NW * 16 terms (wg_chain_pass, 8 terms per lane when that
+// covers them) each fall back to the plain chain when they cannot vouch for
+// their result; a last run of fewer than 512 terms is cheaper on the plain
+// chain. Every thread of the workgroup calls it with the same arguments (a in
+// LDS, 16-byte aligned, n a multiple of 4); work is kWgChainWork words of LDS
+// that nothing else touches meanwhile.
+template <int NW>
+__device__ __forceinline__ float wg_chain_nonneg(const float* __restrict__ a, int n, float s, uint32_t* __restrict__ work) {
+  if (n < 128 + 512) return wave_lane0_f32(wave_chain_from(a, n, s));
+  s = wave_lane0_f32(wave_chain_from(a, 128, s));
   int i = 128;
-  // whole passes: a constant count, so the tail's masking folds away here
-  for (; i + P <= n; i += P)
-    if (!chain_pass<RL>(a + i, P, s, work)) s = wave_chain_from(a + i, P, s);
-  if (n - i >= 512) {
-    if (!chain_pass<RL>(a + i, n - i, s, work)) s = wave_chain_from(a + i, n - i, s);
-  } else if (n > i) {
-    s = wave_chain_from(a + i, n - i, s);
+  while (n - i >= 512) {
+    const int m = min(n - i, 64 * NW * 16);
+    const bool ok = m <= 64 * NW * 8 ? wg_chain_pass<NW, 8>(a + i, m, s, work) : wg_chain_pass<NW, 16>(a + i, m, s, work);
+    if (!ok) s = wave_lane0_f32(wave_chain_from(a + i, m, s));
+    i += m;
   }
+  if (n > i) s = wave_lane0_f32(wave_chain_from(a + i, n - i, s));
   return s;
 }
 

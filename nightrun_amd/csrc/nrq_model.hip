@@ -258,7 +258,7 @@ constexpr int kNormPT = kNormMax / kNormNT;  // values per thread
 // workgroup; n <= kNormMax, a multiple of 256. Thread t owns the 8-value runs
 // t + 256k (four consecutive runs, an aligned lane quad, make one Q8_0 block;
 // 32, an aligned half-wave, one Q8_K block), loaded once, all loads issued
-// before the first use; wave 0 runs the sequential sum of squares. Workgroup r
+// before the first use; the four waves run the ordered sum of squares together. Workgroup r
 // takes row r of [rows][n] x, add, out, xq and xqk (one row per workgroup in a
 // prefill chunk).
 __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, const float* __restrict__ add,
@@ -266,7 +266,7 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
                                                        float* __restrict__ out, uint8_t* __restrict__ xq,
                                                        uint8_t* __restrict__ xqk) {
   __shared__ __align__(16) float sq[kNormMax];
-  __shared__ __align__(16) uint32_t chain_work[kChainWork];
+  __shared__ __align__(16) uint32_t chain_work[kWgChainWork];
   {
     const size_t r = blockIdx.x;
     x += r * n;
@@ -275,7 +275,6 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
     if (xq) xq += r * (size_t)(n / 32) * kQ8_0Bytes;
     if (xqk) xqk += r * (size_t)(n / 256) * kQ8KBytes;
   }
-  __shared__ float s_scale;
   const int tid = threadIdx.x;
   const int nrun = n >> 3;
   constexpr int RK = kNormPT / 8;  // runs per thread
@@ -314,12 +313,8 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
     }
   }
   __syncthreads();
-  if (tid < 64) {
-    const float ss = wave_chain_nonneg(sq, n, 0.0f, chain_work);
-    if (tid == 0) s_scale = 1.0f / sqrtf(ss / (float)n + eps);
-  }
-  __syncthreads();
-  const float scale = s_scale;
+  const float ss = wg_chain_nonneg<kNormNT / 64>(sq, n, 0.0f, chain_work);  // every wave, the same result
+  const float scale = 1.0f / sqrtf(ss / (float)n + eps);
 #pragma unroll
   for (int k = 0; k < RK; k++) {
     const int j = tid + kNormNT * k;

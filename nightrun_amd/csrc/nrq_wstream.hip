@@ -344,10 +344,10 @@ constexpr int kFusedNormMax = 4096;
 constexpr int kFusedNormPT = kFusedNormMax / 256;
 
 // Fused-norm LDS, n floats per array: x (then its squares, in place) | norm
-// weight | add | pad | scale. The add array and the pad are the ordered sum's
-// workspace (kChainWork words) once the squares exist.
-__host__ __device__ inline int ws_norm_pad(int n) { return n < kChainWork ? (kChainWork - n + 3) & ~3 : 0; }
-__host__ __device__ inline size_t ws_norm_floats(int n) { return 3 * (size_t)n + ws_norm_pad(n) + 4; }
+// weight | add. The add array (n >= 256 words) is the ordered sum's workspace
+// (kWgChainWork words) once the squares exist.
+static_assert(kWgChainWork <= 256, "the workspace fits the smallest add array");
+__host__ __device__ inline size_t ws_norm_floats(int n) { return 3 * (size_t)n; }
 
 __device__ __forceinline__ void ws_dma16_g(const void* g, uint32_t m0) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(g) : "memory");
@@ -494,15 +494,10 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
       }
     }
     ws_lds_barrier();
-    float* scale_slot = nxs + 3 * (size_t)n + ws_norm_pad(n);
-    if (wave == 0) {
-      // the add array and the pad (at least kChainWork words) are dead here: the pass workspace
-      const float ss = n >= kChainWork / 2 ? wave_chain_nonneg(sq, n, 0.0f, (uint32_t*)(nxs + 2 * (size_t)n))
-                                           : wave_chain_from(sq, n, 0.0f);
-      if (lane == 0) scale_slot[0] = 1.0f / sqrtf(ss / (float)n + A.eps);
-    }
-    ws_lds_barrier();
-    const float scale = scale_slot[0];
+    // every wave takes part in the ordered sum and gets its result; the add
+    // array is dead here: the sum's workspace
+    const float ss = wg_chain_nonneg<NW>(sq, n, 0.0f, (uint32_t*)(nxs + 2 * (size_t)n));
+    const float scale = 1.0f / sqrtf(ss / (float)n + A.eps);
 #pragma unroll
     for (int k = 0; k < kFusedNormPT / 8; k++) {
       const int j = tid + NT * k;

@@ -1,23 +1,24 @@
-"""The wave-parallel exact sum behind the decode norms (chain_pass and
-wave_chain_nonneg in nightrun_amd/csrc/nrq_device.h), restated lane for lane
+"""The workgroup-parallel exact sum behind the decode norms (wg_chain_pass and
+wg_chain_nonneg in nightrun_amd/csrc/nrq_device.h), restated lane for lane
 in numpy float32 and checked bit-exact against the sequential f32 chain, the
 reference's `ss += v * v` loop (crates/nr-tensor/src/vec.rs:4-14).
 
-The restatement follows the device code: 64 lanes of 16 consecutive terms, an
-f32 prediction of each term's binade, terms rounded to the unit of their
-predicted binade, special terms (binade crossings, ties) resolved in order by
-plain f32 adds, and every check that makes a pass fall back to the plain
-chain (more than 48 special terms in one pass among them). The cases are built
-to reach each of those checks; the fast path must also be the one taken on
-ordinary rows, or the device code would only ever run its fallback. On the
+The restatement follows the device code: four waves of 64 lanes, 8 or 16
+consecutive terms per lane, an f32 prediction of each term's binade (wave
+totals added in wave order across the waves), terms rounded to the unit of
+their predicted binade, special terms (binade crossings, ties) resolved in
+order by plain f32 adds, and every check that makes a pass fall back to the
+plain chain (more than 48 special terms in one pass among them). The cases are
+built to reach each of those checks; the fast path must also be the one taken
+on ordinary rows, or the device code would only ever run its fallback. On the
 GPU, tests/test_gpu_rmsnorm.py runs the kernel itself."""
 import numpy as np
 import pytest
 
 F32 = np.float32
 U32 = np.uint32
-RL = 16
-P = 64 * RL
+NW = 4  # waves of the norm kernels' workgroups
+MAX_SPECIAL = 48
 
 
 def bits(x):
@@ -36,37 +37,45 @@ def serial(a, s):
     return s
 
 
-def chain_pass(a, s):
-    """(ok, s + a[0] + ... + a[m-1]) for m = len(a) <= 1024, as chain_pass<16>."""
+def chain_pass(a, s, rl):
+    """(ok, s + a[0] + ... + a[m-1]) for m = len(a) <= 64 * NW * rl, as wg_chain_pass<NW, rl>."""
     m = len(a)
+    lanes = 64 * NW
+    assert m <= lanes * rl
     sb = int(bits(s))
     if not (0x0D800000 <= sb < 0x7F000000):
         return False, s
-    av = np.zeros(P, F32)
+    av = np.zeros(lanes * rl, F32)
     av[:m] = a
-    av = av.reshape(64, RL)
+    av = av.reshape(lanes, rl)
     if int(bits(av).max()) >= 0x7F800000:
         return False, s
-    tot = np.zeros(64, F32)
-    for j in range(RL):
+    tot = np.zeros(lanes, F32)
+    for j in range(rl):
         tot = (tot + av[:, j]).astype(F32)
-    incl_f = np.cumsum(tot, dtype=F32)  # any association: a prediction
-    excl_f = np.concatenate([[F32(0)], incl_f[:-1]]).astype(F32)
-    p0 = (F32(s) + excl_f).astype(F32)
-    ef = np.zeros((64, RL + 1), U32)
+    # in-wave scans (any association: a prediction), wave totals added in wave order
+    incl_w = np.concatenate([np.cumsum(tot[64 * w:64 * w + 64], dtype=F32) for w in range(NW)]).astype(F32)
+    excl_w = np.concatenate([np.concatenate([[F32(0)], incl_w[64 * w:64 * w + 63]]) for w in range(NW)]).astype(F32)
+    off = [F32(0)]
+    for w in range(NW):
+        off.append(F32(off[-1] + incl_w[64 * w + 63]))
+    p0 = np.array([F32(F32(s) + F32(off[g // 64] + excl_w[g])) for g in range(lanes)], F32)
+    ef = np.zeros((lanes, rl + 1), U32)
     p = p0.copy()
-    for j in range(RL):
+    for j in range(rl):
         ef[:, j] = bits(p) & 0x7F800000
         p = (p + av[:, j]).astype(F32)
-    ef[:63, RL] = bits(p0[1:]) & 0x7F800000
-    ef[63, RL] = int(bits(F32(s) + incl_f[-1])) & 0x7F800000
-    inv_u = f32((0x8A800000 - ef[:, :RL].astype(np.int64)).astype(U32))
+    ef[:lanes - 1, rl] = bits(p0[1:]) & 0x7F800000
+    for w in range(NW):  # a wave's last lane: the next wave's first prediction
+        ef[64 * w + 63, rl] = int(bits(F32(F32(s) + off[w + 1]))) & 0x7F800000
+    assert all(ef[64 * w + 63, rl] == ef[64 * w + 64, 0] for w in range(NW - 1))
+    inv_u = f32((0x8A800000 - ef[:, :rl].astype(np.int64)).astype(U32))
     with np.errstate(over="ignore", invalid="ignore"):
         q = (av * inv_u).astype(F32)
         r = np.rint(np.clip(q, 0, 4294967040)).astype(np.uint64).astype(U32)
         frac = (q - np.floor(q)).astype(F32)
-    sp = (ef[:, :RL] != ef[:, 1:]) | (frac == F32(0.5))
-    sp[(np.arange(64)[:, None] * RL + np.arange(RL)[None, :]) >= m] = False  # only real terms (as the device code)
+    sp = (ef[:, :rl] != ef[:, 1:]) | (frac == F32(0.5))
+    sp[(np.arange(lanes)[:, None] * rl + np.arange(rl)[None, :]) >= m] = False  # only real terms (as the device code)
     r = np.where(sp, U32(0), r)
     racc = np.sum(r, axis=1, dtype=U32)
     cum = (np.cumsum(r, axis=1, dtype=U32) - r).astype(U32)  # before term j
@@ -77,7 +86,7 @@ def chain_pass(a, s):
     Ef = sb & 0x7F800000
     bstart = 0
     specials = list(zip(*np.nonzero(sp)))  # lane-major, term order within a lane
-    if len(specials) > 48:  # the plain chain is cheaper than more special terms
+    if len(specials) > MAX_SPECIAL:  # the plain chain is cheaper than more special terms
         return False, s
     # the binade predicted before each special term is the one predicted after
     # the previous (s's own for the first): the device code relies on it
@@ -89,7 +98,7 @@ def chain_pass(a, s):
         pre = (before - bstart) & 0xFFFFFFFF
         X = S + pre
         se = F32(F32(X & 0xFFFFFFFF) * f32((Ef - (23 << 23)) & 0xFFFFFFFF))
-        nb = int(bits(F32(se + F32(a[RL * L + J]))))
+        nb = int(bits(F32(se + F32(a[rl * L + J]))))
         ok &= pre < 1 << 24 and X < 1 << 24 and 0x0D800000 <= nb < 0x7F000000 and (nb & 0x7F800000) == int(ef[L, J + 1])
         Ef = int(ef[L, J + 1])
         S = (nb & 0x7FFFFF) | 0x800000
@@ -103,8 +112,9 @@ def chain_pass(a, s):
 
 
 def chain_nonneg(a, s, stats=None):
-    """wave_chain_nonneg: 128 plain terms, then passes of up to 1024 terms while
-    at least 512 remain, then the plain chain."""
+    """wg_chain_nonneg<4>: 128 plain terms, then passes of up to 4096 terms (8
+    per lane when 2048 cover them, else 16) while at least 512 remain, then the
+    plain chain."""
     a = np.asarray(a, F32)
     n = len(a)
     if n < 128 + 512:
@@ -112,8 +122,8 @@ def chain_nonneg(a, s, stats=None):
     s = serial(a[:128], s)
     i = 128
     while n - i >= 512:
-        m = min(P, n - i)
-        ok, out = chain_pass(a[i:i + m], s)
+        m = min(64 * NW * 16, n - i)
+        ok, out = chain_pass(a[i:i + m], s, 8 if m <= 64 * NW * 8 else 16)
         if stats is not None:
             stats.append(ok)
         s = out if ok else serial(a[i:i + m], s)
@@ -170,7 +180,7 @@ def same(x, y):
 def test_chain_matches_sequential_sum(kind):
     rng = np.random.default_rng(KINDS.index(kind))
     for t in range(8):
-        n = int(rng.choice([640, 1100, 2048, 2560, 4096, 5000]))
+        n = int(rng.choice([640, 1100, 2048, 2176, 2560, 4096, 5000, 8192]))
         a = family(kind, n, rng)
         s0 = F32(1 << 24) if kind == "ones_past_2p24" else (F32(rng.random() * 10) if t % 3 == 0 else F32(0))
         want = F32(np.add.accumulate(np.concatenate([[s0], a]).astype(F32), dtype=F32)[-1])
@@ -186,7 +196,7 @@ def test_ordinary_rows_take_the_fast_path():
         for _ in range(6):
             x = rng.standard_normal(n).astype(F32)
             chain_nonneg((x * x).astype(F32), F32(0), stats)
-    assert len(stats) >= 30 and all(stats), f"{stats.count(False)} of {len(stats)} passes fell back"
+    assert len(stats) == 18 and all(stats), f"{stats.count(False)} of {len(stats)} passes fell back"  # one pass per row
 
 
 def test_a_planted_rounding_slip_is_caught():

@@ -64,7 +64,7 @@ def rows_for(n, rng):
     return out
 
 
-@pytest.mark.parametrize("n", [256, 512, 2048, 2560, 4096, 8192])
+@pytest.mark.parametrize("n", [256, 512, 768, 2048, 2560, 4096, 6144, 8192])
 def test_rmsnorm_bitexact_on_hard_rows(gpu, oracle, n):
     import torch
 
