@@ -445,46 +445,56 @@ __device__ __forceinline__ int f32_exp(float x) { return (int)((__float_as_uint(
 // adds run one at a time, every check runs on all of them at once afterwards.
 // work: kWgChainWork words of LDS that nothing else touches during the pass.
 constexpr int kWgMaxSpecial = 48;  // past this many, the plain chain is cheaper
-constexpr int kWgChainWork = 32 + 3 * kWgMaxSpecial;
+constexpr int kWgChainWork = 64 + 3 * kWgMaxSpecial;
 template <int NW, int RL>
 __device__ __forceinline__ bool wg_chain_pass(const float* __restrict__ a, int m, float& s, uint32_t* __restrict__ work) {
   static_assert(RL % 4 == 0, "whole 16-byte reads per lane");
-  static_assert(NW >= 1 && NW <= 8, "the exchange holds up to eight waves");
+  static_assert(NW >= 1 && NW <= 16, "the exchange holds up to sixteen waves");
   const uint32_t sb = __builtin_amdgcn_readfirstlane(__float_as_uint(s));
   if (sb - 0x0d800000u >= 0x7f000000u - 0x0d800000u) return false;  // positive, biased exponent 27 .. 253
   const float s_in = __uint_as_float(sb);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int base = RL * (64 * wave + lane);
-  uint32_t* xf = work;        // [wave]: the wave's f32 total; [8 + wave]: it holds a non-finite term
-  uint32_t* xr = work + 16;   // [wave]: the wave's integer total; [8 + wave]: its special count
-  uint32_t* spb = work + 32;  // special term k: the integer prefix before it,
+  uint32_t* xf = work;        // [wave]: the wave's f32 total; [16 + wave]: it holds a non-finite term
+  uint32_t* xr = work + 32;   // [wave]: the wave's integer total; [16 + wave]: its special count
+  uint32_t* spb = work + 64;  // special term k: the integer prefix before it,
   uint32_t* spa = spb + kWgMaxSpecial;  // the binade predicted after it,
   uint32_t* spt = spa + kWgMaxSpecial;  // the term
+  // a wave past the last term (its lanes would hold only zeros) skips the
+  // per-term work and takes part in the exchanges with zero totals
+  const bool busy = RL * 64 * wave < m;
   float av[RL];
-  const float4* a4 = (const float4*)a;
-  const int last4 = (m >> 2) - 1;
+  float inclW = 0.0f;
+  bool nonfinite = false;
+  if (busy) {
+    const float4* a4 = (const float4*)a;
+    const int last4 = (m >> 2) - 1;
 #pragma unroll
-  for (int k = 0; k < RL / 4; k++) {
-    const float4 v = a4[min(base / 4 + k, last4)];
-    av[4 * k] = v.x;
-    av[4 * k + 1] = v.y;
-    av[4 * k + 2] = v.z;
-    av[4 * k + 3] = v.w;
-  }
-  uint32_t mx = 0u;
-  float tot = 0.0f;
+    for (int k = 0; k < RL / 4; k++) {
+      const float4 v = a4[min(base / 4 + k, last4)];
+      av[4 * k] = v.x;
+      av[4 * k + 1] = v.y;
+      av[4 * k + 2] = v.z;
+      av[4 * k + 3] = v.w;
+    }
+    uint32_t mx = 0u;
+    float tot = 0.0f;
 #pragma unroll
-  for (int j = 0; j < RL; j++) {
-    av[j] = base + j < m ? av[j] : 0.0f;
-    mx = max(mx, __float_as_uint(av[j]));
-    tot = tot + av[j];
+    for (int j = 0; j < RL; j++) {
+      av[j] = base + j < m ? av[j] : 0.0f;
+      mx = max(mx, __float_as_uint(av[j]));
+      tot = tot + av[j];
+    }
+    nonfinite = __ballot(mx >= 0x7f800000u) != 0;  // every term a finite float >= +0
+    inclW = wave_incl_scan_f32(tot);
+  } else {
+#pragma unroll
+    for (int j = 0; j < RL; j++) av[j] = 0.0f;
   }
-  const bool nonfinite = __ballot(mx >= 0x7f800000u) != 0;  // every term a finite float >= +0
-  const float inclW = wave_incl_scan_f32(tot);
   if (lane == 63) {
     xf[wave] = __float_as_uint(inclW);
-    xf[8 + wave] = nonfinite ? 1u : 0u;
+    xf[16 + wave] = nonfinite ? 1u : 0u;
   }
   __syncthreads();
   // the waves' totals before this wave and through it, added in wave order
@@ -493,7 +503,7 @@ __device__ __forceinline__ bool wg_chain_pass(const float* __restrict__ a, int m
 #pragma unroll
   for (int i = 0; i < NW; i++) {
     const float t = __uint_as_float(xf[i]);
-    bad_term |= xf[8 + i] != 0u;
+    bad_term |= xf[16 + i] != 0u;
     if (i < wave) offW = offW + t;
     if (i <= wave) offN = offN + t;
   }
@@ -501,43 +511,52 @@ __device__ __forceinline__ bool wg_chain_pass(const float* __restrict__ a, int m
     __syncthreads();  // every wave has read xf before a next pass may write it again
     return false;
   }
-  const float exclW = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(inclW), 0x138, 0xf, 0xf, false));  // wave_shr:1
-  const float p0 = s_in + (offW + exclW);  // predicted sum before the lane's first term
-  uint32_t ef[RL + 1];                     // exponent field of the predicted sum before term j
-  float p = p0;
+  uint32_t ef[RL + 1];  // exponent field of the predicted sum before term j
+  uint32_t cum[RL], special = 0u, racc = 0u, incl = 0u, cnt = 0u, cincl = 0u;  // cum[j]: the lane's roundings before term j
+  if (busy) {
+    const float exclW = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(inclW), 0x138, 0xf, 0xf, false));  // wave_shr:1
+    const float p0 = s_in + (offW + exclW);  // predicted sum before the lane's first term
+    float p = p0;
 #pragma unroll
-  for (int j = 0; j < RL; j++) {
-    ef[j] = __float_as_uint(p) & 0x7f800000u;
-    p = p + av[j];
-  }
-  // after the lane's last term: the next lane's first prediction (wave_shl:1);
-  // the last lane's is the next wave's first, s + offN (s + the total after the last wave)
-  ef[RL] = (uint32_t)__builtin_amdgcn_update_dpp(__float_as_int(s_in + offN), __float_as_int(p0), 0x130, 0xf, 0xf, false) &
-           0x7f800000u;
-  uint32_t cum[RL], special = 0u, racc = 0u;  // cum[j]: the lane's roundings before term j
+    for (int j = 0; j < RL; j++) {
+      ef[j] = __float_as_uint(p) & 0x7f800000u;
+      p = p + av[j];
+    }
+    // after the lane's last term: the next lane's first prediction (wave_shl:1);
+    // the last lane's is the next wave's first, s + offN (s + the total after the last wave)
+    ef[RL] = (uint32_t)__builtin_amdgcn_update_dpp(__float_as_int(s_in + offN), __float_as_int(p0), 0x130, 0xf, 0xf, false) &
+             0x7f800000u;
 #pragma unroll
-  for (int j = 0; j < RL; j++) {
-    const float q = av[j] * __uint_as_float(0x8a800000u - ef[j]);  // a / u: a power-of-two scaling
-    const uint32_t r = (uint32_t)__builtin_rintf(q);
-    // only real terms are special: the zeros past m add nothing, and a zero in a
-    // lane's last slot may sit between two predictions made in different orders
-    const bool sp = base + j < m && (ef[j] != ef[j + 1] || __builtin_amdgcn_fractf(q) == 0.5f);
-    cum[j] = racc;
-    racc += sp ? 0u : r;  // r <= 2^24, so the lane's sum stays below 2^28
-    special |= (sp ? 1u : 0u) << j;
+    for (int j = 0; j < RL; j++) {
+      const float q = av[j] * __uint_as_float(0x8a800000u - ef[j]);  // a / u: a power-of-two scaling
+      const uint32_t r = (uint32_t)__builtin_rintf(q);
+      // only real terms are special: the zeros past m add nothing, and a zero in a
+      // lane's last slot may sit between two predictions made in different orders
+      const bool sp = base + j < m && (ef[j] != ef[j + 1] || __builtin_amdgcn_fractf(q) == 0.5f);
+      cum[j] = racc;
+      racc += sp ? 0u : r;  // r <= 2^24, so the lane's sum stays below 2^28
+      special |= (sp ? 1u : 0u) << j;
+    }
+    incl = wave_incl_scan_u32(racc);  // wraps harmlessly: only run differences are used
+    cnt = (uint32_t)__builtin_popcount(special);
+    cincl = wave_incl_scan_u32(cnt);
+  } else {
+#pragma unroll
+    for (int j = 0; j < RL; j++) {
+      ef[j] = 0u;
+      cum[j] = 0u;
+    }
+    ef[RL] = 0u;
   }
-  const uint32_t incl = wave_incl_scan_u32(racc);  // wraps harmlessly: only run differences are used
-  const uint32_t cnt = (uint32_t)__builtin_popcount(special);
-  const uint32_t cincl = wave_incl_scan_u32(cnt);
   if (lane == 63) {
     xr[wave] = incl;
-    xr[8 + wave] = cincl;
+    xr[16 + wave] = cincl;
   }
   __syncthreads();
   uint32_t offR = 0u, total = 0u, offC = 0u, K = 0u;
 #pragma unroll
   for (int i = 0; i < NW; i++) {
-    const uint32_t r = xr[i], c = xr[8 + i];
+    const uint32_t r = xr[i], c = xr[16 + i];
     if (i < wave) {
       offR += r;
       offC += c;
@@ -611,27 +630,43 @@ __device__ __forceinline__ float wave_lane0_f32(float v) {
 }
 
 // wave_chain_from's result, bit for bit, for terms that are finite and
-// nonnegative (squares), computed by all NW waves of a workgroup together and
-// returned in every lane of every wave: the first 128 terms, where the sum
+// nonnegative (squares, exps), computed by all NW waves of a workgroup together
+// and returned in every lane of every wave: the first 128 terms, where the sum
 // crosses binades often, take the plain chain in every wave alike, then passes
-// of up to 64 * NW * 16 terms (wg_chain_pass, 8 terms per lane when that
-// covers them) each fall back to the plain chain when they cannot vouch for
-// their result; a last run of fewer than 512 terms is cheaper on the plain
+// of up to 64 * NW * MAXRL terms (wg_chain_pass, 4 or 8 terms per lane when
+// that covers them) each fall back to the plain chain when they cannot vouch
+// for their result; a last run of fewer than 512 terms is cheaper on the plain
 // chain. Every thread of the workgroup calls it with the same arguments (a in
 // LDS, 16-byte aligned, n a multiple of 4); work is kWgChainWork words of LDS
-// that nothing else touches meanwhile.
-template <int NW>
+// that nothing else touches meanwhile. Every wave has finished reading a when
+// any wave returns, so a may be written right after the call.
+template <int NW, int MAXRL = 16>
 __device__ __forceinline__ float wg_chain_nonneg(const float* __restrict__ a, int n, float s, uint32_t* __restrict__ work) {
-  if (n < 128 + 512) return wave_lane0_f32(wave_chain_from(a, n, s));
-  s = wave_lane0_f32(wave_chain_from(a, 128, s));
-  int i = 128;
-  while (n - i >= 512) {
-    const int m = min(n - i, 64 * NW * 16);
-    const bool ok = m <= 64 * NW * 8 ? wg_chain_pass<NW, 8>(a + i, m, s, work) : wg_chain_pass<NW, 16>(a + i, m, s, work);
-    if (!ok) s = wave_lane0_f32(wave_chain_from(a + i, m, s));
-    i += m;
+  static_assert(MAXRL == 4 || MAXRL == 8 || MAXRL == 16, "4, 8 or 16 terms per lane");
+  // a plain chain read a after the last barrier of a successful pass (the
+  // decisions below are the same in every wave, so the barrier is reached by all)
+  bool plain_after = true;
+  if (n < 128 + 512) {
+    s = wave_lane0_f32(wave_chain_from(a, n, s));
+  } else {
+    s = wave_lane0_f32(wave_chain_from(a, 128, s));
+    int i = 128;
+    while (n - i >= 512) {
+      const int m = min(n - i, 64 * NW * MAXRL);
+      bool ok;
+      if (MAXRL == 4 || m <= 64 * NW * 4) ok = wg_chain_pass<NW, 4>(a + i, m, s, work);
+      else if (MAXRL == 8 || m <= 64 * NW * 8) ok = wg_chain_pass<NW, MAXRL == 4 ? 4 : 8>(a + i, m, s, work);
+      else ok = wg_chain_pass<NW, MAXRL>(a + i, m, s, work);
+      if (!ok) s = wave_lane0_f32(wave_chain_from(a + i, m, s));
+      plain_after = !ok;
+      i += m;
+    }
+    if (n > i) {
+      s = wave_lane0_f32(wave_chain_from(a + i, n - i, s));
+      plain_after = true;
+    }
   }
-  if (n > i) s = wave_lane0_f32(wave_chain_from(a + i, n - i, s));
+  if (plain_after) __syncthreads();
   return s;
 }
 
