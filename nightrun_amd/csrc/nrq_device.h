@@ -95,39 +95,42 @@ __device__ __forceinline__ void q6k_planes(uint32_t qlA, uint32_t qlB, uint32_t 
   q6[3] = ((qlB >> 4) & m4) | ((qh >> 2) & m2h);
 }
 
-// f16.rs:25-56
+// f16.rs:25-56: round to nearest even for normal results, round half up
+// for subnormal ones, a quiet NaN without payload. Every case is formed and
+// the result picked by selects: no divergent branches.
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float v) {
-  uint32_t bits = __float_as_uint(v);
-  uint32_t sign = (bits >> 31) << 15;
-  int exp = (int)((bits >> 23) & 0xffu);
-  uint32_t frac = bits & 0x7fffffu;
-  if (exp == 0xff) return sign | 0x7c00u | (frac != 0 ? 0x200u : 0u);
-  int e = exp - 127 + 15;
-  if (e >= 0x1f) return sign | 0x7c00u;
-  if (e <= 0) {
-    if (e < -10) return sign;
-    uint32_t f = frac | 0x800000u;
-    uint32_t shift = (uint32_t)(14 - e);
-    uint32_t half = 1u << (shift - 1);
-    return (sign | ((f + half) >> shift)) & 0xffffu;
-  }
-  uint32_t out = sign | ((uint32_t)e << 10) | (frac >> 13);
-  uint32_t round = frac & 0x1fffu;
-  if (round > 0x1000u || (round == 0x1000u && (out & 1u) != 0)) out += 1;
+  const uint32_t bits = __float_as_uint(v);
+  const uint32_t sign = (bits >> 16) & 0x8000u;
+  const int exp = (int)((bits >> 23) & 0xffu);
+  const uint32_t frac = bits & 0x7fffffu;
+  const int e = exp - 127 + 15;
+  // e in 1 .. 30: the top ten fraction bits, then the 13 dropped ones round
+  uint32_t nrm = sign | ((uint32_t)e << 10) | (frac >> 13);
+  const uint32_t rnd = frac & 0x1fffu;
+  nrm += (rnd > 0x1000u || (rnd == 0x1000u && (nrm & 1u) != 0)) ? 1u : 0u;
+  // e in -10 .. 0: the significand shifted right by 14 - e, half up
+  const uint32_t sh = (uint32_t)min(max(14 - e, 14), 24);
+  const uint32_t sub = sign | (((frac | 0x800000u) + (1u << (sh - 1))) >> sh);
+  // e >= 31: infinity, or a quiet NaN for exp 0xff with a nonzero fraction
+  const uint32_t big = sign | 0x7c00u | (exp == 0xff && frac != 0 ? 0x200u : 0u);
+  uint32_t out = e <= 0 ? (e < -10 ? sign : sub) : nrm;
+  out = e >= 0x1f ? big : out;
   return out & 0xffffu;
 }
 
-// Rust `f as i32`: truncate, saturate, NaN -> 0.
+// Rust `f as i32`: truncate toward zero, saturate to [i32::MIN, i32::MAX],
+// NaN -> 0. That is what v_cvt_i32_f32 does; checked against the three-way
+// restatement of those rules on all 2^32 f32 inputs on gfx950.
 __device__ __forceinline__ int rust_f32_to_i32(float f) {
-  if (f != f) return 0;
-  if (f >= 2147483648.0f) return 2147483647;
-  if (f <= -2147483648.0f) return (-2147483647 - 1);
-  return (int)f;
+  int r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(f));
+  return r;
 }
 
-// kquant.rs:145-153
+// kquant.rs:145-153 (the two sums formed, one picked: no branch)
 __device__ __forceinline__ int nearest_int(float v) {
-  return v >= 0.0f ? rust_f32_to_i32(v + 0.5f) : rust_f32_to_i32(v - 0.5f);
+  const float up = v + 0.5f, down = v - 0.5f;
+  return rust_f32_to_i32(v >= 0.0f ? up : down);
 }
 
 // One Q8_K block (kquant.rs:157-187) from 32 lanes of a half-wave, lane r
