@@ -632,34 +632,51 @@ __device__ __forceinline__ float wave_lane0_f32(float v) {
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
 
+// s + a[0] + a[1] + a[2] + ... + a[15] in index order (a 16-byte aligned),
+// the same value in every lane
+__device__ __forceinline__ float chain_head16(const float* __restrict__ a, float s) {
+  const float4* a4 = (const float4*)a;
+  const float4 v0 = a4[0], v1 = a4[1], v2 = a4[2], v3 = a4[3];
+  const float4 v[4] = {v0, v1, v2, v3};
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    s = s + v[k].x;
+    s = s + v[k].y;
+    s = s + v[k].z;
+    s = s + v[k].w;
+  }
+  return s;
+}
+
 // wave_chain_from's result, bit for bit, for terms that are finite and
 // nonnegative (squares, exps), computed by all NW waves of a workgroup together
-// and returned in every lane of every wave: the first 128 terms, where the sum
-// crosses binades often, take the plain chain in every wave alike, then passes
-// of up to 64 * NW * MAXRL terms (wg_chain_pass, 4 or 8 terms per lane when
-// that covers them) each fall back to the plain chain when they cannot vouch
-// for their result; a last run of fewer than 512 terms is cheaper on the plain
-// chain. Every thread of the workgroup calls it with the same arguments (a in
-// LDS, 16-byte aligned, n a multiple of 4); work is kWgChainWork words of LDS
-// that nothing else touches meanwhile. Every wave has finished reading a when
-// any wave returns, so a may be written right after the call.
+// and returned in every lane of every wave: the first 16 terms take the plain
+// chain in every lane alike (the pass needs a positive running sum to start
+// from), then passes of up to 64 * NW * MAXRL terms (wg_chain_pass, 4 or 8
+// terms per lane when that covers them) each fall back to the plain chain when
+// they cannot vouch for their result; a last run of fewer than 512 terms is
+// cheaper on the plain chain. Every thread of the workgroup calls it with the
+// same arguments (a in LDS, 16-byte aligned, n a multiple of 4); work is
+// kWgChainWork words of LDS that nothing else touches meanwhile. Every wave has
+// finished reading a when any wave returns, so a may be written right after
+// the call.
 template <int NW, int MAXRL = 16>
 __device__ __forceinline__ float wg_chain_nonneg(const float* __restrict__ a, int n, float s, uint32_t* __restrict__ work) {
   static_assert(MAXRL == 4 || MAXRL == 8 || MAXRL == 16, "4, 8 or 16 terms per lane");
   // a plain chain read a after the last barrier of a successful pass (the
   // decisions below are the same in every wave, so the barrier is reached by all)
   bool plain_after = true;
-  if (n < 128 + 512) {
+  if (n < 16 + 512) {
     s = wave_lane0_f32(wave_chain_from(a, n, s));
   } else {
-    s = wave_lane0_f32(wave_chain_from(a, 128, s));
-    int i = 128;
+    s = chain_head16(a, s);
+    int i = 16;
     while (n - i >= 512) {
       const int m = min(n - i, 64 * NW * MAXRL);
       bool ok;
       if (MAXRL == 4 || m <= 64 * NW * 4) ok = wg_chain_pass<NW, 4>(a + i, m, s, work);
-      else if (MAXRL == 8 || m <= 64 * NW * 8) ok = wg_chain_pass<NW, MAXRL == 4 ? 4 : 8>(a + i, m, s, work);
-      else ok = wg_chain_pass<NW, MAXRL>(a + i, m, s, work);
+      else if (MAXRL == 8 || m <= 64 * NW * 8) ok = wg_chain_pass<NW, 8>(a + i, m, s, work);
+      else ok = wg_chain_pass<NW, 16>(a + i, m, s, work);
       if (!ok) s = wave_lane0_f32(wave_chain_from(a + i, m, s));
       plain_after = !ok;
       i += m;

@@ -3,7 +3,7 @@ wg_chain_nonneg in nightrun_amd/csrc/nrq_device.h), restated lane for lane
 in numpy float32 and checked bit-exact against the sequential f32 chain, the
 reference's `ss += v * v` loop (crates/nr-tensor/src/vec.rs:4-14).
 
-The restatement follows the device code: four waves of 64 lanes, 8 or 16
+The restatement follows the device code: four waves of 64 lanes, 4, 8 or 16
 consecutive terms per lane, an f32 prediction of each term's binade (wave
 totals added in wave order across the waves), terms rounded to the unit of
 their predicted binade, special terms (binade crossings, ties) resolved in
@@ -112,18 +112,19 @@ def chain_pass(a, s, rl):
 
 
 def chain_nonneg(a, s, stats=None):
-    """wg_chain_nonneg<4>: 128 plain terms, then passes of up to 4096 terms (8
-    per lane when 2048 cover them, else 16) while at least 512 remain, then the
-    plain chain."""
+    """wg_chain_nonneg<4>: 16 plain terms, then passes of up to 4096 terms (4 or
+    8 per lane when that covers them, else 16) while at least 512 remain, then
+    the plain chain."""
     a = np.asarray(a, F32)
     n = len(a)
-    if n < 128 + 512:
+    if n < 16 + 512:
         return serial(a, s)
-    s = serial(a[:128], s)
-    i = 128
+    s = serial(a[:16], s)
+    i = 16
     while n - i >= 512:
         m = min(64 * NW * 16, n - i)
-        ok, out = chain_pass(a[i:i + m], s, 8 if m <= 64 * NW * 8 else 16)
+        rl = next(r for r in (4, 8, 16) if m <= 64 * NW * r)
+        ok, out = chain_pass(a[i:i + m], s, rl)
         if stats is not None:
             stats.append(ok)
         s = out if ok else serial(a[i:i + m], s)
