@@ -758,11 +758,12 @@ __global__ __launch_bounds__(NT) void attention_kernel(
   }
 }
 
-// Prefill attention for all GH query heads of one KV head: workgroup (g, i)
-// serves token i of a chunk (position base + i) for heads g*GH .. g*GH+GH-1.
-// Each key row is loaded once for the GH scores and each value piece once for
-// the GH heads' products, so a launch reads the cached keys and values GH
-// times less than one workgroup per head would. Per head, everything else is
+// Prefill attention for GH query heads of one KV head: workgroup (b, i) of NT
+// threads serves token i of a chunk (position base + i) for heads b*GH ..
+// b*GH+GH-1 (all of a KV group's heads, or a part of them), whose KV head is
+// b*GH / (n_heads / n_kv_heads). Each key row is loaded once for the GH scores
+// and each value piece once for the GH heads' products, so a launch reads the
+// cached keys and values GH times less than one workgroup per head would. Per head, everything else is
 // attention_kernel's, in the same order: dot_f16 in dimension order times the
 // scale, the max, expf, the exp-sum in position order (one wave per head),
 // a = e * inv, and out[d] += a_t * v_t[d] in position order (one chain lane
@@ -770,31 +771,32 @@ __global__ __launch_bounds__(NT) void attention_kernel(
 // LDS: att[GH][ctx128] | prod[2][GH * HD * CP] | q[GH * HD] | red[64]
 constexpr int kGrpProd = 9216;  // floats per product stage
 
-template <int HD, int GH>
+template <int HD, int GH, int NT = kAttNT>
 struct AttGroup {
   static constexpr int C = (kGrpProd / (GH * HD) - 4) & ~3;  // positions per chunk
   static constexpr int CP = C + 4;
   static constexpr int stage = GH * HD * CP;
   static constexpr int cw = GH * HD / 64;  // chain waves
-  static constexpr int nprod = kAttNT - 64 * cw;
+  static constexpr int nprod = NT - 64 * cw;
   static constexpr int npc = C * (HD / 8);  // 16-byte value pieces per chunk
   static size_t lds_bytes(int ctx) {
     return ((size_t)GH * ((ctx + 127) & ~127) + 2 * (size_t)stage + (size_t)GH * HD + 64) * 4;
   }
 };
 
-template <int HD, int GH>
-__global__ __launch_bounds__(kAttNT) void attention_group_kernel(
+template <int HD, int GH, int NT = kAttNT>
+__global__ __launch_bounds__(NT) void attention_group_kernel(
     const float* __restrict__ q_in, const int* __restrict__ ctl, int n_heads, int n_kv_heads, int ctx, int layer,
     float scale, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, float* __restrict__ out,
     uint8_t* __restrict__ out_q8) {
-  using A = AttGroup<HD, GH>;
+  using A = AttGroup<HD, GH, NT>;
   constexpr int hd = HD, g8 = HD / 8, C = A::C, CP = A::CP, cw = A::cw, nprod = A::nprod, npc = A::npc;
   static_assert(C >= 4, "product chunk too small");
   static_assert(npc <= nprod, "one value piece per producer thread");
-  static_assert(GH <= kAttNT / 64, "one wave per head for the exp-sum");
+  static_assert(GH <= NT / 64 && NT / 64 <= 16, "one wave per head for the exp-sum, 16 waves at most");
   extern __shared__ __align__(16) float sm[];
-  const int g = blockIdx.x, tok = blockIdx.y, tid = threadIdx.x;
+  const int h0 = (int)blockIdx.x * GH, tok = blockIdx.y, tid = threadIdx.x;
+  const int g = h0 / (n_heads / n_kv_heads);  // the KV head
   const int pos = ctl[CTL_POS] + tok, n = pos + 1;
   const int n128 = (n + 127) & ~127;
   const int ctx128 = (ctx + 127) & ~127;
@@ -802,18 +804,18 @@ __global__ __launch_bounds__(kAttNT) void attention_group_kernel(
   float* prod = sm + (size_t)GH * ctx128;
   float* qs = prod + 2 * A::stage;  // [GH][hd]
   float* red = qs + GH * hd;         // [64]
-  q_in += (size_t)tok * n_heads * hd + (size_t)g * GH * hd;
-  out += (size_t)tok * n_heads * hd + (size_t)g * GH * hd;
-  if (out_q8) out_q8 += ((size_t)tok * n_heads * hd + (size_t)g * GH * hd) / 32 * kQ8_0Bytes;
+  q_in += (size_t)tok * n_heads * hd + (size_t)h0 * hd;
+  out += (size_t)tok * n_heads * hd + (size_t)h0 * hd;
+  if (out_q8) out_q8 += ((size_t)tok * n_heads * hd + (size_t)h0 * hd) / 32 * kQ8_0Bytes;
   const size_t base = ((size_t)layer * n_kv_heads + g) * hd * ctx;
   const size_t ctx8 = (size_t)ctx * 8;
-  for (int i = tid; i < GH * hd; i += kAttNT) qs[i] = q_in[i];
+  for (int i = tid; i < GH * hd; i += NT) qs[i] = q_in[i];
   __syncthreads();
-  // scores: thread tid takes positions tid, tid + kAttNT, ...
+  // scores: thread tid takes positions tid, tid + NT, ...
   float mx[GH];
 #pragma unroll
   for (int j = 0; j < GH; j++) mx[j] = -INFINITY;
-  for (int t = tid; t < n; t += kAttNT) {
+  for (int t = tid; t < n; t += NT) {
     uint4 kr[g8];
     const uint4* src = (const uint4*)(kc + base + (size_t)t * 8);
 #pragma unroll
@@ -836,7 +838,7 @@ __global__ __launch_bounds__(kAttNT) void attention_group_kernel(
     }
   }
   // each thread's maximum per head over the scores it wrote
-  for (int t = tid; t < n; t += kAttNT) {
+  for (int t = tid; t < n; t += NT) {
 #pragma unroll
     for (int j = 0; j < GH; j++) mx[j] = fmaxf(mx[j], att[(size_t)j * ctx128 + t]);
   }
@@ -849,11 +851,11 @@ __global__ __launch_bounds__(kAttNT) void attention_group_kernel(
 #pragma unroll
   for (int j = 0; j < GH; j++) {
     float m = red[j * 16];
-    for (int w = 1; w < kAttNT / 64; w++) m = fmaxf(m, red[j * 16 + w]);
+    for (int w = 1; w < NT / 64; w++) m = fmaxf(m, red[j * 16 + w]);
     mx[j] = m;
   }
   __syncthreads();  // red is reused below
-  for (int t = tid; t < n128; t += kAttNT) {
+  for (int t = tid; t < n128; t += NT) {
 #pragma unroll
     for (int j = 0; j < GH; j++)
       att[(size_t)j * ctx128 + t] = t < n ? dev_expf(att[(size_t)j * ctx128 + t] - mx[j]) : 0.0f;
@@ -867,7 +869,7 @@ __global__ __launch_bounds__(kAttNT) void attention_group_kernel(
     }
   }
   __syncthreads();
-  for (int t = tid; t < n; t += kAttNT) {
+  for (int t = tid; t < n; t += NT) {
 #pragma unroll
     for (int j = 0; j < GH; j++) att[(size_t)j * ctx128 + t] = att[(size_t)j * ctx128 + t] * red[j];
   }
@@ -1720,20 +1722,34 @@ int att_dim_split(const nrq_model_config& c) {
   return c.head_dim == 64 ? 2 : c.head_dim == 128 ? 4 : 1;
 }
 
-// The grouped prefill attention for this model's shape, or null (then one
-// workgroup per query head); NRQ_ATT_GROUP=0 forces the latter.
-AttGroupFn att_group(const nrq_model_config& c, size_t* lds) {
-  *lds = 0;
+// The grouped prefill attention for this model's shape, or fn null (then one
+// workgroup per query head); NRQ_ATT_GROUP=0 forces the latter. 64-wide heads:
+// all of a KV group's heads in one 1024-thread workgroup. 128-wide heads: two
+// heads per 768-thread workgroup (168 registers per lane for the 16-piece key
+// row; with 1024 threads, or four heads, the key row and the chains exceed the
+// registers or the product stage).
+struct AttGroupCfg {
+  AttGroupFn fn = nullptr;
+  size_t lds = 0;
+  int gh = 0, nt = 0;
+};
+AttGroupCfg att_group(const nrq_model_config& c) {
+  AttGroupCfg g;
   const char* env = getenv("NRQ_ATT_GROUP");
-  if (env && env[0] == '0') return nullptr;
-  const int gh = c.n_heads / c.n_kv_heads;
-  // head_dim 64 only: at 128 the key row and the chains exceed 128 registers
-  AttGroupFn f = c.head_dim == 64 ? att_group_for<64>(gh, lds, c.ctx) : nullptr;
-  if (!f || *lds > 160 * 1024) {
-    *lds = 0;
-    return nullptr;
+  if (env && env[0] == '0') return g;
+  const int gqa = c.n_heads / c.n_kv_heads;
+  if (c.head_dim == 64) {
+    g.fn = att_group_for<64>(gqa, &g.lds, c.ctx);
+    g.gh = gqa;
+    g.nt = nrq::kAttNT;
+  } else if (c.head_dim == 128 && gqa % 2 == 0) {
+    g.fn = nrq::attention_group_kernel<128, 2, 768>;
+    g.lds = nrq::AttGroup<128, 2, 768>::lds_bytes(c.ctx);
+    g.gh = 2;
+    g.nt = 768;
   }
-  return f;
+  if (!g.fn || g.lds > 160 * 1024) g = AttGroupCfg{};
+  return g;
 }
 
 int prefill_alloc(nrq_model* m) {
@@ -1850,10 +1866,9 @@ int enqueue_prefill(nrq_model* m, int B) {
     if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: rope launch failed");
     {
       const bool q8 = Ly.m[3].dt == NRQ_Q8_0;
-      size_t glds = 0;
-      const AttGroupFn gk = att_group(c, &glds);
-      if (gk) {
-        hipLaunchKernelGGL(gk, dim3(c.n_kv_heads, B), dim3(nrq::kAttNT), glds, m->stream, m->bq, m->ctl, c.n_heads,
+      const AttGroupCfg gk = att_group(c);
+      if (gk.fn) {
+        hipLaunchKernelGGL(gk.fn, dim3(c.n_heads / gk.gh, B), dim3(gk.nt), gk.lds, m->stream, m->bq, m->ctl, c.n_heads,
                            c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->battn, q8 ? m->bxq : nullptr);
       } else {
         auto* kern = c.head_dim == 32   ? nrq::attention_kernel<32, true>
