@@ -1796,26 +1796,33 @@ int matmul_group_rows(nrq_model* m, const Mat* const* ws, float* const* ys, cons
   int rc;
   if (need_q8 && !have_q8 && (rc = quantize_for(m, NRQ_Q8_0, x, B * cols, m->bxq))) return rc;
   if (need_q8k && !have_q8k && (rc = quantize_for(m, NRQ_Q4_K, x, B * cols, m->bxq2))) return rc;
-  bool same = n > 1;
-  for (int i = 1; i < n; i++) same = same && ws[i]->dt == ws[0]->dt;
-  if (same) {  // one launch for the group where the prefill kernel takes it
-    nrq::MatmulGroupLaunch G{};
-    for (int i = 0; i < n; i++) {
-      G.w[i] = ws[i]->w;
-      G.y[i] = ys[i];
-      G.rows[i] = rows[i];
+  // each run of neighbours of one format in one launch where the prefill
+  // kernel takes it (Qwen3 Q4_K_M: q|k, then the Q6_K v alone)
+  for (int i = 0; i < n;) {
+    int j = i + 1;
+    while (j < n && ws[j]->dt == ws[i]->dt) j++;
+    bool done = false;
+    if (j - i > 1) {
+      nrq::MatmulGroupLaunch G{};
+      for (int k = i; k < j; k++) {
+        G.w[k - i] = ws[k]->w;
+        G.y[k - i] = ys[k];
+        G.rows[k - i] = rows[k];
+      }
+      G.nmat = j - i;
+      G.xs = ws[i]->dt == NRQ_Q8_0 ? m->bxq : m->bxq2;
+      G.bpr = cols / qk_of(ws[i]->dt);
+      G.batch = B;
+      G.stream = m->stream;
+      const int lr = nrq::launch_mmt_group(ws[i]->dt, G);
+      if (lr != nrq::NRQ_LAUNCH_OK && lr != nrq::NRQ_LAUNCH_BAD_ARG)
+        return mfail(NRQ_ERR_DEVICE, "model: matmul group launch failed");
+      done = lr == nrq::NRQ_LAUNCH_OK;
     }
-    G.nmat = n;
-    G.xs = ws[0]->dt == NRQ_Q8_0 ? m->bxq : m->bxq2;
-    G.bpr = cols / qk_of(ws[0]->dt);
-    G.batch = B;
-    G.stream = m->stream;
-    const int lr = nrq::launch_mmt_group(ws[0]->dt, G);
-    if (lr == nrq::NRQ_LAUNCH_OK) return NRQ_OK;
-    if (lr != nrq::NRQ_LAUNCH_BAD_ARG) return mfail(NRQ_ERR_DEVICE, "model: matmul group launch failed");
+    for (int k = i; k < j && !done; k++)
+      if ((rc = matmul_rows(m, *ws[k], ws[k]->dt == NRQ_Q8_0 ? m->bxq : m->bxq2, ys[k], rows[k], cols, B))) return rc;
+    i = j;
   }
-  for (int i = 0; i < n; i++)
-    if ((rc = matmul_rows(m, *ws[i], ws[i]->dt == NRQ_Q8_0 ? m->bxq : m->bxq2, ys[i], rows[i], cols, B))) return rc;
   return NRQ_OK;
 }
 
