@@ -348,12 +348,13 @@ __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, co
 // Prefill: rope::apply (rope.rs:49-65) on every query and key head of token i
 // = blockIdx.x at position base + i, queries in place, and the f16 KV append of
 // its key and value rows (infer.rs:642-651). A chunk appends all its rows
-// before any of its tokens attends, as prefill_chunk does. With qn/kn (Qwen3),
-// each head is first RMS-normalized in place (vec.rs:17-28, infer.rs:643-650):
-// its squares go to LDS, one thread per head sums them in element order, and
+// before any of its tokens attends, as prefill_chunk does. One wave per head,
+// four heads per workgroup: blockIdx.y * 4 + wave indexes the query heads, then
+// the key heads (whose waves also append the value row). With qn/kn (Qwen3),
+// the head is first RMS-normalized (vec.rs:17-28, infer.rs:643-650): its
+// squares are summed in element order by the wave (wave_chain_from), and
 // x * (scale * w) is applied as the pair is rotated. Pair j of a head is
-// (2j, 2j+1), or (j, j + hd/2) with neox. LDS: (n_heads + n_kv_heads) * (hd + 1)
-// floats with qn, else none.
+// (2j, 2j+1), or (j, j + hd/2) with neox. head_dim <= 128, a multiple of 32.
 __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q, const float* __restrict__ k,
                                                           const float* __restrict__ v,
                                                           const float* __restrict__ rope_cs,
@@ -361,54 +362,53 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float* __restrict__ q,
                                                           int hd, int ctx, int layer, uint16_t* __restrict__ kc,
                                                           uint16_t* __restrict__ vc, const float* __restrict__ qn,
                                                           const float* __restrict__ kn, float eps, int neox) {
-  extern __shared__ __align__(16) float rsm[];
-  const int i = blockIdx.x, half = hd / 2;
+  __shared__ __align__(16) float raw[4][128];
+  __shared__ __align__(16) float sqs[4][128];
+  const int i = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63, half = hd / 2;
+  const int h = (int)blockIdx.y * 4 + w;  // the wave's head: queries, then keys
+  const bool live = h < n_heads + n_kv_heads, isq = h < n_heads;
+  const int hh = isq ? h : h - n_heads;
   const int pos = ctl[CTL_POS] + i;
+  float* qi = q + ((size_t)i * n_heads + hh) * hd;
+  const float* src = isq ? (const float*)qi : k + ((size_t)i * n_kv_heads + hh) * hd;
+  float* rw = raw[w];
+  float* sq = sqs[w];
+  if (live)
+    for (int d = lane; d < hd; d += 64) {
+      const float x = src[d];
+      rw[d] = x;
+      sq[d] = x * x;
+    }
+  __syncthreads();
+  if (!live) return;
+  float scale = 0.0f;
+  if (qn) scale = 1.0f / sqrtf(wave_lane0_f32(wave_chain_from(sq, hd, 0.0f)) / (float)hd + eps);
   const float* cst = rope_cs + (size_t)i * hd;
-  float* qi = q + (size_t)i * n_heads * hd;
-  const float* ki = k + (size_t)i * n_kv_heads * hd;
-  const float* vi = v + (size_t)i * n_kv_heads * hd;
+  const float* nw = isq ? qn : kn;
   const size_t ctx8 = (size_t)ctx * 8;
-  auto kvi = [&](int g, int d) {
-    return ((size_t)layer * n_kv_heads + g) * hd * ctx + (size_t)(d >> 3) * ctx8 + (size_t)pos * 8 + (d & 7);
+  auto kvi = [&](int d) {
+    return ((size_t)layer * n_kv_heads + hh) * hd * ctx + (size_t)(d >> 3) * ctx8 + (size_t)pos * 8 + (d & 7);
   };
-  const int nq = n_heads * hd, nhh = n_heads + n_kv_heads;
-  float* hscale = rsm + (size_t)nhh * hd;  // per-head norm scale: q heads, then k heads
-  if (qn) {
-    for (int idx = threadIdx.x; idx < nq; idx += blockDim.x) rsm[idx] = qi[idx] * qi[idx];
-    for (int idx = threadIdx.x; idx < n_kv_heads * hd; idx += blockDim.x) rsm[nq + idx] = ki[idx] * ki[idx];
-    __syncthreads();
-    for (int t = threadIdx.x; t < nhh; t += blockDim.x)
-      hscale[t] = 1.0f / sqrtf(chain_sum(rsm + (size_t)t * hd, hd) / (float)hd + eps);
-    __syncthreads();
-  }
-  for (int idx = threadIdx.x; idx < n_heads * half; idx += blockDim.x) {
-    const int h = idx / half, j = idx % half;
+  for (int j = lane; j < half; j += 64) {
     const int ia = neox ? j : 2 * j, ib = neox ? j + half : 2 * j + 1;
     const float cs = cst[2 * j], sn = cst[2 * j + 1];
-    float a = qi[(size_t)h * hd + ia], b = qi[(size_t)h * hd + ib];
+    float a = rw[ia], b = rw[ib];
     if (qn) {
-      a = a * (hscale[h] * qn[ia]);
-      b = b * (hscale[h] * qn[ib]);
+      a = a * (scale * nw[ia]);
+      b = b * (scale * nw[ib]);
     }
-    qi[(size_t)h * hd + ia] = a * cs - b * sn;
-    qi[(size_t)h * hd + ib] = a * sn + b * cs;
-  }
-  for (int idx = threadIdx.x; idx < n_kv_heads * half; idx += blockDim.x) {
-    const int g = idx / half, j = idx % half;
-    const int ia = neox ? j : 2 * j, ib = neox ? j + half : 2 * j + 1;
-    const float cs = cst[2 * j], sn = cst[2 * j + 1];
-    float a = ki[(size_t)g * hd + ia], b = ki[(size_t)g * hd + ib];
-    if (qn) {
-      a = a * (hscale[n_heads + g] * kn[ia]);
-      b = b * (hscale[n_heads + g] * kn[ib]);
+    const float ra = a * cs - b * sn, rb = a * sn + b * cs;
+    if (isq) {
+      qi[ia] = ra;
+      qi[ib] = rb;
+    } else {
+      kc[kvi(ia)] = (uint16_t)f32_to_f16_bits(ra);
+      kc[kvi(ib)] = (uint16_t)f32_to_f16_bits(rb);
     }
-    kc[kvi(g, ia)] = (uint16_t)f32_to_f16_bits(a * cs - b * sn);
-    kc[kvi(g, ib)] = (uint16_t)f32_to_f16_bits(a * sn + b * cs);
   }
-  for (int idx = threadIdx.x; idx < n_kv_heads * hd; idx += blockDim.x) {
-    const int g = idx / hd, d = idx % hd;
-    vc[kvi(g, d)] = (uint16_t)f32_to_f16_bits(vi[idx]);
+  if (!isq) {
+    const float* vi = v + ((size_t)i * n_kv_heads + hh) * hd;
+    for (int d = lane; d < hd; d += 64) vc[kvi(d)] = (uint16_t)f32_to_f16_bits(vi[d]);
   }
 }
 
@@ -1866,8 +1866,8 @@ int enqueue_prefill(nrq_model* m, int B) {
       if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: norm launch failed");
       if ((rc = matmul_group_rows(m, ws, ys, rows, 3, m->bxn, d, B, q8, q8k))) return rc;
     }
-    const size_t rlds = Ly.q_norm ? (size_t)(c.n_heads + c.n_kv_heads) * (c.head_dim + 1) * 4 : 0;
-    hipLaunchKernelGGL(nrq::rope_append_kernel, dim3(B), dim3(256), rlds, m->stream, m->bq, m->bk, m->bv, m->brope,
+    hipLaunchKernelGGL(nrq::rope_append_kernel, dim3(B, (c.n_heads + c.n_kv_heads + 3) / 4), dim3(256), 0, m->stream,
+                       m->bq, m->bk, m->bv, m->brope,
                        m->ctl, c.n_heads, c.n_kv_heads, c.head_dim, c.ctx, l, m->kc, m->vc, Ly.q_norm, Ly.k_norm,
                        c.norm_eps, m->rope_neox);
     if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: rope launch failed");
