@@ -103,6 +103,10 @@ struct MatmulGroupLaunch {
   void* stream;
 };
 int launch_mmt_group(int dtype, const MatmulGroupLaunch& G);
+// Two such groups, of two different K-quant formats over one activation (q|k
+// Q4_K and v Q6_K), in one launch; NRQ_LAUNCH_BAD_ARG when the kernel does not
+// take the pair.
+int launch_mmt_group2(int dt0, const MatmulGroupLaunch& G0, int dt1, const MatmulGroupLaunch& G1);
 // AVX2-order batched matmul on int8 MFMA (nrq_mma.hip): 32-row x 32-token
 // K-quant tiles, 8-row x 32-token Q8_0 tiles.
 int launch_mma(int dtype, const MatmulLaunch& L);

@@ -447,14 +447,13 @@ struct MdMats {
 // its operands are consumed; NB = 2 or 4 is a ring whose loads run NB - 1
 // rounds ahead of the block being computed.
 template <int FMT, int KS, int NB>
-__global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* __restrict__ X, int bpr, int batch,
-                                                      int ntt, int nrt, int early_x) {
+__device__ __forceinline__ void mmd_body(const int wg, const MdMats& M, const uint8_t* __restrict__ X, int bpr,
+                                         int batch, int ntt, int nrt, int early_x) {
   constexpr int OWN = 16 / KS;  // chain elements per lane when KS > 1
   constexpr size_t BS = FMT == kQ4K ? kQ4KBytes : FMT == kQ6K ? kQ6KBytes : kQ8_0Bytes;
   constexpr size_t XS = FMT == kQ8_0 ? kQ8_0Bytes : kQ8KBytes;  // activation block bytes
   extern __shared__ __align__(16) uint32_t lds[];
   // XCD-aware numbering: the token tiles of one row tile share an XCD and its L2.
-  const int wg = blockIdx.x;
   const int xcd = wg & 7, slot = wg >> 3;
   const int tt = slot % ntt;
   const int rt = (slot / ntt) * 8 + xcd;
@@ -644,6 +643,24 @@ __global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* _
   }
 }
 
+template <int FMT, int KS, int NB>
+__global__ __launch_bounds__(64 * KS) void mmd_kernel(MdMats M, const uint8_t* __restrict__ X, int bpr, int batch,
+                                                      int ntt, int nrt, int early_x) {
+  mmd_body<FMT, KS, NB>((int)blockIdx.x, M, X, bpr, batch, ntt, nrt, early_x);
+}
+
+// Two K-quant groups of different formats over one activation (Qwen3 Q4_K_M:
+// q|k in Q4_K and v in Q6_K) in one launch: workgroups below nwg0 run the F0
+// group's tiles, the others the F1 group's, each numbered as in its own launch.
+template <int F0, int F1, int KS>
+__global__ __launch_bounds__(64 * KS) void mmd2_kernel(MdMats M0, MdMats M1, const uint8_t* __restrict__ X, int bpr,
+                                                       int batch, int ntt, int nrt0, int nrt1, int nwg0, int early0,
+                                                       int early1) {
+  const int wg = (int)blockIdx.x;
+  if (wg < nwg0) mmd_body<F0, KS, 1>(wg, M0, X, bpr, batch, ntt, nrt0, early0);
+  else mmd_body<F1, KS, 1>(wg - nwg0, M1, X, bpr, batch, ntt, nrt1, early1);
+}
+
 // ---- launch ----------------------------------------------------------------------------------
 
 namespace {
@@ -733,6 +750,33 @@ int md_choose(int dtype, long row_tiles, int batch, int bpr) {
 
 int md_buffers(int dtype, int ks);
 
+// the early activation loads of md_launch_t, by format and row length
+int md_early_x(int fmt, int bpr) {
+  const char* ex = getenv("NRQ_MMT_EARLY_X");
+  return ex && ex[0] ? ex[0] == '1' : (fmt == kQ6K || (fmt == kQ4K && bpr >= 16));
+}
+
+template <int F0, int F1, int KS>
+int md2_launch_t(const MatmulGroupLaunch& G0, const MatmulGroupLaunch& G1) {
+  int nrt0 = 0, nrt1 = 0;
+  const MdMats M0 = md_mats(G0, &nrt0), M1 = md_mats(G1, &nrt1);
+  const int ntt = (G0.batch + 31) / 32;
+  const long nwg0 = (long)((nrt0 + 7) / 8) * 8 * ntt, nwg1 = (long)((nrt1 + 7) / 8) * 8 * ntt;
+  if (nwg0 + nwg1 > 0x7fffffffL) return NRQ_LAUNCH_BAD_ARG;
+  const size_t lds = (size_t)KS * kMdScalDw * 4 + (size_t)2 * KS * 1024 * 4 + (size_t)KS * kMdStage;
+  hipLaunchKernelGGL((mmd2_kernel<F0, F1, KS>), dim3((unsigned)(nwg0 + nwg1)), dim3(64 * KS), lds,
+                     (hipStream_t)G0.stream, M0, M1, (const uint8_t*)G0.xs, G0.bpr, G0.batch, ntt, nrt0, nrt1,
+                     (int)nwg0, md_early_x(F0, G0.bpr), md_early_x(F1, G1.bpr));
+  return hipGetLastError() == hipSuccess ? 0 : NRQ_LAUNCH_FAILED;
+}
+
+template <int F0, int F1>
+int md2_launch_ks(const MatmulGroupLaunch& G0, const MatmulGroupLaunch& G1, int ks) {
+  if (ks >= 8) return md2_launch_t<F0, F1, 8>(G0, G1);
+  if (ks == 4) return md2_launch_t<F0, F1, 4>(G0, G1);
+  return md2_launch_t<F0, F1, 2>(G0, G1);
+}
+
 int md_group(int dtype, const MatmulGroupLaunch& G) {
   long row_tiles = 0;
   for (int i = 0; i < G.nmat; i++) row_tiles += (G.rows[i] + 31) / 32;
@@ -794,6 +838,25 @@ int launch_mmt_group(int dtype, const MatmulGroupLaunch& G) {
   }
   if (dtype == kQ8_0 && (total < 1024 || (bases & 3u))) return NRQ_LAUNCH_BAD_ARG;
   return md_group(dtype, G);
+}
+
+// Two groups of different K-quant formats over one activation in one launch,
+// when the split rule gives both more than one split (so that both take one
+// load buffer, as their own launches would); else NRQ_LAUNCH_BAD_ARG.
+int launch_mmt_group2(int dt0, const MatmulGroupLaunch& G0, int dt1, const MatmulGroupLaunch& G1) {
+  const bool kq0 = dt0 == kQ4K || dt0 == kQ6K, kq1 = dt1 == kQ4K || dt1 == kQ6K;
+  if (!kq0 || !kq1 || dt0 == dt1 || G0.xs != G1.xs || G0.bpr != G1.bpr || G0.batch != G1.batch) return NRQ_LAUNCH_BAD_ARG;
+  for (const MatmulGroupLaunch* G : {&G0, &G1}) {
+    if (G->nmat < 1 || G->nmat > 3 || G->bpr <= 0 || G->batch <= 0) return NRQ_LAUNCH_BAD_ARG;
+    for (int i = 0; i < G->nmat; i++)
+      if (G->rows[i] <= 0) return NRQ_LAUNCH_BAD_ARG;
+  }
+  long row_tiles = 0;
+  for (const MatmulGroupLaunch* G : {&G0, &G1})
+    for (int i = 0; i < G->nmat; i++) row_tiles += (G->rows[i] + 31) / 32;
+  const int ks = md_choose(dt0, row_tiles, G0.batch, G0.bpr);
+  if (ks < 2 || md_buffers(dt0, ks) != 1 || md_buffers(dt1, ks) != 1) return NRQ_LAUNCH_BAD_ARG;
+  return dt0 == kQ4K ? md2_launch_ks<kQ4K, kQ6K>(G0, G1, ks) : md2_launch_ks<kQ6K, kQ4K>(G0, G1, ks);
 }
 
 }  // namespace nrq

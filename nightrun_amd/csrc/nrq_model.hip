@@ -1796,8 +1796,35 @@ int matmul_group_rows(nrq_model* m, const Mat* const* ws, float* const* ys, cons
   int rc;
   if (need_q8 && !have_q8 && (rc = quantize_for(m, NRQ_Q8_0, x, B * cols, m->bxq))) return rc;
   if (need_q8k && !have_q8k && (rc = quantize_for(m, NRQ_Q4_K, x, B * cols, m->bxq2))) return rc;
+  // two runs of different K-quant formats (Qwen3 Q4_K_M: q|k, then the Q6_K
+  // v) in one launch where the prefill kernel takes the pair
+  {
+    int j = 1;
+    while (j < n && ws[j]->dt == ws[0]->dt) j++;
+    bool two = j < n && ws[0]->dt != NRQ_Q8_0 && ws[j]->dt != NRQ_Q8_0;
+    for (int k = j + 1; k < n && two; k++) two = ws[k]->dt == ws[j]->dt;
+    if (two) {
+      nrq::MatmulGroupLaunch G[2]{};
+      for (int gi = 0; gi < 2; gi++) {
+        const int a = gi ? j : 0, b = gi ? n : j;
+        for (int k = a; k < b; k++) {
+          G[gi].w[k - a] = ws[k]->w;
+          G[gi].y[k - a] = ys[k];
+          G[gi].rows[k - a] = rows[k];
+        }
+        G[gi].nmat = b - a;
+        G[gi].xs = m->bxq2;
+        G[gi].bpr = cols / 256;
+        G[gi].batch = B;
+        G[gi].stream = m->stream;
+      }
+      const int lr = nrq::launch_mmt_group2(ws[0]->dt, G[0], ws[j]->dt, G[1]);
+      if (lr == nrq::NRQ_LAUNCH_OK) return NRQ_OK;
+      if (lr != nrq::NRQ_LAUNCH_BAD_ARG) return mfail(NRQ_ERR_DEVICE, "model: matmul group launch failed");
+    }
+  }
   // each run of neighbours of one format in one launch where the prefill
-  // kernel takes it (Qwen3 Q4_K_M: q|k, then the Q6_K v alone)
+  // kernel takes it
   for (int i = 0; i < n;) {
     int j = i + 1;
     while (j < n && ws[j]->dt == ws[i]->dt) j++;
