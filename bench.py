@@ -577,6 +577,35 @@ def measure_qwen3(fill=512, n=64):
                                "source": "docs/benchmarks.md:63-64, docs/baseline-x86.md:144"}}
 
 
+def measure_qwen3_prefill(tokens):
+    """The Qwen3 leg's model (Q4_K_M formats through a Qwen3 .nrm file), then
+    nrq_model_prefill of a random `tokens`-token prompt in 64-token chunks
+    (eager launches, no graph): the prefill alone, for kernel traces."""
+    import torch
+
+    from nightrun_amd import nrm
+
+    cfg = QWEN3_4B
+    w = synth_model(cfg, 0x5EED0044, dtypes=QWEN3_DTYPES, embed_dtype=3, qk_norm=True)
+    blob = nrm_blob(cfg, w, arch=2, name=b"qwen3-4b")
+    del w
+    f = nrm.NrmFile(blob)
+    m = f.load(tokens + 8, verify=False)
+    del blob
+    prompt = np.random.default_rng(44).integers(0, cfg["vocab"], tokens).astype(np.uint32)
+    m.prefill(prompt[:64], logits=False)  # warm-up
+    m.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    m.prefill(prompt, logits=False)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    m.close()
+    return {"workload": f"Qwen3-4B architecture, Q4_K_M formats, random init: prefill of {tokens} tokens in "
+                        "64-token chunks, eager launches", "tokens": tokens, "seconds": round(dt, 4),
+            "tok_s": round(tokens / dt, 1)}
+
+
 def measure_qwen3_eager(steps, fill=512):
     """The Qwen3-4B leg's model and prompt, then `steps` greedy decode steps
     launched eagerly (nrq_model_forward, no graph): a kernel trace of the
@@ -792,6 +821,8 @@ def main():
     ap.add_argument("--no-qwen3", action="store_true", help="skip the Qwen3-4B decode/prefill leg")
     ap.add_argument("--qwen3-eager", type=int, default=0, metavar="STEPS",
                     help="only: the Qwen3-4B model, then STEPS eagerly launched greedy steps (no graph)")
+    ap.add_argument("--qwen3-prefill", type=int, default=0, metavar="TOKENS",
+                    help="only: the Qwen3-4B model, then nrq_model_prefill of TOKENS tokens (eager, no graph)")
     ap.add_argument("--prefill-only", type=int, default=0, metavar="TOKENS",
                     help="only time nrq_model_prefill of TOKENS tokens on the Llama-3.2-1B-shape model")
     ap.add_argument("--crc-only", type=int, default=0, metavar="BYTES",
@@ -807,6 +838,12 @@ def main():
 
         nightrun_amd.init(0)
         print(json.dumps({"decode_qwen3_eager": measure_qwen3_eager(args.qwen3_eager)}))
+        return
+    if args.qwen3_prefill:
+        import nightrun_amd
+
+        nightrun_amd.init(0)
+        print(json.dumps({"prefill_qwen3": measure_qwen3_prefill(args.qwen3_prefill)}))
         return
     if args.qwen3_only:
         import nightrun_amd
