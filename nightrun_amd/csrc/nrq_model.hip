@@ -476,7 +476,7 @@ __global__ __launch_bounds__(NT) void attention_kernel(
   const int bq = (int)blockIdx.x >> 3;
   const int h = DS > 1 ? 8 * (bq / DS) + ((int)blockIdx.x & 7) : (int)blockIdx.x, tid = threadIdx.x;
   const int dim0 = DS > 1 ? (bq % DS) * DW : 0;  // this workgroup's first value dimension
-  const int tok = PF ? (int)blockIdx.y : 0;
+  const int tok = PF ? (int)(gridDim.y - 1 - blockIdx.y) : 0;  // prefill: the longest rows first
   const int pos = ctl[CTL_POS] + tok, n = pos + 1;
   const int self = PF ? -1 : pos;  // the position served from LDS rather than the cache
   if (PF) {
@@ -795,7 +795,8 @@ __global__ __launch_bounds__(NT) void attention_group_kernel(
   static_assert(npc <= nprod, "one value piece per producer thread");
   static_assert(GH <= NT / 64 && NT / 64 <= 16, "one wave per head for the exp-sum, 16 waves at most");
   extern __shared__ __align__(16) float sm[];
-  const int h0 = (int)blockIdx.x * GH, tok = blockIdx.y, tid = threadIdx.x;
+  // the chunk's last tokens (the most positions) are dispatched first
+  const int h0 = (int)blockIdx.x * GH, tok = (int)(gridDim.y - 1 - blockIdx.y), tid = threadIdx.x;
   const int g = h0 / (n_heads / n_kv_heads);  // the KV head
   const int pos = ctl[CTL_POS] + tok, n = pos + 1;
   const int n128 = (n + 127) & ~127;
