@@ -247,7 +247,7 @@ __global__ void embed_rows_kernel(const uint8_t* __restrict__ E, int dt, const i
   x[(size_t)row * dim + i] = escale != 1.0f ? v * escale : v;  // muP embedding scale (infer.rs:608-615)
 }
 
-constexpr int kNormNT = 256;
+constexpr int kNormNT = 512;
 constexpr int kNormMax = 8192;
 constexpr int kNormPT = kNormMax / kNormNT;  // values per thread
 
@@ -255,10 +255,11 @@ constexpr int kNormPT = kNormMax / kNormNT;  // values per thread
 // rmsnorm (vec.rs:4-14): ss += v*v in element order, scale = 1/sqrtf(ss/n + eps),
 // out = x * scale * w. Writes out (f32) and, when xq != null, its Q8_0 blocks
 // (q8.rs:27-44), when xqk != null its Q8_K blocks (kquant.rs:157-187). One
-// workgroup; n <= kNormMax, a multiple of 256. Thread t owns the 8-value runs
-// t + 256k (four consecutive runs, an aligned lane quad, make one Q8_0 block;
-// 32, an aligned half-wave, one Q8_K block), loaded once, all loads issued
-// before the first use; the four waves run the ordered sum of squares together. Workgroup r
+// workgroup of kNormNT threads; n <= kNormMax, a multiple of 256. Thread t owns
+// the 8-value runs t + kNormNT k (four consecutive runs, an aligned lane quad,
+// make one Q8_0 block; 32, an aligned half-wave, one Q8_K block), loaded once,
+// all loads issued before the first use; all waves run the ordered sum of
+// squares together. Workgroup r
 // takes row r of [rows][n] x, add, out, xq and xqk (one row per workgroup in a
 // prefill chunk).
 __global__ __launch_bounds__(kNormNT) void norm_kernel(float* __restrict__ x, const float* __restrict__ add,
