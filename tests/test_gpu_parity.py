@@ -247,6 +247,37 @@ def test_hand_derived_step_pins_on_device(gpu):
             assert np.all(gpu_matmul(dtype, 0, wr, xs, rows, cols, 5) == want)
 
 
+@pytest.mark.parametrize("dtype", [2, 3])
+def test_scale_chain_past_2p24_on_device(gpu, oracle, dtype):
+    """The K-quant scale chains whose partial sums pass 2^24 and round
+    (tests/test_oracle_kquant_order.py: Q4_K 11521440, Q6_K 2^25, where the
+    exact integer sums are 11521441 and 2^25 + 3), in every third row beside
+    random blocks, so that the lanes of a wave take both the integer and the
+    f32 form of the chain; decode matvec and prefill tiles."""
+    from tests.test_oracle_kquant_order import _q6k_chain_case, q4k_chain_case
+
+    if dtype == 2:
+        wc, xc, _ = q4k_chain_case()
+        want = 11521440.0
+    else:
+        wc, xc, _ = _q6k_chain_case()
+        want = 2.0 ** 25
+    assert gpu_matvec(dtype, 0, wc, xc, 1, 256)[0] == want
+    cols = 512
+    xr = oracle.quantize_act(dtype, oracle.Rng(17).normal(256))
+    x = np.ascontiguousarray(np.concatenate([xc.reshape(-1), xr.reshape(-1)]))
+    for rows in (40, 1056):
+        w = oracle.gen_weights(dtype, 90 + rows, rows, cols).reshape(rows, 2, -1).copy()
+        w[::3, 0] = wc[0]
+        w = np.ascontiguousarray(w.reshape(rows, -1))
+        ref = oracle.matvec(dtype, 0, w, x, rows, cols)
+        assert_bitwise(gpu_matvec(dtype, 0, w, x, rows, cols), ref, f"{NAMES[dtype]} {rows} rows")
+        xs = np.ascontiguousarray(np.tile(x, 5))
+        got = gpu_matmul(dtype, 0, w, xs, rows, cols, 5).reshape(5, rows)
+        for t in range(5):
+            assert_bitwise(got[t], ref, f"{NAMES[dtype]} {rows} rows, token {t}")
+
+
 # ---- f16 scale decode --------------------------------------------------------------
 
 

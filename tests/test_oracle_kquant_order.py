@@ -158,6 +158,21 @@ def q4k_sub(b4, bx, j):
 # ---- Q4_K scalar -----------------------------------------------------------------
 
 
+def q4k_chain_case():
+    """Sub-blocks 0-4 and 6-7 have scale 63 and sub-dot 32*15*(+-127); sub-block 5
+    has scale 1 and sub-dot 1; d = 1, dmin = 0, x.d = 1 (the case below)."""
+    q4 = np.zeros(256, dtype=np.int64)
+    q8 = np.zeros(256, dtype=np.int64)
+    for j in (0, 1, 2, 3, 4, 6, 7):
+        q4[32 * j:32 * j + 32] = 15
+        q8[32 * j:32 * j + 32] = 127 if j < 5 else -127
+    q4[32 * 5], q8[32 * 5] = 1, 1
+    sc = [63, 63, 63, 63, 63, 1, 63, 63]
+    w = q4k_block(F16_ONE, 0, sc, [0] * 8, q4).reshape(1, 144)
+    x = q8k_block(1.0, q8).reshape(1, 292)
+    return w, x, sc
+
+
 def test_q4k_scalar_sum_q_is_an_f32_chain_in_subblock_order(oracle):
     """sum_q += sc*sub for j = 0..7 in f32 (kquant.rs:212). With sc = 63 and
     sub = 32*15*127 = 60960, T = sc*sub = 3840480. Sub-blocks 0-4 give +T,
@@ -168,15 +183,7 @@ def test_q4k_scalar_sum_q_is_an_f32_chain_in_subblock_order(oracle):
     that adds the 1 below 2^24) gives 11521441."""
     O = oracle
     T = 63 * 60960
-    q4 = np.zeros(256, dtype=np.int64)
-    q8 = np.zeros(256, dtype=np.int64)
-    for j in (0, 1, 2, 3, 4, 6, 7):
-        q4[32 * j:32 * j + 32] = 15
-        q8[32 * j:32 * j + 32] = 127 if j < 5 else -127
-    q4[32 * 5], q8[32 * 5] = 1, 1
-    sc = [63, 63, 63, 63, 63, 1, 63, 63]
-    w = q4k_block(F16_ONE, 0, sc, [0] * 8, q4).reshape(1, 144)
-    x = q8k_block(1.0, q8).reshape(1, 292)
+    w, x, sc = q4k_chain_case()
     terms = [sc[j] * q4k_sub(w[0], x[0], j) for j in range(8)]
     assert terms == [T] * 5 + [1, -T, -T]
     got = O.dot(O.Q4K, O.ORDER_SCALAR, w, x)
