@@ -105,7 +105,7 @@ def run_pair(oracle, cfg, weights, ctx, prompt, n_gen, check_kv=True, prefill=Fa
         else:
             for i, t in enumerate(prompt):
                 lg = m.forward(int(t), logits=(i == len(prompt) - 1))
-        first = int(np.argmax(lg)) if lg is not None else None
+        first = oracle.argmax(lg) if lg is not None else None  # vec.rs:80-90: NaN never wins
         # the first generated token comes from the prompt's last logits
         assert first == want_tokens[0], (first, want_tokens[0])
         got_tokens, last = m.generate(first, n_gen, logits=True)
@@ -126,6 +126,29 @@ def test_tiny_model_forward_and_generate(gpu, oracle):
     w = oracle.gen_model(TINY, 1234)
     prompt = np.random.default_rng(1).integers(0, TINY["vocab"], 70).astype(np.uint32)
     run_pair(oracle, TINY, w, 128, prompt, 20)
+
+
+@pytest.mark.parametrize("case", ["all_equal", "two_best_and_nan"])
+def test_greedy_pick_ties_and_nan(gpu, oracle, case):
+    """The greedy pick (vec.rs:80-90: the first index of the largest logit,
+    NaN never chosen) over the head launch's workgroups, which each leave the
+    pick of their own rows: every row of the tied head equal (every logit
+    ties, token 0), or all rows zero but two equal ones in different
+    workgroups and one whose scale is NaN."""
+    w = oracle.gen_model(TINY, 4321)
+    e = w["embed"].reshape(TINY["vocab"], -1, 34).copy()
+    if case == "all_equal":
+        e[:] = e[7]
+        prompt = [3, 9, 27]
+    else:
+        keep = e[123].copy()
+        e[:] = 0
+        e[300] = keep
+        e[700] = keep
+        e[5, :, 0:2] = np.array([0x7E00], dtype=np.uint16).view(np.uint8)  # f16 NaN scales
+        prompt = [300, 700, 300, 1]
+    w["embed"] = e.reshape(w["embed"].shape)
+    run_pair(oracle, TINY, w, 64, np.array(prompt, dtype=np.uint32), 6)
 
 
 def test_step_profile_is_a_forward_step(gpu, oracle):
