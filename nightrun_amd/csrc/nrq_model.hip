@@ -774,7 +774,10 @@ constexpr int kGrpProd = 9216;  // floats per product stage
 
 template <int HD, int GH, int NT = kAttNT>
 struct AttGroup {
-  static constexpr int C = (kGrpProd / (GH * HD) - 4) & ~3;  // positions per chunk
+  // positions per chunk: the product stage's, at most one value piece per producer thread
+  static constexpr int C0 = (kGrpProd / (GH * HD) - 4) & ~3;
+  static constexpr int C1 = ((NT - GH * HD) / (HD / 8)) & ~3;
+  static constexpr int C = C0 < C1 ? C0 : C1;
   static constexpr int CP = C + 4;
   static constexpr int stage = GH * HD * CP;
   static constexpr int cw = GH * HD / 64;  // chain waves
@@ -786,7 +789,7 @@ struct AttGroup {
 };
 
 template <int HD, int GH, int NT = kAttNT>
-__global__ __launch_bounds__(NT) void attention_group_kernel(
+__global__ __launch_bounds__(NT, NT <= 512 ? 4 : 1) void attention_group_kernel(
     const float* __restrict__ q_in, const int* __restrict__ ctl, int n_heads, int n_kv_heads, int ctx, int layer,
     float scale, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, float* __restrict__ out,
     uint8_t* __restrict__ out_q8) {
@@ -818,25 +821,55 @@ __global__ __launch_bounds__(NT) void attention_group_kernel(
 #pragma unroll
   for (int j = 0; j < GH; j++) mx[j] = -INFINITY;
   for (int t = tid; t < n; t += NT) {
-    uint4 kr[g8];
     const uint4* src = (const uint4*)(kc + base + (size_t)t * 8);
+    if constexpr (NT <= 512) {
+      // the key row in halves of g8 / 2 pieces (registers for four waves per SIMD);
+      // each head's dot runs on over the halves, in dimension order
+      constexpr int hp = g8 / 2;
+      float sc[GH];
 #pragma unroll
-    for (int p8 = 0; p8 < g8; p8++) kr[p8] = src[(size_t)p8 * ctx];
-#pragma unroll 1
-    for (int j = 0; j < GH; j++) {  // one head at a time beside the packed key
-      const float* q = qs + j * hd;
-      float sc = 0.0f;
+      for (int j = 0; j < GH; j++) sc[j] = 0.0f;
 #pragma unroll
-      for (int p8 = 0; p8 < g8; p8++) {
-        const uint32_t kw[4] = {kr[p8].x, kr[p8].y, kr[p8].z, kr[p8].w};
+      for (int hf = 0; hf < 2; hf++) {
+        uint4 kr[hp];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          sc = sc + f16_bits_to_f32(kw[e] & 0xffffu) * q[8 * p8 + 2 * e];
-          sc = sc + f16_bits_to_f32(kw[e] >> 16) * q[8 * p8 + 2 * e + 1];
+        for (int p = 0; p < hp; p++) kr[p] = src[(size_t)(hp * hf + p) * ctx];
+#pragma unroll
+        for (int j = 0; j < GH; j++) {
+          const float* q = qs + j * hd + 8 * hp * hf;
+#pragma unroll
+          for (int p = 0; p < hp; p++) {
+            const uint32_t kw[4] = {kr[p].x, kr[p].y, kr[p].z, kr[p].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              sc[j] = sc[j] + f16_bits_to_f32(kw[e] & 0xffffu) * q[8 * p + 2 * e];
+              sc[j] = sc[j] + f16_bits_to_f32(kw[e] >> 16) * q[8 * p + 2 * e + 1];
+            }
+          }
         }
       }
-      const float a = sc * scale;
-      att[(size_t)j * ctx128 + t] = a;
+#pragma unroll
+      for (int j = 0; j < GH; j++) att[(size_t)j * ctx128 + t] = sc[j] * scale;
+    } else {
+      uint4 kr[g8];
+#pragma unroll
+      for (int p8 = 0; p8 < g8; p8++) kr[p8] = src[(size_t)p8 * ctx];
+#pragma unroll 1
+      for (int j = 0; j < GH; j++) {  // one head at a time beside the packed key
+        const float* q = qs + j * hd;
+        float sc = 0.0f;
+#pragma unroll
+        for (int p8 = 0; p8 < g8; p8++) {
+          const uint32_t kw[4] = {kr[p8].x, kr[p8].y, kr[p8].z, kr[p8].w};
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            sc = sc + f16_bits_to_f32(kw[e] & 0xffffu) * q[8 * p8 + 2 * e];
+            sc = sc + f16_bits_to_f32(kw[e] >> 16) * q[8 * p8 + 2 * e + 1];
+          }
+        }
+        const float a = sc * scale;
+        att[(size_t)j * ctx128 + t] = a;
+      }
     }
   }
   // each thread's maximum per head over the scores it wrote
@@ -1801,10 +1834,10 @@ AttGroupCfg att_group(const nrq_model_config& c) {
     g.gh = gqa;
     g.nt = nrq::kAttNT;
   } else if (c.head_dim == 128 && gqa % 2 == 0) {
-    g.fn = nrq::attention_group_kernel<128, 2, 768>;
-    g.lds = nrq::AttGroup<128, 2, 768>::lds_bytes(c.ctx);
+    g.fn = nrq::attention_group_kernel<128, 2, 512>;
+    g.lds = nrq::AttGroup<128, 2, 512>::lds_bytes(c.ctx);
     g.gh = 2;
-    g.nt = 768;
+    g.nt = 512;
   }
   if (!g.fn || g.lds > 160 * 1024) g = AttGroupCfg{};
   return g;
