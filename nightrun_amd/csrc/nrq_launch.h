@@ -47,12 +47,6 @@ struct QuantLaunch {
 // Scalar order: the streaming kernel (nrq_wstream.hip); AVX2 order: the
 // one-shot LDS tile kernel (nrq_matvec.hip).
 int launch_matvec(int dtype, int order, const MatvecLaunch& L);
-// The scalar-order matvec with each workgroup's greedy pick (vec.rs:80-90:
-// the first row of its largest output, NaN and -inf never chosen) written to
-// part[2 w] (value bits) and part[2 w + 1] (row, or 0x7fffffff for none), for
-// workgroups w < *nparts; part holds 2 * rows words. NRQ_LAUNCH_TOO_WIDE when
-// the rows do not fit its tiles.
-int launch_matvec_argmax(int dtype, const MatvecLaunch& L, uint32_t* part, int* nparts);
 // Scalar-order decode, one lane per block, per-wave LDS streaming (nrq_wstream.hip).
 int launch_wstream_scalar(int dtype, const MatvecLaunch& L);
 // scalar-order matvecs of up to three matrices of one format sharing the

@@ -992,46 +992,6 @@ __global__ void scale_kernel(float* __restrict__ x, int n, float s) {
 
 constexpr int kArgNT = 1024;
 
-// The end of a greedy pick: the workgroup's candidates (value, first index;
-// none: -inf, 0x7fffffff) combined, larger value or equal value and smaller
-// index winning, then the step's bookkeeping: next token, output slot,
-// position + 1 (without ctl, only out_tokens[0]).
-__device__ inline void pick_finish(float bv, int bi, float* sv, int* si, int* __restrict__ ctl,
-                                   uint32_t* __restrict__ out_tokens, int max_out) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const float ov = __shfl_xor(bv, m);
-    const int oi = __shfl_xor(bi, m);
-    if (ov > bv || (ov == bv && oi < bi)) {
-      bv = ov;
-      bi = oi;
-    }
-  }
-  if ((tid & 63) == 0) {
-    sv[tid >> 6] = bv;
-    si[tid >> 6] = bi;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    for (int wv = 1; wv < kArgNT / 64; wv++)
-      if (sv[wv] > bv || (sv[wv] == bv && si[wv] < bi)) {
-        bv = sv[wv];
-        bi = si[wv];
-      }
-    const int best = bi == 0x7fffffff ? 0 : bi;
-    if (!ctl) {  // a lone draw (nrq_dev_sample): the id only
-      out_tokens[0] = (uint32_t)best;
-      return;
-    }
-    ctl[CTL_TOKEN] = best;
-    const int step = ctl[CTL_STEP];
-    if (out_tokens && step < max_out) out_tokens[step] = (uint32_t)best;
-    ctl[CTL_STEP] = step + 1;
-    ctl[CTL_POS] = ctl[CTL_POS] + 1;
-  }
-}
-
 // vec.rs:80-90 (first index of the largest value; NaN never wins), then the
 // step's bookkeeping: next token, output slot, position + 1 (without ctl, only
 // out_tokens[0]).
@@ -1072,28 +1032,37 @@ __global__ __launch_bounds__(kArgNT) void argmax_kernel(const float* __restrict_
       bv = x[i];
       bi = i;
     }
-  pick_finish(bv, bi, sv, si, ctl, out_tokens, max_out);
-}
-
-// The same pick over the head launch's per-workgroup partials (value bits,
-// row; rows 0x7fffffff for none), which cover the rows in order.
-__global__ __launch_bounds__(kArgNT) void argmax_part_kernel(const uint2* __restrict__ part, int np,
-                                                             int* __restrict__ ctl, uint32_t* __restrict__ out_tokens,
-                                                             int max_out) {
-  __shared__ float sv[kArgNT / 64];
-  __shared__ int si[kArgNT / 64];
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int p = threadIdx.x; p < np; p += kArgNT) {
-    const uint2 q = part[p];
-    const float v = __uint_as_float(q.x);
-    const int i = (int)q.y;
-    if (v > bv || (v == bv && i < bi)) {
-      bv = v;
-      bi = i;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(bv, m);
+    const int oi = __shfl_xor(bi, m);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
     }
   }
-  pick_finish(bv, bi, sv, si, ctl, out_tokens, max_out);
+  if ((tid & 63) == 0) {
+    sv[tid >> 6] = bv;
+    si[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int wv = 1; wv < kArgNT / 64; wv++)
+      if (sv[wv] > bv || (sv[wv] == bv && si[wv] < bi)) {
+        bv = sv[wv];
+        bi = si[wv];
+      }
+    const int best = bi == 0x7fffffff ? 0 : bi;
+    if (!ctl) {  // a lone draw (nrq_dev_sample): the id only
+      out_tokens[0] = (uint32_t)best;
+      return;
+    }
+    ctl[CTL_TOKEN] = best;
+    const int step = ctl[CTL_STEP];
+    if (out_tokens && step < max_out) out_tokens[step] = (uint32_t)best;
+    ctl[CTL_STEP] = step + 1;
+    ctl[CTL_POS] = ctl[CTL_POS] + 1;
+  }
 }
 
 constexpr int kTopK = 64;                      // sample.rs:12
@@ -1490,8 +1459,6 @@ struct nrq_model {
   float samp_t = 0.0f, samp_p = 1.0f;
   unsigned long long* rng = nullptr;  // device word, seed | 1
   unsigned long long* samp_part = nullptr;  // the sampler's partial top-64 lists
-  // the head launch's per-workgroup greedy picks (value bits, row)
-  uint32_t* am_part = nullptr;
   // the recipe (infer.rs:447-461): Neox rope pairs, muP scalars
   int rope_neox = 0;
   float embed_scale = 1.0f, att_scale = 0.0f, res_scale = 1.0f, logit_recip = 1.0f;
@@ -1744,29 +1711,6 @@ int enqueue_step(nrq_model* m) {
   }
   if ((rc = norm_quant(m, xr, pending, m->out_norm, m->output.dt))) return rc;
   step_mark(m, kStFinalNorm);
-  if (m->samp_t <= 0.0f && m->logit_recip == 1.0f) {
-    // greedy, unscaled logits: each workgroup of the head's launch leaves the
-    // first row of its largest logit, and one workgroup picks among those
-    nrq::MatvecLaunch L;
-    L.w = m->output.w;
-    L.x = m->xq;
-    L.y = m->logits;
-    L.rows = c.vocab;
-    L.bpr = d / qk_of(m->output.dt);
-    L.tile_rows = 0;
-    L.stream = m->stream;
-    int np = 0;
-    const int lrc = nrq::launch_matvec_argmax(m->output.dt, L, m->am_part, &np);
-    if (lrc == 0) {
-      step_mark(m, kStHead);
-      hipLaunchKernelGGL(nrq::argmax_part_kernel, dim3(1), dim3(nrq::kArgNT), 0, m->stream, (const uint2*)m->am_part,
-                         np, m->ctl, m->out_tokens, m->max_out);
-      if (hipGetLastError() != hipSuccess) return mfail(NRQ_ERR_DEVICE, "model: argmax launch failed");
-      step_mark(m, kStPick);
-      return NRQ_OK;
-    }
-    if (lrc != nrq::NRQ_LAUNCH_TOO_WIDE) return mfail(NRQ_ERR_DEVICE, "model: head launch failed");
-  }
   if ((rc = matvec(m, m->output, m->xq, m->logits, c.vocab, d))) return rc;
   if ((rc = scale_logits(m))) return rc;
   step_mark(m, kStHead);
@@ -2120,7 +2064,6 @@ int nrq_model_create(const nrq_model_config* cfg, nrq_model** out) {
       {(void**)&m->ctl, nrq::CTL_WORDS * 4},
       {(void**)&m->rng, 8},
       {(void**)&m->samp_part, (size_t)(c.vocab + nrq::kSelSlice - 1) / nrq::kSelSlice * nrq::kSelPart * 4},
-      {(void**)&m->am_part, (size_t)c.vocab * 8},  // at most one workgroup per row
   };
   for (auto& a : allocs) {
     if ((e = hipMalloc(a.p, a.bytes)) != hipSuccess) return bail(e, "hipMalloc");
@@ -2499,8 +2442,7 @@ int nrq_model_destroy(nrq_model* m) {
   if (m->graph) hipGraphDestroy(m->graph);
   void* bufs[] = {m->freqs, m->rope_cs, m->kc, m->vc, m->x, m->x2, m->xb, m->q, m->k, m->v, m->attn, m->gate, m->up, m->xb2,
                   m->logits, m->xq, m->xq2, m->ctl, m->out_tokens, m->owned, m->bx, m->bxb, m->bxn, m->bq,
-                  m->bk, m->bv, m->battn, m->bgate, m->bup, m->brope, m->bxq, m->bxq2, m->btok, m->rng, m->samp_part,
-                  m->am_part};
+                  m->bk, m->bv, m->battn, m->bgate, m->bup, m->brope, m->bxq, m->bxq2, m->btok, m->rng, m->samp_part};
   for (void* p : bufs)
     if (p) hipFree(p);
   if (m->stream) hipStreamDestroy(m->stream);

@@ -283,8 +283,6 @@ struct WsArgs {
   // fused norm, K-quant weights: workgroup 0 also stores the activation's Q8_K
   // blocks here (or null), for the next matvec over the same activation
   uint8_t* xq_out;
-  // fused greedy pick (one matrix): one partial per workgroup (value bits, row)
-  uint32_t* am_part;
 };
 
 // Block contributions of a wave's rows wait in LDS for the per-row sum. Long
@@ -295,22 +293,7 @@ __host__ __device__ inline bool ws_u_rowmajor(int bpr) { return bpr >= 48; }
 // Kernel variants, chosen at launch so that each instantiation carries only
 // its own code: the fused rmsnorm prologue, the swiglu pair epilogue, and the
 // row-major contribution layout.
-enum { kWsNorm = 1, kWsSwiglu = 2, kWsRowMajorU = 4, kWsQuant = 8, kWsArgmax = 16 };
-
-// vec.rs:80-90 (first index of the largest value, NaN never wins) as a
-// reduction: candidate (ov, oi) replaces (bv, bi) when it is larger, or equal
-// with a smaller index. NaN and -inf never enter as candidates.
-__device__ __forceinline__ void am_take(float& bv, int& bi, float ov, int oi) {
-  if (ov > bv || (ov == bv && oi < bi)) {
-    bv = ov;
-    bi = oi;
-  }
-}
-
-__device__ __forceinline__ void am_wave(float& bv, int& bi) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) am_take(bv, bi, __shfl_xor(bv, m), __shfl_xor(bi, m));
-}
+enum { kWsNorm = 1, kWsSwiglu = 2, kWsRowMajorU = 4, kWsQuant = 8 };
 __host__ __device__ inline int ws_u_stride(int bpr) { return ((bpr + 3) & ~3) + 4; }
 
 template <int FMT>
@@ -373,9 +356,8 @@ __device__ __forceinline__ void ws_dma16_g(const void* g, uint32_t m0) {
 template <int FMT, int NW, int NS, int MODE>
 __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int rpw, int nstages) {
   constexpr bool NORM = (MODE & kWsNorm) != 0, SWI = (MODE & kWsSwiglu) != 0, URM = (MODE & kWsRowMajorU) != 0;
-  constexpr bool QNT = (MODE & kWsQuant) != 0, ARG = (MODE & kWsArgmax) != 0;
+  constexpr bool QNT = (MODE & kWsQuant) != 0;
   using F = WS<FMT>;
-  static_assert(!ARG || !(NORM || SWI || QNT), "the fused pick follows a plain matvec");
   static_assert(!QNT || (!NORM && FMT != kQ8_0), "the quantize prologue makes Q8_K blocks from an f32 activation");
   constexpr int NI = F::NI, BS = F::BS, TBK = 64 * F::BPL, STAGE = NI * 1024, NT = 64 * NW;
   static_assert(NS >= 1 && NS <= 4, "the vmcnt waits cover up to 4 stages");
@@ -635,29 +617,6 @@ __global__ __launch_bounds__(64 * NW) void wstream_matvec(WsArgs A, int bpr, int
       }
     }
   }
-  if constexpr (ARG) {
-    // the wave's, then the workgroup's first index of its largest logit, to
-    // the workgroup's partial (combined by argmax_part_kernel after the launch)
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    if (lane < nr && s > -INFINITY) {
-      bv = s;
-      bi = row0 + lane;
-    }
-    am_wave(bv, bi);
-    float* amv = (float*)(xraw + G.xraw);  // wave 0's first stage: every tile has been read
-    int* ami = (int*)(amv + NW);
-    ws_lds_barrier();
-    if (lane == 0) {
-      amv[wave] = bv;
-      ami[wave] = bi;
-    }
-    ws_lds_barrier();
-    if (tid == 0) {
-      for (int w = 1; w < NW; w++) am_take(bv, bi, amv[w], ami[w]);
-      ((uint2*)A.am_part)[blockIdx.x] = make_uint2(__float_as_uint(bv), (uint32_t)bi);
-    }
-  }
 }
 
 // ---- launch ----------------------------------------------------------------------------------
@@ -889,37 +848,6 @@ int launch_wstream_group(int dtype, const void* const* w, float* const* y, const
   if (dtype == kQ8_0) return launch_ws_group<kQ8_0>(w, y, rows, n, x, bpr, stream);
   if (dtype == kQ4K) return launch_ws_group<kQ4K>(w, y, rows, n, x, bpr, stream);
   if (dtype == kQ6K) return launch_ws_group<kQ6K>(w, y, rows, n, x, bpr, stream);
-  return NRQ_LAUNCH_BAD_ARG;
-}
-
-// launch_ws with each workgroup's greedy pick after its rows (one matrix).
-template <int FMT>
-static int launch_ws_argmax(const MatvecLaunch& L, uint32_t* part, int* nparts) {
-  int rpw = ws_rows_per_wave<FMT>(L.bpr, L.tile_rows);
-  if (L.tile_rows == 0 && rpw % 2 == 0) {
-    constexpr int TBK = 64 * WS<FMT>::BPL;
-    const long waves = ((long)L.rows + rpw - 1) / rpw;
-    if (waves < 4L * ws_num_cus() && 2L * (rpw / 2) * L.bpr >= TBK) rpw /= 2;
-  }
-  WsArgs A{};
-  A.w[0] = (const uint8_t*)L.w;
-  A.y[0] = L.y;
-  A.rows[0] = L.rows;
-  A.nmat = 1;
-  A.x = (const uint8_t*)L.x;
-  A.am_part = part;
-  // four waves per workgroup (where the LDS holds them; else NRQ_LAUNCH_TOO_WIDE
-  // and the caller picks from the logits): nparts workgroups, one partial each
-  *nparts = (int)((((long)L.rows + rpw - 1) / rpw + 3) / 4);
-  return ws_u_rowmajor(L.bpr) ? launch_ws_t<FMT, 4, 2, kWsRowMajorU | kWsArgmax>(A, L.bpr, rpw, L.stream)
-                              : launch_ws_t<FMT, 4, 2, kWsArgmax>(A, L.bpr, rpw, L.stream);
-}
-
-int launch_matvec_argmax(int dtype, const MatvecLaunch& L, uint32_t* part, int* nparts) {
-  if (L.rows <= 0 || L.bpr <= 0 || !part || !nparts) return NRQ_LAUNCH_BAD_ARG;
-  if (dtype == kQ8_0) return launch_ws_argmax<kQ8_0>(L, part, nparts);
-  if (dtype == kQ4K) return launch_ws_argmax<kQ4K>(L, part, nparts);
-  if (dtype == kQ6K) return launch_ws_argmax<kQ6K>(L, part, nparts);
   return NRQ_LAUNCH_BAD_ARG;
 }
 
