@@ -792,7 +792,7 @@ template <int HD, int GH, int NT = kAttNT, int PROD = kGrpProd>
 __global__ __launch_bounds__(NT, NT <= 512 ? 4 : 1) void attention_group_kernel(
     const float* __restrict__ q_in, const int* __restrict__ ctl, int n_heads, int n_kv_heads, int ctx, int layer,
     float scale, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, float* __restrict__ out,
-    uint8_t* __restrict__ out_q8) {
+    uint8_t* __restrict__ out_q8, uint8_t* __restrict__ out_q8k) {
   using A = AttGroup<HD, GH, NT, PROD>;
   constexpr int hd = HD, g8 = HD / 8, C = A::C, CP = A::CP, cw = A::cw, nprod = A::nprod, npc = A::npc;
   static_assert(C >= 4, "product chunk too small");
@@ -968,6 +968,26 @@ __global__ __launch_bounds__(NT, NT <= 512 ? 4 : 1) void attention_group_kernel(
   if (tid < GH * hd) {
     out[tid] = o;
     if (out_q8) quant_q8_0_lane(o, tid & 31, out_q8 + (size_t)(tid >> 5) * kQ8_0Bytes);
+  }
+  if constexpr (GH * HD == 256) {
+    // the output's Q8_K block (kquant.rs:157-187) for a K-quant o projection:
+    // the workgroup's heads are one block; the product stages are free
+    if (out_q8k) {
+      float* ob = prod;
+      if (tid < 256) ob[tid] = o;
+      __syncthreads();
+      if (tid < 64) {  // both half-waves form the block; the first stores it
+        const int r = tid & 31;
+        const float4 v0 = ((const float4*)ob)[2 * r], v1 = ((const float4*)ob)[2 * r + 1];
+        const float v8[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        uint32_t lo, hi, d_bits;
+        int ps;
+        q8k_half_lanes(v8, r, &lo, &hi, &ps, &d_bits);
+        if (tid < 32)
+          q8k_half_store(out_q8k + ((size_t)tok * n_heads * hd + (size_t)h0 * hd) / 256 * kQ8KBytes, r, lo, hi, ps,
+                         d_bits);
+      }
+    }
   }
 }
 
@@ -1735,7 +1755,7 @@ int enqueue_step(nrq_model* m) {
 constexpr int kMaxBatch = 64;  // MAX_BATCH (infer.rs:101)
 
 using AttGroupFn = void (*)(const float*, const int*, int, int, int, int, float, const uint16_t*, const uint16_t*,
-                            float*, uint8_t*);
+                            float*, uint8_t*, uint8_t*);
 
 template <int HD, int NT = nrq::kAttNT, int PROD = nrq::kGrpProd>
 AttGroupFn att_group_for(int gh, size_t* lds, int ctx) {
@@ -1940,9 +1960,13 @@ int enqueue_prefill(nrq_model* m, int B) {
     {
       const bool q8 = Ly.m[3].dt == NRQ_Q8_0;
       const AttGroupCfg gk = att_group(c);
+      // a K-quant o projection's Q8_K input, written by the attention when a
+      // workgroup's heads are one 256-value block
+      const bool q8k = !q8 && gk.fn && gk.gh * c.head_dim == 256;
       if (gk.fn) {
         hipLaunchKernelGGL(gk.fn, dim3(c.n_heads / gk.gh, B), dim3(gk.nt), gk.lds, m->stream, m->bq, m->ctl, c.n_heads,
-                           c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->battn, q8 ? m->bxq : nullptr);
+                           c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->battn, q8 ? m->bxq : nullptr,
+                           q8k ? m->bxq2 : nullptr);
       } else {
         auto* kern = c.head_dim == 32   ? nrq::attention_kernel<32, true>
                      : c.head_dim == 64 ? nrq::attention_kernel<64, true>
@@ -1957,7 +1981,7 @@ int enqueue_prefill(nrq_model* m, int B) {
       const Mat* ws[1] = {&Ly.m[3]};
       float* ys[1] = {m->bxb};
       const int rows[1] = {d};
-      if ((rc = matmul_group_rows(m, ws, ys, rows, 1, m->battn, att, B, q8))) return rc;
+      if ((rc = matmul_group_rows(m, ws, ys, rows, 1, m->battn, att, B, q8, q8k))) return rc;
     }
     {
       const Mat* ws[2] = {&Ly.m[4], &Ly.m[5]};
