@@ -461,7 +461,8 @@ __global__ __launch_bounds__(NT) void attention_kernel(
     float scale, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, float* __restrict__ out,
     uint8_t* __restrict__ out_q8, const float* __restrict__ qn, const float* __restrict__ kn, float eps, int neox) {
   constexpr int hd = HD, half = HD / 2, g8 = HD / 8;
-  static_assert(DS == 1 || (!PF && HD % (8 * DS) == 0 && HD / DS == 32), "dimension groups of 32");
+  static_assert(DS == 1 || (!PF && HD % (8 * DS) == 0 && (HD / DS == 32 || HD / DS == 16)),
+                "dimension groups of 32, or 16 without the Q8_0 output");
   constexpr int DW = HD / DS;   // dimensions of this workgroup's value chains
   constexpr int g8w = DW / 8;   // their 16-byte pieces per position
   constexpr int C = DS > 1 ? 256 : (8192 / HD) & ~63 ? (8192 / HD) & ~63 : 64;  // positions per product chunk
@@ -755,7 +756,9 @@ __global__ __launch_bounds__(NT) void attention_kernel(
   if (producer) __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
   if (tid < DW) {
     out[(size_t)h * hd + dim0 + tid] = o;
-    if (out_q8) quant_q8_0_lane(o, tid & 31, out_q8 + (size_t)((h * hd + dim0 + tid) >> 5) * kQ8_0Bytes);
+    if constexpr (DW >= 32) {  // a Q8_0 block is 32 dimensions of one workgroup
+      if (out_q8) quant_q8_0_lane(o, tid & 31, out_q8 + (size_t)((h * hd + dim0 + tid) >> 5) * kQ8_0Bytes);
+    }
   }
 }
 
@@ -1674,13 +1677,16 @@ int enqueue_step(nrq_model* m) {
     }
     {
       const bool q8 = Ly.m[3].dt == NRQ_Q8_0;
-      const int ds = att_dim_split(c);
+      // a K-quant o projection quantizes the output itself: 128-wide heads
+      // then split eight ways (16 value dimensions per workgroup)
+      const int ds = att_dim_split(c) * (c.head_dim == 128 && !q8 && att_dim_split(c) == 4 ? 2 : 1);
       auto* kern = c.head_dim == 32   ? nrq::attention_kernel<32>
                    : c.head_dim == 64 ? (ds == 2 ? nrq::attention_kernel<64, false, nrq::kAttNT, 2>
                                                  : nrq::attention_kernel<64>)
                    : c.head_dim == 96 ? nrq::attention_kernel<96>
-                                      : (ds == 4 ? nrq::attention_kernel<128, false, 768, 4>
-                                                 : nrq::attention_kernel<128>);
+                                      : (ds == 8   ? nrq::attention_kernel<128, false, 768, 8>
+                                         : ds == 4 ? nrq::attention_kernel<128, false, 768, 4>
+                                                   : nrq::attention_kernel<128>);
       hipLaunchKernelGGL(kern, dim3(c.n_heads * ds), dim3(nrq::att_threads(c.head_dim)), m->att_lds, m->stream, m->q, m->k, m->v,
                          m->rope_cs, m->ctl, c.n_heads, c.n_kv_heads, c.ctx, l, scale, m->kc, m->vc, m->attn,
                          q8 ? m->xq : nullptr, Ly.q_norm, Ly.k_norm, c.norm_eps, m->rope_neox);
