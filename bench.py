@@ -425,7 +425,7 @@ def measure_decode(fill=1024, n=128):
     crc = {"workload": "CRC-32 (IEEE) of the Llama-3.2-1B-shape Q8_0 data section in HBM",
            **measure_crc(data, f.meta["data_crc"])}
     del data
-    # the prompt: `fill` random tokens through the batched prefill (64-token
+    # the prompt: `fill` random tokens through the batched prefill (512-token
     # chunks), once untimed for warm-up, then timed from position 0
     prompt = np.random.default_rng(5).integers(0, cfg["vocab"], fill).astype(np.uint32)
     m.prefill(prompt[:64], logits=False)
@@ -579,7 +579,7 @@ def measure_qwen3(fill=512, n=64):
 
 def measure_qwen3_prefill(tokens):
     """The Qwen3 leg's model (Q4_K_M formats through a Qwen3 .nrm file), then
-    nrq_model_prefill of a random `tokens`-token prompt in 64-token chunks
+    nrq_model_prefill of a random `tokens`-token prompt in 512-token chunks
     (eager launches, no graph): the prefill alone, for kernel traces."""
     import torch
 
@@ -602,7 +602,7 @@ def measure_qwen3_prefill(tokens):
     dt = time.perf_counter() - t0
     m.close()
     return {"workload": f"Qwen3-4B architecture, Q4_K_M formats, random init: prefill of {tokens} tokens in "
-                        "64-token chunks, eager launches", "tokens": tokens, "seconds": round(dt, 4),
+                        "512-token chunks, eager launches", "tokens": tokens, "seconds": round(dt, 4),
             "tok_s": round(tokens / dt, 1)}
 
 

@@ -227,7 +227,8 @@ int nrq_model_pos(const nrq_model *m);
  * copies the logits to host `logits` (vocab floats) unless NULL. */
 int nrq_model_forward(nrq_model *m, uint32_t token, float *logits);
 /* InferCtx::prefill (infer.rs:753-759): the n prompt tokens in chunks of up to
- * MAX_BATCH = 64, each chunk as prefill_chunk (infer.rs:601-750) does it:
+ * 512 tokens (the reference's MAX_BATCH is 64: the KV cache and logits are the same
+ * at any chunk size), each chunk as prefill_chunk (infer.rs:601-750) does it:
  * batched norms and matmuls (int8 MFMA), every row's rope and f16 KV append,
  * then causal attention for all (head, token) pairs in one launch. The KV
  * cache and the last token's logits (copied to host `logits`, vocab floats,

@@ -1758,7 +1758,7 @@ int enqueue_step(nrq_model* m) {
   return NRQ_OK;
 }
 
-constexpr int kMaxBatch = 64;  // MAX_BATCH (infer.rs:101)
+constexpr int kMaxBatch = 512;  // tokens per prefill chunk (the reference's MAX_BATCH is 64, infer.rs:101)
 
 using AttGroupFn = void (*)(const float*, const int*, int, int, int, int, float, const uint16_t*, const uint16_t*,
                             float*, uint8_t*, uint8_t*);

@@ -5,7 +5,7 @@ tensors that live in HBM.
     m = Model(cfg, ctx=1152)
     m.set_weights(weights)            # numpy block arrays -> HBM, bound once
     logits = m.forward(token)          # InferCtx::forward
-    logits = m.prefill(prompt)         # InferCtx::prefill, 64-token batched chunks
+    logits = m.prefill(prompt)         # InferCtx::prefill, batched chunks of up to 512 tokens
     toks = m.generate(token, n)        # greedy (sample.rs:33-35), one HIP graph per step
 
 torch provides the device memory; every computation is a libnrq kernel.
@@ -116,7 +116,8 @@ class Model:
         return out
 
     def prefill(self, tokens, logits: bool = True):
-        """InferCtx::prefill (infer.rs:753-759): the prompt in 64-token chunks, each one
+        """InferCtx::prefill (infer.rs:753-759): the prompt in chunks of up to 512 tokens
+        (the reference takes 64; the results are the same at any chunk size), each one
         batched pass; returns the last token's logits."""
         t = np.ascontiguousarray(tokens, np.uint32)
         out = np.empty(self.cfg["vocab"], np.float32) if logits else None
