@@ -725,13 +725,14 @@ int md_launch(const MatmulGroupLaunch& L, int ks, int nb) {
   return nb >= 2 ? md_launch_ks<FMT, 2>(L, ks) : md_launch_ks<FMT, 1>(L, ks);
 }
 
-// Block splits per tile: none when the tiles alone give two waves per CU
-// (a whole row of blocks per wave, double-buffered, beat two splits by 3-6%
-// on 9728 x 2560); else the fewest that give about one wave per SIMD (4 per
-// CU), and at most 4 for rows of fewer than 16 blocks (more splits leave each
-// wave one or two blocks; the o projection's 16-block rows take 8 with the
-// early activation loads, 12.4 -> 12.0 us). Measured on the Qwen3-4B layer
-// shapes at M = 64.
+// Block splits per tile: none when the tiles alone give four waves per CU
+// (sixteen for rows of 32+ blocks; a whole row of blocks per wave,
+// double-buffered, beat two splits by 3-6% on 9728 x 2560 at M = 64); else the
+// fewest that give about two waves per SIMD (four for rows of 32+ blocks), and
+// at most 4 for rows of fewer than 16 blocks (more splits leave each wave one
+// or two blocks; the o projection's 16-block rows take 8 with the early
+// activation loads, 12.4 -> 12.0 us). Measured on the Qwen3-4B layer shapes
+// at M = 64 and M = 512.
 int md_choose(int dtype, long row_tiles, int batch, int bpr) {
   const char* env = getenv("NRQ_MMT_SPLITS");  // tuning override: 1, 2, 4 or 8
   if (env && env[0]) {
@@ -740,9 +741,13 @@ int md_choose(int dtype, long row_tiles, int batch, int bpr) {
   }
   const long tiles = row_tiles * ((batch + 31) / 32);
   const int cap = bpr < 16 ? 4 : 8;
-  // Q8_0 blocks are an eighth of a K-quant block's work: aim for twice the waves
-  const long want = dtype == kQ8_0 ? 8L * 256 : 4L * 256;
-  if (dtype != kQ8_0 && tiles >= 2L * 256) return 1;
+  // Q8_0 blocks are an eighth of a K-quant block's work: aim for twice the
+  // waves. K-quants: splits until about 8 (rows of 32+ blocks: 16) tiles per
+  // CU; at M = 512 the Qwen3-4B down (80 row tiles, 38 blocks) takes 117 us in
+  // 4 splits against 158 in none, v (32 row tiles) 12 against 17; gate|up
+  // (608 row tiles) and q|k keep whole rows.
+  const long want = dtype == kQ8_0 ? 8L * 256 : (bpr >= 32 ? 16L : 8L) * 256;
+  if (dtype != kQ8_0 && tiles >= (bpr >= 32 ? 16L : 4L) * 256) return 1;
   int ks = 1;
   while (ks < cap && ks < bpr && tiles * ks < want) ks *= 2;
   return ks;
