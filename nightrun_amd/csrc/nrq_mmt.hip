@@ -753,7 +753,7 @@ int md_choose(int dtype, long row_tiles, int batch, int bpr) {
   return ks;
 }
 
-int md_buffers(int dtype, int ks);
+int md_buffers(int dtype, int ks, int batch, int bpr);
 
 // the early activation loads of md_launch_t, by format and row length
 int md_early_x(int fmt, int bpr) {
@@ -786,7 +786,7 @@ int md_group(int dtype, const MatmulGroupLaunch& G) {
   long row_tiles = 0;
   for (int i = 0; i < G.nmat; i++) row_tiles += (G.rows[i] + 31) / 32;
   const int ks = md_choose(dtype, row_tiles, G.batch, G.bpr);
-  const int nb = md_buffers(dtype, ks);
+  const int nb = md_buffers(dtype, ks, G.batch, G.bpr);
   if (dtype == kQ8_0) return md_launch<kQ8_0>(G, ks, nb);
   return dtype == kQ4K ? md_launch<kQ4K>(G, ks, nb) : md_launch<kQ6K>(G, ks, nb);
 }
@@ -796,13 +796,16 @@ int md_group(int dtype, const MatmulGroupLaunch& G) {
 // (eight splits of the Qwen3-4B down projection: 30.4 us on one buffer, 34.1
 // on two, which spill). Q8_0: one (on the Llama-3.2-1B shapes at M = 64 one
 // buffer beat two and a ring of four by 4-20%).
-int md_buffers(int dtype, int ks) {
+int md_buffers(int dtype, int ks, int batch, int bpr) {
   const char* nb = getenv("NRQ_MMT_NB");  // tuning override: 1, 2 or 4 (4: Q8_0 only)
   if (nb && nb[0]) return atoi(nb);
   const char* env = getenv("NRQ_MMT_DB");  // tuning override: 0 (one buffer) or 1 (two)
   if (env && env[0]) return env[0] == '1' ? 2 : 1;
   if (dtype == kQ8_0) return 1;
-  return ks == 1 ? 2 : 1;
+  // whole rows: two buffers, except for rows of fewer than 16 blocks at more
+  // than 64 tokens (Qwen3-4B gate and up at M = 512: 58 against 63 us; o's 16
+  // blocks: 40 against 37)
+  return ks == 1 && (batch <= 64 || bpr >= 16) ? 2 : 1;
 }
 
 }  // namespace
@@ -860,7 +863,7 @@ int launch_mmt_group2(int dt0, const MatmulGroupLaunch& G0, int dt1, const Matmu
   for (const MatmulGroupLaunch* G : {&G0, &G1})
     for (int i = 0; i < G->nmat; i++) row_tiles += (G->rows[i] + 31) / 32;
   const int ks = md_choose(dt0, row_tiles, G0.batch, G0.bpr);
-  if (ks < 2 || md_buffers(dt0, ks) != 1 || md_buffers(dt1, ks) != 1) return NRQ_LAUNCH_BAD_ARG;
+  if (ks < 2 || md_buffers(dt0, ks, G0.batch, G0.bpr) != 1 || md_buffers(dt1, ks, G1.batch, G1.bpr) != 1) return NRQ_LAUNCH_BAD_ARG;
   return dt0 == kQ4K ? md2_launch_ks<kQ4K, kQ6K>(G0, G1, ks) : md2_launch_ks<kQ6K, kQ4K>(G0, G1, ks);
 }
 
