@@ -193,6 +193,25 @@ __device__ __forceinline__ void md_q8_window(const uint8_t* __restrict__ blk, in
   off = p | (pd << 2);
 }
 
+// A Q8_0 block's window, as md_q8_window, from a copy of its row in LDS whose
+// start keeps the row's alignment mod 16 (reads of 4-byte alignment only).
+__device__ __forceinline__ void md_q8_window_lds(const uint8_t* blk, int kg, u32x4& v, uint32_t& v4, uint32_t& d,
+                                                 uint32_t& off) {
+  const uint8_t* q = blk + 2 + 16 * kg;
+  const uint32_t p = (uint32_t)((uintptr_t)q & 3u);
+  const uint8_t* a = q - p;
+  v = (u32x4)(*(const u32x4a*)a);
+  v4 = *(const uint16_t*)(a + (p ? 16 : 14));
+  const uint32_t pd = (uint32_t)((uintptr_t)blk & 3u);
+  d = *(const uint32_t*)(blk - pd);
+  off = p | (pd << 2);
+}
+
+// Q8_0 spans: 8 blocks of a row, 272 bytes, 17 aligned 16-byte windows when
+// rows are 8-block multiples on 16-byte aligned bases. A tile's span is 32 x 17
+// windows per operand, window i of the tile being row i / 17, piece i % 17.
+constexpr int kMdSpanB = 8 * 34, kMdSpanWin = 17, kMdSpanLd = (32 * kMdSpanWin + 63) / 64;  // 9 loads per lane
+
 template <>
 __device__ __forceinline__ void md_load<kQ8_0>(MdLoad<kQ8_0>& L, const uint8_t* __restrict__ xb,
                                                const uint8_t* __restrict__ wb, int kg, const uint32_t* xo) {
@@ -503,7 +522,56 @@ __device__ __forceinline__ void mmd_body(const int wg, const MdMats& M, const ui
       for (int e = 0; e < 16; e += 4) *(float4*)(dst + e) = make_float4(c[e], c[e + 1], c[e + 2], c[e + 3]);
     }
   };
-  if constexpr (NB == 4) {
+  if constexpr (NB == 8) {
+    // Spans through LDS (Q8_0, whole rows per wave): the wave reads a span of
+    // its 32 weight rows and 32 tokens as consecutive 16-byte windows (about 4
+    // rows per load instruction, where one operand per lane touches 32 rows'
+    // lines), writes them to its stages, and takes each block's operands from
+    // there; the next span's windows load during the current span's blocks.
+    static_assert(FMT == kQ8_0 && KS == 1, "spans: Q8_0, whole rows");
+    uint8_t* sw = (uint8_t*)(lds + kMdScalDw);  // 32 rows x 272 bytes
+    uint8_t* sx = sw + 32 * kMdSpanB;           // 32 tokens x 272 bytes
+    size_t wro[kMdSpanLd], xro[kMdSpanLd];  // window offsets at span 0
+#pragma unroll
+    for (int j = 0; j < kMdSpanLd; j++) {
+      const int i = min(64 * j + lane, 32 * kMdSpanWin - 1);
+      const int rr = i / kMdSpanWin, pc = i - rr * kMdSpanWin;
+      wro[j] = (size_t)min(r0 + rr, rows - 1) * bpr * BS + 16 * pc;
+      xro[j] = (size_t)min(t0 + rr, batch - 1) * bpr * XS + 16 * pc;
+    }
+    const int nspan = bpr / 8;
+    u32x4 gw[kMdSpanLd], gx[kMdSpanLd];
+#pragma unroll
+    for (int j = 0; j < kMdSpanLd; j++) {
+      gw[j] = *(const u32x4*)(W + wro[j]);
+      gx[j] = *(const u32x4*)(X + xro[j]);
+    }
+    for (int sp = 0; sp < nspan; sp++) {
+#pragma unroll
+      for (int j = 0; j < kMdSpanLd; j++) {
+        const int i = 64 * j + lane;
+        if (j < kMdSpanLd - 1 || i < 32 * kMdSpanWin) {
+          *(u32x4*)(sw + 16 * i) = gw[j];
+          *(u32x4*)(sx + 16 * i) = gx[j];
+        }
+      }
+      const size_t nxt = (size_t)min(sp + 1, nspan - 1) * kMdSpanB;  // the last span reloads itself
+#pragma unroll
+      for (int j = 0; j < kMdSpanLd; j++) {
+        gw[j] = *(const u32x4*)(W + wro[j] + nxt);
+        gx[j] = *(const u32x4*)(X + xro[j] + nxt);
+      }
+#pragma unroll 2
+      for (int jb = 0; jb < 8; jb++) {
+        MdLoad<kQ8_0> L;
+        md_q8_window_lds(sx + ta * kMdSpanB + 34 * jb, kg, L.a, L.a4, L.ad, L.ao);
+        md_q8_window_lds(sw + ta * kMdSpanB + 34 * jb, kg, L.w, L.w4, L.wd, L.wo);
+        float c[16];
+        md_q8(L, scal, ta, kg, c, [&]() {});
+        finish(8 * sp + jb, c);
+      }
+    }
+  } else if constexpr (NB == 4) {
     // four register buffers in a ring: round k's block is loaded at round k - 3
     MdLoad<FMT> L0, L1, L2, L3;
     {
@@ -695,7 +763,7 @@ int md_launch_t(const MatmulGroupLaunch& G) {
   const long nwg = rt_pad * ntt;
   if (nwg > 0x7fffffffL) return NRQ_LAUNCH_BAD_ARG;
   const size_t lds = (size_t)KS * kMdScalDw * 4 + (KS > 1 ? (size_t)2 * KS * 1024 * 4 : 0) +
-                     (FMT == kQ8_0 ? 0 : (size_t)KS * kMdStage);
+                     (FMT == kQ8_0 ? (NB == 8 ? (size_t)2 * 32 * kMdSpanB : 0) : (size_t)KS * kMdStage);
   // one buffer: the next block's activation windows load as soon as the
   // current block's are staged (Q6_K, and Q4_K rows of 16+ blocks: down 30.5 ->
   // 27.7 us, o 13.4 -> 12.4 us on the Qwen3-4B layer at M = 64; q|k|v, 10
@@ -720,6 +788,7 @@ int md_launch_ks(const MatmulGroupLaunch& L, int ks) {
 template <int FMT>
 int md_launch(const MatmulGroupLaunch& L, int ks, int nb) {
   if constexpr (FMT == kQ8_0) {
+    if (nb == 8 && ks == 1) return md_launch_t<FMT, 1, 8>(L);
     if (nb >= 4) return md_launch_ks<FMT, 4>(L, ks);
   }
   return nb >= 2 ? md_launch_ks<FMT, 2>(L, ks) : md_launch_ks<FMT, 1>(L, ks);
@@ -786,7 +855,12 @@ int md_group(int dtype, const MatmulGroupLaunch& G) {
   long row_tiles = 0;
   for (int i = 0; i < G.nmat; i++) row_tiles += (G.rows[i] + 31) / 32;
   const int ks = md_choose(dtype, row_tiles, G.batch, G.bpr);
-  const int nb = md_buffers(dtype, ks, G.batch, G.bpr);
+  int nb = md_buffers(dtype, ks, G.batch, G.bpr);
+  if (nb == 8) {  // spans need 8-block rows on 16-byte aligned bases
+    uintptr_t a = (uintptr_t)G.xs;
+    for (int i = 0; i < G.nmat; i++) a |= (uintptr_t)G.w[i];
+    if (ks != 1 || G.bpr % 8 != 0 || (a & 15u) != 0) nb = 1;
+  }
   if (dtype == kQ8_0) return md_launch<kQ8_0>(G, ks, nb);
   return dtype == kQ4K ? md_launch<kQ4K>(G, ks, nb) : md_launch<kQ6K>(G, ks, nb);
 }
@@ -797,11 +871,13 @@ int md_group(int dtype, const MatmulGroupLaunch& G) {
 // on two, which spill). Q8_0: one (on the Llama-3.2-1B shapes at M = 64 one
 // buffer beat two and a ring of four by 4-20%).
 int md_buffers(int dtype, int ks, int batch, int bpr) {
-  const char* nb = getenv("NRQ_MMT_NB");  // tuning override: 1, 2 or 4 (4: Q8_0 only)
+  const char* nb = getenv("NRQ_MMT_NB");  // tuning override: 1, 2, 4 or 8 (4, 8: Q8_0 only)
   if (nb && nb[0]) return atoi(nb);
   const char* env = getenv("NRQ_MMT_DB");  // tuning override: 0 (one buffer) or 1 (two)
   if (env && env[0]) return env[0] == '1' ? 2 : 1;
-  if (dtype == kQ8_0) return 1;
+  // Q8_0 whole rows past 64 tokens: 8-block spans through LDS (Llama-3.2-1B
+  // gate|up, 16384 x 2048 at M = 512: see the staging branch of mmd_body)
+  if (dtype == kQ8_0) return ks == 1 && batch > 64 && bpr % 8 == 0 ? 8 : 1;
   // whole rows: two buffers, except for rows of fewer than 16 blocks at more
   // than 64 tokens (Qwen3-4B gate and up at M = 512: 58 against 63 us; o's 16
   // blocks: 40 against 37)

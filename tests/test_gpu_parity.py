@@ -604,14 +604,34 @@ def test_matmul_every_split_count(gpu, oracle, dtype, monkeypatch):
         w = oracle.gen_weights(dtype, 800 + bpr, rows, cols)
         xs = oracle.quantize_act(dtype, oracle.Rng(801 + bpr).normal(batch * cols))
         cases.append((rows, cols, batch, w, xs, oracle.matmul(dtype, 0, w, xs, rows, cols, batch, threads=THREADS)))
-    # register buffers of block loads: 1 or 2, and a ring of 4 for Q8_0
-    for nb in ("1", "2", "4") if dtype == 1 else ("1", "2"):
+    # register buffers of block loads: 1 or 2, a ring of 4 for Q8_0, and Q8_0's
+    # 8-block spans through LDS (whole rows of 8-block multiples only, else 1)
+    for nb in ("1", "2", "4", "8") if dtype == 1 else ("1", "2"):
         monkeypatch.setenv("NRQ_MMT_NB", nb)
         for ks in ("1", "2", "4", "8"):
             monkeypatch.setenv("NRQ_MMT_SPLITS", ks)
             for rows, cols, batch, w, xs, want in cases:
                 assert_bitwise(gpu_matmul(dtype, 0, w, xs, rows, cols, batch), want,
                                f"splits {ks} buffers {nb} rows {rows} cols {cols} batch {batch}")
+
+
+def test_matmul_q8_0_spans(gpu, oracle, monkeypatch):
+    """Q8_0 tiles of whole rows past 64 tokens read 8-block spans of their rows
+    and tokens into LDS: ragged row and token tiles, one span and several, and
+    the span path forced below 64 tokens, all with the oracle's bits."""
+    cases = []
+    for rows, bpr, batch in ((1024, 8, 65), (1100, 16, 130), (1030, 64, 200), (1056, 24, 5), (1024, 8, 33)):
+        cols = bpr * 32
+        w = oracle.gen_weights(1, 810 + bpr, rows, cols)
+        xs = oracle.quantize_act(1, oracle.Rng(811 + batch).normal(batch * cols))
+        cases.append((rows, cols, batch, w, xs, oracle.matmul(1, 0, w, xs, rows, cols, batch, threads=THREADS)))
+    for forced in (False, True):
+        if forced:
+            monkeypatch.setenv("NRQ_MMT_NB", "8")
+            monkeypatch.setenv("NRQ_MMT_SPLITS", "1")
+        for rows, cols, batch, w, xs, want in cases:
+            assert_bitwise(gpu_matmul(1, 0, w, xs, rows, cols, batch), want,
+                           f"spans forced {forced} rows {rows} cols {cols} batch {batch}")
 
 
 @pytest.mark.parametrize("dtype", [1, 2, 3])
