@@ -809,6 +809,11 @@ int md_choose(int dtype, long row_tiles, int batch, int bpr) {
     if (ks == 1 || ks == 2 || ks == 4 || ks == 8) return ks;
   }
   const long tiles = row_tiles * ((batch + 31) / 32);
+  // Q8_0 past 64 tokens, rows of 8-block multiples: whole rows in 8-block
+  // spans from 1024 tiles (Llama-3.2-1B at M = 512: q|k|v 72 -> 39 us, o 48
+  // -> 34, down 174 -> 117, gate 181 -> 82; at M = 128 gate's 1024 tiles 49 ->
+  // 34, while q|k|v's 384 tiles keep 2 splits, 25 against 27)
+  if (dtype == kQ8_0 && batch > 64 && bpr % 8 == 0 && tiles >= 1024) return 1;
   const int cap = bpr < 16 ? 4 : 8;
   // Q8_0 blocks are an eighth of a K-quant block's work: aim for twice the
   // waves. K-quants: splits until about 8 (rows of 32+ blocks: 16) tiles per
