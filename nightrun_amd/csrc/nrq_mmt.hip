@@ -555,6 +555,9 @@ __device__ __forceinline__ void mmd_body(const int wg, const MdMats& M, const ui
           *(u32x4*)(sx + 16 * i) = gx[j];
         }
       }
+      // lanes read other lanes' windows: the wave's LDS accesses run in program
+      // order, and these compiler barriers keep that order in the code
+      asm volatile("" ::: "memory");
       const size_t nxt = (size_t)min(sp + 1, nspan - 1) * kMdSpanB;  // the last span reloads itself
 #pragma unroll
       for (int j = 0; j < kMdSpanLd; j++) {
@@ -570,6 +573,7 @@ __device__ __forceinline__ void mmd_body(const int wg, const MdMats& M, const ui
         md_q8(L, scal, ta, kg, c, [&]() {});
         finish(8 * sp + jb, c);
       }
+      asm volatile("" ::: "memory");  // the span's reads come before the next span's writes
     }
   } else if constexpr (NB == 4) {
     // four register buffers in a ring: round k's block is loaded at round k - 3
