@@ -146,12 +146,17 @@ __device__ __forceinline__ void md_load_windows(u32x4a (&x)[kMdXi], const uint8_
 
 // The lane's windows into the wave's stage (the last load's upper half-wave
 // holds repeats and is not written).
+// Lanes then read windows other lanes wrote: the wave's LDS accesses run in
+// program order, and the compiler barriers keep that order in the code (the
+// previous block's reads before these writes, these writes before the reads).
 __device__ __forceinline__ void md_stage(const u32x4a (&x)[kMdXi], uint8_t* stg, int lane) {
+  asm volatile("" ::: "memory");
 #pragma unroll
   for (int i = 0; i < kMdXi; i++) {
     const int idx = 64 * i + lane;
     if (i < kMdXi - 1 || idx < 32 * kMdWin) *(u32x4*)(stg + 16 * idx) = (u32x4)x[i];
   }
+  asm volatile("" ::: "memory");
 }
 
 // Byte offsets of the lane's windows from the tile's block column: token
